@@ -1,0 +1,192 @@
+/*
+ * llm_accel.h -- C ABI of the MI355X resident decoder-layer path.
+ *
+ * Drop-in for LLM-ACCEL's coarse-task boundary: the host hands the device
+ * an operator id, layer, active row count (1..8) and first position; the
+ * device runs the whole sublayer with hidden state, KV cache and all
+ * intermediates resident in HBM, and returns the controller's 64-byte
+ * status record.  Plain pointers and sizes only.
+ *
+ * Reference interfaces replaced (paths under the reference repository):
+ *   - device kernel control_cache_8x64_dual_core_nk + status sink
+ *     (include/vitis_stream_8x64.hpp:219-258, kernel/control_cache_8x64.cpp
+ *     :5767-6481) -> llm_task();
+ *   - accelerator_t construction, persistent aux tables and one-time weight
+ *     migration (host/host_qwen_8x64.cpp:1026-1086, :2144-2190, :2458-2478)
+ *     -> llm_ctx_create(), llm_load_*();
+ *   - feature-pair H2D / D2H migration and port rebinding
+ *     (host/host_qwen_8x64.cpp:1283-1445, :1846-1888, :2062-2103)
+ *     -> llm_hidden_upload*(), llm_hidden_download*(), pair ids of
+ *     llm_task();
+ *   - KV cache preload / inspection (host/host_qwen_8x64.cpp:1729-1843)
+ *     -> llm_kv_write(), llm_kv_read().
+ *
+ * Threading: one host thread per context; every call is synchronous with
+ * respect to the caller (work runs on the context's own HIP stream).
+ * Return values: >= 0 is a reference status code (llm_task) or 0; < 0 is an
+ * error of this library (LLM_E_*), with a message in llm_last_error().
+ */
+#ifndef LLM_ACCEL_H
+#define LLM_ACCEL_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Operator ids (include/control_cache_8x64.hpp:253-276).  Only the
+ * resident-layer image's operators run here; ids 1..15 and 17 return
+ * LLM_STATUS_BAD_OPERATOR exactly as that image does
+ * (kernel/control_cache_8x64.cpp:6483-6494). */
+enum {
+    LLM_OP_NOP = 0,
+    LLM_OP_DECODER_LAYER = 16,     /* attention + FFN sublayers        */
+    LLM_OP_ATTENTION_SUBLAYER = 18, /* Task 18                         */
+    LLM_OP_FFN_SUBLAYER = 19,       /* Task 19                         */
+    LLM_OP_FINAL_NORM = 20          /* Task 20                         */
+};
+
+/* Status codes (include/control_cache_8x64.hpp:279-286). */
+enum {
+    LLM_STATUS_OK = 0,
+    LLM_STATUS_BAD_OPERATOR = 1,
+    LLM_STATUS_BAD_TOKEN_COUNT = 2,
+    LLM_STATUS_BAD_TILE_LENGTH = 3,
+    LLM_STATUS_BAD_POSITION = 4,
+    LLM_STATUS_BAD_LAYER = 5
+};
+
+/* Library errors (never produced by the reference). */
+enum {
+    LLM_E_ARG = -1,    /* bad argument / shape                   */
+    LLM_E_HIP = -2,    /* HIP runtime error                      */
+    LLM_E_NOMEM = -3,  /* device allocation failed               */
+    LLM_E_STATE = -4   /* missing weights / tables               */
+};
+
+/* Projection ids, in the reference's packed order
+ * (host/host_qwen_8x64.cpp:325-376, kernel/mm_controller.cpp:51-102). */
+enum {
+    LLM_PROJ_Q = 0,
+    LLM_PROJ_K = 1,
+    LLM_PROJ_V = 2,
+    LLM_PROJ_O = 3,
+    LLM_PROJ_GATE = 4,
+    LLM_PROJ_UP = 5,
+    LLM_PROJ_DOWN = 6
+};
+
+/* Model shape (model_shape_t, host/host_qwen_8x64.cpp:110-118).
+ * Requirements of this build: num_kv_heads >= 1, num_heads % num_kv_heads
+ * == 0, head_dim even and <= 128, heads per KV group <= 16. */
+typedef struct {
+    uint32_t vocab_size;
+    uint32_t hidden_size;
+    uint32_t intermediate_size;
+    uint32_t num_layers;
+    uint32_t num_heads;
+    uint32_t num_kv_heads;
+    uint32_t max_seq_len;
+    double rope_theta; /* 1e6 in the reference (host:47) */
+} llm_shape_t;
+
+/* The controller's 64-byte status record (kernel/cc8_status_sink.cpp:4-15,
+ * decoded at host/host_qwen_8x64.cpp:670-684).  op, code, token_count and
+ * last_task follow the reference exactly; the four schedule counters are
+ * the values the 8x64 controller would report for the same command,
+ * computed from its formulas (kernel/control_cache_8x64.cpp:5974-6481). */
+typedef struct {
+    uint32_t op;
+    uint32_t code;
+    uint32_t token_count;
+    uint32_t output_waves;
+    uint32_t mm_tasks;
+    uint32_t vector_tasks;
+    uint32_t completed_packets;
+    uint32_t last_task;
+    uint32_t reserved[8];
+} llm_status_t;
+
+typedef struct llm_ctx llm_ctx_t;
+
+/* Create a context on HIP device `device`: allocates weights, norm table,
+ * RoPE table (built here from rope_theta exactly as the reference host
+ * builds aux1), a zeroed KV cache for max_seq_len positions of every
+ * layer, `num_pairs` hidden-state pairs of 8 rows, and scratch.  The
+ * reference binds 4 feature buffers (two pairs); num_pairs >= 2. */
+int llm_ctx_create(const llm_shape_t* shape, int device, uint32_t num_pairs,
+                   llm_ctx_t** out);
+void llm_ctx_destroy(llm_ctx_t* ctx);
+const char* llm_last_error(void);
+
+/* Weights of one projection of one layer, row-major [out_dim][in_dim]
+ * Q4.12 raw int16 (the values projection_weight_raw returns,
+ * host/host_qwen_8x64.cpp:899-935). */
+int llm_load_projection(llm_ctx_t* ctx, uint32_t layer, uint32_t proj,
+                        const int16_t* weights);
+/* The reference's 16 packed weight shards (host/host_qwen_8x64.cpp:842-869,
+ * :899-935): shard i holds `shard_words` 64-byte words of 32 int16 lanes
+ * covering every layer's 16x16 tiles. */
+int llm_load_packed_shards(llm_ctx_t* ctx, const int16_t* const shards[16],
+                           uint64_t shard_words);
+/* Norm table, [(2*num_layers + 1)][hidden] Q8.8: rows 2l (attention),
+ * 2l+1 (FFN), 2L (final) (include/control_cache_8x64.hpp:111-123). */
+int llm_load_norms(llm_ctx_t* ctx, const int16_t* norms);
+
+/* Hidden-state pairs: rows are [rows][hidden] int16 Q8.8. */
+int llm_hidden_upload(llm_ctx_t* ctx, uint32_t pair, const int16_t* rows,
+                      uint32_t row_count);
+int llm_hidden_download(llm_ctx_t* ctx, uint32_t pair, int16_t* rows,
+                        uint32_t row_count);
+/* The reference's packed feature ports (host/host_qwen_8x64.cpp:2062-2103):
+ * rows 0-3 in port0, rows 4-7 in port1, row stride `stride_words` 64-byte
+ * words (ceil(max(H, I) / 32) in the reference). */
+int llm_hidden_upload_ports(llm_ctx_t* ctx, uint32_t pair,
+                            const int16_t* port0, const int16_t* port1,
+                            uint32_t row_count, uint32_t stride_words);
+int llm_hidden_download_ports(llm_ctx_t* ctx, uint32_t pair, int16_t* port0,
+                              int16_t* port1, uint32_t row_count,
+                              uint32_t stride_words);
+
+/* One coarse task: the controller invocation with scalar arguments
+ * operator_kind, layer_id, token_count, position, tile_len
+ * (kernel/control_cache_8x64.cpp:5767-5797), reading pair `in_pair` and
+ * writing pair `out_pair` (the reference's port rebinding; equal pairs are
+ * allowed).  Returns the status code (also in *status when non-NULL). */
+int llm_task(llm_ctx_t* ctx, uint32_t op, uint32_t layer,
+             uint32_t token_count, uint32_t position, uint32_t tile_len,
+             uint32_t in_pair, uint32_t out_pair, llm_status_t* status);
+
+/* KV cache rows of one layer and KV head, positions [pos0, pos0 + n):
+ * k / v are [n][head_dim] Q8.8 (K stored after RoPE, V raw). */
+int llm_kv_read(llm_ctx_t* ctx, uint32_t layer, uint32_t kv_head,
+                uint32_t pos0, uint32_t n, int16_t* k, int16_t* v);
+int llm_kv_write(llm_ctx_t* ctx, uint32_t layer, uint32_t kv_head,
+                 uint32_t pos0, uint32_t n, const int16_t* k,
+                 const int16_t* v);
+/* Zero the whole KV cache (accelerator_t constructor, host:1073-1074). */
+int llm_kv_clear(llm_ctx_t* ctx);
+
+/* Device pointer of a pair's [8][hidden] rows (for zero-copy callers). */
+void* llm_pair_device_ptr(llm_ctx_t* ctx, uint32_t pair);
+/* The context's HIP stream (hipStream_t) and a full synchronisation. */
+void* llm_stream(llm_ctx_t* ctx);
+int llm_sync(llm_ctx_t* ctx);
+
+/* HIP-event timing on the context stream: record into slot (0..63), and
+ * the elapsed milliseconds between two recorded slots (synchronises). */
+int llm_event_record(llm_ctx_t* ctx, uint32_t slot);
+int llm_event_elapsed_ms(llm_ctx_t* ctx, uint32_t slot_a, uint32_t slot_b,
+                         float* ms);
+
+/* The two exp tables the kernels use, 2049 entries for x = -8 .. 0 in
+ * Q8.8 steps: q8_8 = floor(e^x * 256) (SiLU), q2_14 = floor(e^x * 16384)
+ * (attention probabilities). */
+int llm_exp_tables(int16_t* q8_8, int16_t* q2_14);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,244 @@
+"""ctypes binding of libllm_accel.so (the C ABI in include/llm_accel.h).
+
+This is the Python mirror of the reference's accelerator_t boundary
+(host/host_qwen_8x64.cpp:1024-2013): a context holding the resident model,
+hidden pairs and KV cache, and `task()` = one controller invocation of
+Task 16/18/19/20.  Loading fails loudly when the HIP library is missing;
+there is no CPU fallback.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libllm_accel.so")
+
+OP_NOP, OP_DECODER_LAYER = 0, 16
+OP_ATTENTION, OP_FFN, OP_FINAL_NORM = 18, 19, 20
+STATUS_OK, BAD_OPERATOR, BAD_TOKEN_COUNT = 0, 1, 2
+BAD_TILE_LENGTH, BAD_POSITION, BAD_LAYER = 3, 4, 5
+PROJ_Q, PROJ_K, PROJ_V, PROJ_O, PROJ_GATE, PROJ_UP, PROJ_DOWN = range(7)
+
+_i16p = ctypes.POINTER(ctypes.c_int16)
+_u32 = ctypes.c_uint32
+
+# Every symbol include/llm_accel.h declares.
+EXPORTS = (
+    "llm_ctx_create", "llm_ctx_destroy", "llm_last_error",
+    "llm_load_projection", "llm_load_packed_shards", "llm_load_norms",
+    "llm_hidden_upload", "llm_hidden_download", "llm_hidden_upload_ports",
+    "llm_hidden_download_ports", "llm_task", "llm_kv_read", "llm_kv_write",
+    "llm_kv_clear", "llm_pair_device_ptr", "llm_stream", "llm_sync",
+    "llm_event_record", "llm_event_elapsed_ms", "llm_exp_tables",
+)
+
+
+class Shape(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint32) for n in (
+        "vocab_size", "hidden_size", "intermediate_size", "num_layers",
+        "num_heads", "num_kv_heads", "max_seq_len")] + [
+            ("rope_theta", ctypes.c_double)]
+
+    @property
+    def head_dim(self):
+        return self.hidden_size // self.num_heads
+
+    @property
+    def kv_channels(self):
+        return self.num_kv_heads * self.head_dim
+
+
+class Status(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint32) for n in (
+        "op", "code", "token_count", "output_waves", "mm_tasks",
+        "vector_tasks", "completed_packets", "last_task")] + [
+            ("reserved", ctypes.c_uint32 * 8)]
+
+    def as_tuple(self):
+        return (self.op, self.code, self.token_count, self.output_waves,
+                self.mm_tasks, self.vector_tasks, self.completed_packets,
+                self.last_task)
+
+
+class AccelError(RuntimeError):
+    pass
+
+
+def load_library(path=LIB_PATH):
+    if not os.path.exists(path):
+        raise AccelError(
+            f"{path} is missing: build it with `make -C llm-accel_amd` "
+            "(the HIP path has no CPU fallback)")
+    lib = ctypes.CDLL(path)
+    vp = ctypes.c_void_p
+    sig = {
+        "llm_ctx_create": (ctypes.c_int, [ctypes.POINTER(Shape), ctypes.c_int,
+                                          _u32, ctypes.POINTER(vp)]),
+        "llm_ctx_destroy": (None, [vp]),
+        "llm_last_error": (ctypes.c_char_p, []),
+        "llm_load_projection": (ctypes.c_int, [vp, _u32, _u32, _i16p]),
+        "llm_load_packed_shards": (ctypes.c_int, [vp, ctypes.POINTER(_i16p),
+                                                  ctypes.c_uint64]),
+        "llm_load_norms": (ctypes.c_int, [vp, _i16p]),
+        "llm_hidden_upload": (ctypes.c_int, [vp, _u32, _i16p, _u32]),
+        "llm_hidden_download": (ctypes.c_int, [vp, _u32, _i16p, _u32]),
+        "llm_hidden_upload_ports": (ctypes.c_int, [vp, _u32, _i16p, _i16p,
+                                                   _u32, _u32]),
+        "llm_hidden_download_ports": (ctypes.c_int, [vp, _u32, _i16p, _i16p,
+                                                     _u32, _u32]),
+        "llm_task": (ctypes.c_int, [vp, _u32, _u32, _u32, _u32, _u32, _u32,
+                                    _u32, ctypes.POINTER(Status)]),
+        "llm_kv_read": (ctypes.c_int, [vp, _u32, _u32, _u32, _u32, _i16p,
+                                       _i16p]),
+        "llm_kv_write": (ctypes.c_int, [vp, _u32, _u32, _u32, _u32, _i16p,
+                                        _i16p]),
+        "llm_kv_clear": (ctypes.c_int, [vp]),
+        "llm_pair_device_ptr": (vp, [vp, _u32]),
+        "llm_stream": (vp, [vp]),
+        "llm_sync": (ctypes.c_int, [vp]),
+        "llm_event_record": (ctypes.c_int, [vp, _u32]),
+        "llm_event_elapsed_ms": (ctypes.c_int, [vp, _u32, _u32,
+                                                ctypes.POINTER(ctypes.c_float)]),
+        "llm_exp_tables": (ctypes.c_int, [_i16p, _i16p]),
+    }
+    for name, (res, args) in sig.items():
+        f = getattr(lib, name)
+        f.restype = res
+        f.argtypes = args
+    return lib
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        _lib = load_library()
+    return _lib
+
+
+def _p16(a):
+    assert a.dtype == np.int16 and a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(_i16p)
+
+
+def exp_tables():
+    a = np.zeros(2049, np.int16)
+    b = np.zeros(2049, np.int16)
+    lib().llm_exp_tables(_p16(a), _p16(b))
+    return a, b
+
+
+class Accelerator:
+    """One device context (mirror of accelerator_t)."""
+
+    def __init__(self, shape, device=0, num_pairs=4):
+        self.shape = shape
+        self._ctx = ctypes.c_void_p()
+        rc = lib().llm_ctx_create(ctypes.byref(shape), device, num_pairs,
+                                  ctypes.byref(self._ctx))
+        self._check(rc, "llm_ctx_create")
+
+    def close(self):
+        if getattr(self, "_ctx", None) and self._ctx.value:
+            lib().llm_ctx_destroy(self._ctx)
+            self._ctx = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    @staticmethod
+    def _check(rc, what):
+        if rc < 0:
+            msg = lib().llm_last_error()
+            raise AccelError(f"{what} failed ({rc}): "
+                             f"{msg.decode() if msg else ''}")
+        return rc
+
+    # --- model ---------------------------------------------------------
+    def load_projection(self, layer, proj, w):
+        w = np.ascontiguousarray(w, np.int16)
+        self._check(lib().llm_load_projection(self._ctx, layer, proj, _p16(w)),
+                    "llm_load_projection")
+
+    def load_norms(self, norms):
+        norms = np.ascontiguousarray(norms, np.int16)
+        self._check(lib().llm_load_norms(self._ctx, _p16(norms)),
+                    "llm_load_norms")
+
+    def load_packed_shards(self, shards):
+        shards = [np.ascontiguousarray(s, np.int16) for s in shards]
+        arr = (_i16p * 16)(*[_p16(s) for s in shards])
+        words = shards[0].size // 32
+        self._check(lib().llm_load_packed_shards(self._ctx, arr, words),
+                    "llm_load_packed_shards")
+
+    def load_model(self, model):
+        """model: object with weight(layer, proj) and norms()."""
+        for layer in range(self.shape.num_layers):
+            for proj in range(7):
+                self.load_projection(layer, proj, model.weight(layer, proj))
+        self.load_norms(model.norms())
+
+    # --- hidden pairs ---------------------------------------------------
+    def upload(self, pair, rows):
+        rows = np.ascontiguousarray(rows, np.int16)
+        self._check(lib().llm_hidden_upload(self._ctx, pair, _p16(rows),
+                                            rows.shape[0]), "upload")
+
+    def download(self, pair, n):
+        out = np.zeros((n, self.shape.hidden_size), np.int16)
+        self._check(lib().llm_hidden_download(self._ctx, pair, _p16(out), n),
+                    "download")
+        return out
+
+    # --- tasks ------------------------------------------------------------
+    def task(self, op, layer, token_count, position, in_pair, out_pair,
+             tile_len=0):
+        st = Status()
+        rc = lib().llm_task(self._ctx, op, layer, token_count, position,
+                            tile_len, in_pair, out_pair, ctypes.byref(st))
+        self._check(rc, "llm_task")
+        return rc, st
+
+    # --- KV cache -------------------------------------------------------
+    def kv_read(self, layer, kv_head, pos0, n):
+        d = self.shape.head_dim
+        k = np.zeros((n, d), np.int16)
+        v = np.zeros((n, d), np.int16)
+        self._check(lib().llm_kv_read(self._ctx, layer, kv_head, pos0, n,
+                                      _p16(k), _p16(v)), "kv_read")
+        return k, v
+
+    def kv_write(self, layer, kv_head, pos0, k, v):
+        k = np.ascontiguousarray(k, np.int16)
+        v = np.ascontiguousarray(v, np.int16)
+        self._check(lib().llm_kv_write(self._ctx, layer, kv_head, pos0,
+                                       k.shape[0], _p16(k), _p16(v)),
+                    "kv_write")
+
+    def kv_clear(self):
+        self._check(lib().llm_kv_clear(self._ctx), "kv_clear")
+
+    def sync(self):
+        self._check(lib().llm_sync(self._ctx), "sync")
+
+    def record(self, slot):
+        self._check(lib().llm_event_record(self._ctx, slot), "event_record")
+
+    def elapsed_ms(self, a, b):
+        ms = ctypes.c_float()
+        self._check(lib().llm_event_elapsed_ms(self._ctx, a, b,
+                                               ctypes.byref(ms)), "elapsed")
+        return ms.value

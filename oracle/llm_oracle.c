@@ -1,0 +1,777 @@
+/*
+ * llm_oracle.c -- CPU restatement of LLM-ACCEL's fixed-point golden model.
+ *
+ * TEST INFRASTRUCTURE ONLY (parity checker and CPU baseline).  Nothing in
+ * the product path links or calls this file.
+ *
+ * Citations are to /root/reference: "host:" = host/host_qwen_8x64.cpp,
+ * "ctrl:" = kernel/control_cache_8x64.cpp.
+ *
+ * Raw-integer notation used below:  rnd(v, s) = floor(v / 2^s + 1/2)
+ * (ap_fixed AP_RND dropping s fraction bits), sat16 / sat32 = AP_SAT into
+ * the 16- / 32-bit signed range.
+ */
+#include "llm_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define ATTN_TILE 64u /* kAttentionTile, host:44 / CC8_ATTN_TILE */
+
+/* ------------------------------------------------------------------ */
+/* fixed-point helpers                                                  */
+/* ------------------------------------------------------------------ */
+static inline int64_t rnd64(int64_t v, int s) {
+    /* arithmetic shift (gcc), adding the first dropped bit */
+    return (v + ((int64_t)1 << (s - 1))) >> s;
+}
+static inline __int128 rnd128(__int128 v, int s) {
+    return (v + ((__int128)1 << (s - 1))) >> s;
+}
+static inline int32_t sat32(int64_t v) {
+    if (v > INT32_MAX) return INT32_MAX;
+    if (v < INT32_MIN) return INT32_MIN;
+    return (int32_t)v;
+}
+static inline int32_t sat32_128(__int128 v) {
+    if (v > INT32_MAX) return INT32_MAX;
+    if (v < INT32_MIN) return INT32_MIN;
+    return (int32_t)v;
+}
+static inline int16_t sat16(int64_t v) {
+    if (v > INT16_MAX) return INT16_MAX;
+    if (v < INT16_MIN) return INT16_MIN;
+    return (int16_t)v;
+}
+/* golden_weight_t(golden_fm_t x): Q8.8 -> Q4.12, exact shift, saturating
+ * at +-8 (host:3251-3252, :3706-3708). */
+static inline int32_t fm_to_wt(int16_t x) { return sat16((int32_t)x * 16); }
+/* golden_clamp (host:523-535) on raw Q8.8. */
+static inline int16_t clamp16(int16_t v, int16_t lo, int16_t hi) {
+    return v < lo ? lo : (v > hi ? hi : v);
+}
+
+/* ------------------------------------------------------------------ */
+/* hls::exp tables                                                      */
+/* ------------------------------------------------------------------ */
+/* golden_exp sees Q8.8 inputs clamped to [-8, 8] (host:578-586);
+ * golden_attention_probability sees [-8, 0] (host:588-596).  The tables
+ * hold the candidate definition of the two hls::exp instantiations. */
+static int16_t g_exp_q8_8[4097];  /* x raw -2048 .. 2048 */
+static int16_t g_exp_q2_14[2049]; /* x raw -2048 .. 0    */
+static int g_tables_ready = 0;
+
+static int16_t exp_entry(int x_raw, int frac_bits, int policy) {
+    long double x = (long double)x_raw / 256.0L;
+    long double y = expl(x) * (long double)(1 << frac_bits);
+    long double q = policy == ORC_EXP_ROUND ? floorl(y + 0.5L) : floorl(y);
+    if (q > 32767.0L) q = 32767.0L;
+    return (int16_t)q;
+}
+
+void orc_set_exp_policy(int q8_8_policy, int q2_14_policy) {
+    for (int x = -2048; x <= 2048; x++)
+        g_exp_q8_8[x + 2048] = exp_entry(x, 8, q8_8_policy);
+    for (int x = -2048; x <= 0; x++)
+        g_exp_q2_14[x + 2048] = exp_entry(x, 14, q2_14_policy);
+    g_tables_ready = 1;
+}
+
+/* Install explicit tables: q8_8 covers x raw -2048..2048 (4097 entries),
+ * q2_14 covers x raw -2048..0 (2049 entries).  Either may be NULL. */
+void orc_set_exp_tables(const int16_t* q8_8, const int16_t* q2_14) {
+    if (!g_tables_ready) orc_set_exp_policy(ORC_EXP_FLOOR, ORC_EXP_FLOOR);
+    if (q8_8) memcpy(g_exp_q8_8, q8_8, sizeof(g_exp_q8_8));
+    if (q2_14) memcpy(g_exp_q2_14, q2_14, sizeof(g_exp_q2_14));
+}
+
+static void ensure_tables(void) {
+    if (!g_tables_ready) orc_set_exp_policy(ORC_EXP_FLOOR, ORC_EXP_FLOOR);
+}
+
+int16_t orc_exp_q8_8(int16_t x) {
+    ensure_tables();
+    int16_t c = clamp16(x, -2048, 2048);
+    return g_exp_q8_8[c + 2048];
+}
+
+int16_t orc_attn_prob(int16_t x) {
+    ensure_tables();
+    int16_t c = clamp16(x, -2048, 0);
+    return g_exp_q2_14[c + 2048];
+}
+
+void orc_get_exp_tables(int16_t* q8_8_table, int16_t* q2_14_table) {
+    ensure_tables();
+    if (q8_8_table) memcpy(q8_8_table, g_exp_q8_8 + 0, 2049 * sizeof(int16_t));
+    if (q2_14_table) memcpy(q2_14_table, g_exp_q2_14, 2049 * sizeof(int16_t));
+}
+
+/* ------------------------------------------------------------------ */
+/* scalar primitives                                                    */
+/* ------------------------------------------------------------------ */
+int16_t orc_quantize_fix16(double v) { /* host:496-505 */
+    double s = round(v * 256.0);
+    if (s > 32767.0) return 32767;
+    if (s < -32768.0) return -32768;
+    return (int16_t)s;
+}
+
+/* golden_recip (host:537-576).  fm(2^-12) is raw 0, so `safe` is
+ * max(x, 0).  Each Newton step: est = fm(est * (2 - safe*est)), an exact
+ * 24-fraction-bit product rounded once to Q8.8. */
+int16_t orc_recip(int16_t x) {
+    int32_t safe = x < 0 ? 0 : x;
+    int32_t est;
+    if (safe >= 16384) est = 4;          /* >= 64   -> 1/64 */
+    else if (safe >= 8192) est = 8;      /* >= 32   -> 1/32 */
+    else if (safe >= 4096) est = 16;     /* >= 16   -> 1/16 */
+    else if (safe >= 2048) est = 32;     /* >= 8    -> 1/8  */
+    else if (safe >= 1024) est = 64;     /* >= 4    -> 1/4  */
+    else if (safe >= 512) est = 128;     /* >= 2    -> 1/2  */
+    else if (safe >= 256) est = 256;     /* >= 1    -> 1    */
+    else if (safe >= 128) est = 512;     /* >= 0.5  -> 2    */
+    else if (safe >= 64) est = 1024;     /* >= 0.25 -> 4    */
+    else if (safe >= 32) est = 2048;     /* >= .125 -> 8    */
+    else est = 4096;                     /*         -> 16   */
+    for (int i = 0; i < 3; i++) {
+        int64_t d = ((int64_t)2 << 16) - (int64_t)safe * est; /* 16 fb */
+        est = sat16(rnd64((int64_t)est * d, 16));             /* 24->8 */
+    }
+    return clamp16((int16_t)est, 0, 16384);
+}
+
+/* golden_rsqrt (host:621-656) on a Q16.16 argument. */
+int16_t orc_rsqrt(int32_t v) {
+    int64_t safe = v < 16 ? 16 : v; /* accum(2^-12) = raw 16 */
+    int32_t est;
+    if (safe >= ((int64_t)64 << 16)) est = 32;       /* 0.125 */
+    else if (safe >= ((int64_t)16 << 16)) est = 64;  /* 0.25  */
+    else if (safe >= ((int64_t)4 << 16)) est = 128;  /* 0.5   */
+    else if (safe >= ((int64_t)1 << 16)) est = 256;  /* 1     */
+    else if (safe >= 16384) est = 512;               /* 2     */
+    else if (safe >= 4096) est = 1024;               /* 4     */
+    else est = 2048;                                 /* 8     */
+    for (int i = 0; i < 3; i++) {
+        /* accum(est)*accum(est): est^2 is exact at 16 fraction bits */
+        int32_t square = sat32((int64_t)est * est);
+        /* 1.5 - 0.5*safe*square, exact at 48 fraction bits */
+        __int128 t = ((__int128)98304 << 32) -
+                     (__int128)32768 * safe * (__int128)square;
+        int32_t refine = sat32_128(rnd128(t, 32));
+        /* fm(accum(est) * refine): 32 -> 8 fraction bits */
+        est = sat16(rnd64((int64_t)est * refine, 16));
+    }
+    return clamp16((int16_t)est, 0, 8192);
+}
+
+/* golden_silu (host:658-668). */
+int16_t orc_silu(int16_t x) {
+    if (x >= 0) {
+        int16_t e = orc_exp_q8_8(sat16(-(int32_t)x));
+        int16_t r = orc_recip(sat16(256 + (int32_t)e));
+        return sat16(rnd64((int64_t)x * r, 8));
+    }
+    int16_t e = orc_exp_q8_8(x);
+    int16_t r = orc_recip(sat16(256 + (int32_t)e));
+    return sat16(rnd64((int64_t)x * e * r, 16));
+}
+
+/* golden_fm_t(golden_accum_t(1) / max(sum, 2^-12)) (host:3726-3730,
+ * ctrl:4093-4099).  The ap_fixed quotient keeps 16 fraction bits
+ * (truncating integer division), then AP_RND to Q8.8. */
+int16_t orc_inv_sum(int32_t sum) {
+    int64_t b = sum < 16 ? 16 : sum;
+    int64_t q = (((int64_t)1 << 32)) / b;
+    return sat16(rnd64(q, 8));
+}
+
+/* ------------------------------------------------------------------ */
+/* vector / matrix ops                                                  */
+/* ------------------------------------------------------------------ */
+static int g_threads = 0;
+void orc_set_threads(int n) {
+    g_threads = n;
+#ifdef _OPENMP
+    if (n > 0) omp_set_num_threads(n);
+#endif
+}
+
+/* golden_projection (host:3105-3142): exact 48-bit raw Q28.20 dot
+ * product, narrowed Q28.20 -> Q16.16 (AP_RND, AP_SAT) -> Q8.8. */
+void orc_projection(const int16_t* x, uint32_t rows, uint32_t in_dim,
+                    const int16_t* w, uint32_t out_dim, int16_t* y) {
+    #pragma omp parallel for schedule(static) if (g_threads != 1)
+    for (uint32_t o = 0; o < out_dim; o++) {
+        const int16_t* wr = w + (size_t)o * in_dim;
+        for (uint32_t r = 0; r < rows; r++) {
+            const int16_t* xr = x + (size_t)r * in_dim;
+            int64_t acc = 0;
+            for (uint32_t k = 0; k < in_dim; k++)
+                acc += (int32_t)xr[k] * (int32_t)wr[k];
+            int32_t t = sat32(rnd64(acc, 4));
+            y[(size_t)r * out_dim + o] = sat16(rnd64(t, 8));
+        }
+    }
+}
+
+void orc_residual(const int16_t* a, const int16_t* b, size_t n, int16_t* y) {
+    for (size_t i = 0; i < n; i++) y[i] = sat16((int32_t)a[i] + b[i]);
+}
+
+/* golden_rmsnorm (host:3162-3197). */
+void orc_rmsnorm(const int16_t* x, uint32_t rows, uint32_t cols,
+                 const int16_t* gamma, int16_t* y) {
+    int16_t inv_elems = orc_recip(sat16((int64_t)cols * 256));
+    for (uint32_t r = 0; r < rows; r++) {
+        const int16_t* xr = x + (size_t)r * cols;
+        int64_t sum_sq = 0; /* saturating; every term is >= 0 */
+        for (uint32_t c = 0; c < cols; c++) {
+            sum_sq += (int32_t)xr[c] * xr[c];
+            if (sum_sq > INT32_MAX) sum_sq = INT32_MAX;
+        }
+        int32_t mean = sat32(rnd64(sum_sq * inv_elems * 256, 16));
+        /* + accum(1e-6): that constant is raw 0 in Q16.16 */
+        int16_t inv = orc_rsqrt(mean);
+        for (uint32_t c = 0; c < cols; c++)
+            y[(size_t)r * cols + c] =
+                sat16(rnd64((int64_t)xr[c] * inv * gamma[c], 16));
+    }
+}
+
+void orc_silu_mul(const int16_t* gate, const int16_t* up, size_t n,
+                  int16_t* y) {
+    for (size_t i = 0; i < n; i++)
+        y[i] = sat16(rnd64((int64_t)orc_silu(gate[i]) * up[i], 8));
+}
+
+/* initialize_persistent_auxiliary_data (host:2159-2189). */
+void orc_rope_table(uint32_t max_seq, uint32_t head_dim, double theta,
+                    int16_t* table) {
+    uint32_t half = head_dim / 2;
+    for (uint32_t p = 0; p < max_seq; p++) {
+        for (uint32_t i = 0; i < half; i++) {
+            double exponent = (double)(2 * i) / head_dim;
+            double inv_freq = 1.0 / pow(theta, exponent);
+            double angle = p * inv_freq;
+            table[(size_t)p * head_dim + i] = orc_quantize_fix16(cos(angle));
+            table[(size_t)p * head_dim + half + i] =
+                orc_quantize_fix16(sin(angle));
+        }
+    }
+}
+
+/* rotate_fix16_pair_with_quantized_rope (host:4765-4788): pairs (i,
+ * i + d/2), each output rounded once from the exact Q16.16 expression. */
+void orc_rope_apply(int16_t* vec, uint32_t heads, uint32_t head_dim,
+                    const int16_t* row) {
+    uint32_t half = head_dim / 2;
+    for (uint32_t h = 0; h < heads; h++) {
+        int16_t* b = vec + (size_t)h * head_dim;
+        for (uint32_t i = 0; i < half; i++) {
+            int32_t x0 = b[i], x1 = b[half + i];
+            int32_t c = row[i], s = row[half + i];
+            b[i] = sat16(rnd64((int64_t)x0 * c - (int64_t)x1 * s, 8));
+            b[half + i] = sat16(rnd64((int64_t)x1 * c + (int64_t)x0 * s, 8));
+        }
+    }
+}
+
+/* fm(1/sqrt(d)) (host:3225-3227): AP_RND of the double. */
+static int32_t qk_scale(uint32_t d) {
+    return (int32_t)floor(256.0 / sqrt((double)d) + 0.5);
+}
+
+/* golden_attention_mm(query, k_tile, 64, true) (host:3219-3278):
+ * four k-mod-4 Q16.16 banks of AP_RND-narrowed Q8.8 x Q4.12 products,
+ * summed, scaled by fm(1/sqrt(d)) at Q16.16, narrowed to Q8.8. */
+void orc_qk_scores(const int16_t* q, uint32_t G, uint32_t d,
+                   const int16_t* k, uint32_t n, int16_t* scores) {
+    int64_t scale = (int64_t)qk_scale(d) << 8; /* accum(scale) raw */
+    for (uint32_t r = 0; r < G; r++) {
+        for (uint32_t p = 0; p < n; p++) {
+            int32_t banks[4] = {0, 0, 0, 0};
+            for (uint32_t e = 0; e < d; e++) {
+                int32_t w = fm_to_wt(k[(size_t)p * d + e]);
+                int32_t prod = (int32_t)rnd64((int64_t)q[r * d + e] * w, 4);
+                banks[e & 3] = sat32((int64_t)banks[e & 3] + prod);
+            }
+            int32_t total = sat32((int64_t)banks[0] + banks[1] +
+                                  banks[2] + banks[3]);
+            total = sat32(rnd64((int64_t)total * scale, 16));
+            scores[(size_t)r * n + p] = sat16(rnd64(total, 8));
+        }
+    }
+}
+
+/* golden_tiled_flash_attention_q2_14_impl (host:3609-3738) and the
+ * legacy Q8.8 golden_tiled_flash_attention_impl<fm_t,false>
+ * (host:3419-3575).  Tiles of 64 positions anchored at position 0. */
+void orc_attention(const int16_t* q, uint32_t G, uint32_t d,
+                   const int16_t* k, const int16_t* v, uint32_t n,
+                   int semantics, int16_t* out) {
+    const int legacy = semantics == 2;
+    int16_t* m = malloc(G * sizeof(int16_t));
+    int32_t* sum = calloc(G, sizeof(int32_t));
+    int32_t* acc = calloc((size_t)G * d, sizeof(int32_t));
+    int16_t* scores = malloc((size_t)G * ATTN_TILE * sizeof(int16_t));
+    int16_t* prob = malloc((size_t)G * ATTN_TILE * sizeof(int16_t));
+    for (uint32_t r = 0; r < G; r++) m[r] = INT16_MIN; /* fm(-128) */
+
+    for (uint32_t tb = 0; tb < n; tb += ATTN_TILE) {
+        uint32_t tl = n - tb < ATTN_TILE ? n - tb : ATTN_TILE;
+        orc_qk_scores(q, G, d, k + (size_t)tb * d, tl, scores);
+        for (uint32_t r = 0; r < G; r++) {
+            int16_t rowmax = m[r];
+            for (uint32_t p = 0; p < tl; p++)
+                if (scores[r * tl + p] > rowmax) rowmax = scores[r * tl + p];
+            int16_t diff = sat16((int32_t)m[r] - rowmax);
+            int64_t old; /* accum(old_scale) raw, Q16.16 */
+            int64_t tile_sum = 0;
+            if (legacy) {
+                old = (int64_t)orc_exp_q8_8(diff) << 8;
+                for (uint32_t p = 0; p < tl; p++) {
+                    int16_t pr = orc_exp_q8_8(
+                        sat16((int32_t)scores[r * tl + p] - rowmax));
+                    prob[r * tl + p] = pr;
+                    tile_sum = sat32(tile_sum + ((int64_t)pr << 8));
+                }
+            } else {
+                old = (int64_t)orc_attn_prob(diff) << 2;
+                for (uint32_t p = 0; p < tl; p++) {
+                    int16_t pr = orc_attn_prob(
+                        sat16((int32_t)scores[r * tl + p] - rowmax));
+                    prob[r * tl + p] = pr;
+                    tile_sum = sat32(tile_sum + ((int64_t)pr << 2));
+                }
+            }
+            /* sum = accum(sum*old + tile_sum): exact, one rounding */
+            sum[r] = sat32(rnd64((int64_t)sum[r] * old + (tile_sum << 16), 16));
+            m[r] = rowmax;
+            for (uint32_t e = 0; e < d; e++)
+                acc[r * d + e] = sat32(rnd64((int64_t)acc[r * d + e] * old, 16));
+        }
+        /* PV for this tile */
+        for (uint32_t r = 0; r < G; r++) {
+            for (uint32_t e = 0; e < d; e++) {
+                int32_t banks[4] = {0, 0, 0, 0};
+                for (uint32_t p = 0; p < tl; p++) {
+                    int32_t w = fm_to_wt(v[(size_t)(tb + p) * d + e]);
+                    int64_t pw = (int64_t)prob[r * tl + p] * w;
+                    /* raw payload / legacy: Q8.8 x Q4.12 (20 fb);
+                     * direct: Q2.14 x Q4.12 (26 fb) -> Q16.16 */
+                    int32_t prod = (int32_t)(semantics == 1 ? rnd64(pw, 10)
+                                                            : rnd64(pw, 4));
+                    banks[p & 3] = sat32((int64_t)banks[p & 3] + prod);
+                }
+                int32_t total = sat32((int64_t)banks[0] + banks[1] +
+                                      banks[2] + banks[3]);
+                if (semantics == 0) /* x accum(fm(1/64)) = raw 4<<8 */
+                    total = sat32(rnd64((int64_t)total * 1024, 16));
+                int16_t tv = sat16(rnd64(total, 8));
+                acc[r * d + e] = sat32((int64_t)acc[r * d + e] + ((int32_t)tv << 8));
+            }
+        }
+    }
+    for (uint32_t r = 0; r < G; r++) {
+        int64_t inv = orc_inv_sum(sum[r]);
+        for (uint32_t e = 0; e < d; e++)
+            out[r * d + e] = sat16(rnd64((int64_t)acc[r * d + e] * inv, 16));
+    }
+    free(m); free(sum); free(acc); free(scores); free(prob);
+}
+
+/* ------------------------------------------------------------------ */
+/* random generators (libstdc++ mt19937 + uniform_int_distribution)    */
+/* ------------------------------------------------------------------ */
+typedef struct { uint32_t mt[624]; uint32_t idx; } mt19937_t;
+
+static void mt_seed(mt19937_t* g, uint32_t s) {
+    g->mt[0] = s;
+    for (uint32_t i = 1; i < 624; i++)
+        g->mt[i] = 1812433253u * (g->mt[i - 1] ^ (g->mt[i - 1] >> 30)) + i;
+    g->idx = 624;
+}
+
+static void mt_twist(mt19937_t* g) {
+    for (uint32_t i = 0; i < 624; i++) {
+        uint32_t y = (g->mt[i] & 0x80000000u) | (g->mt[(i + 1) % 624] & 0x7fffffffu);
+        g->mt[i] = g->mt[(i + 397) % 624] ^ (y >> 1) ^ ((y & 1u) ? 0x9908b0dfu : 0u);
+    }
+    g->idx = 0;
+}
+
+static inline uint32_t mt_next(mt19937_t* g) {
+    if (g->idx >= 624) mt_twist(g);
+    uint32_t y = g->mt[g->idx++];
+    y ^= y >> 11;
+    y ^= (y << 7) & 0x9d2c5680u;
+    y ^= (y << 15) & 0xefc60000u;
+    y ^= y >> 18;
+    return y;
+}
+
+uint32_t orc_mt19937_nth(uint32_t seed, uint64_t n) {
+    mt19937_t g;
+    mt_seed(&g, seed);
+    uint32_t v = 0;
+    for (uint64_t i = 0; i < n; i++) v = mt_next(&g);
+    return v;
+}
+
+static inline int32_t uid_draw(mt19937_t* g, int32_t a, int32_t b, int alg) {
+    uint32_t range = (uint32_t)(b - a) + 1u;
+    if (alg == ORC_UID_LEMIRE) {
+        uint64_t p = (uint64_t)mt_next(g) * range;
+        uint32_t lo = (uint32_t)p;
+        if (lo < range) {
+            uint32_t thr = (uint32_t)(-range) % range;
+            while (lo < thr) {
+                p = (uint64_t)mt_next(g) * range;
+                lo = (uint32_t)p;
+            }
+        }
+        return (int32_t)(p >> 32) + a;
+    }
+    uint64_t scaling = 0xffffffffull / range;
+    uint64_t past = (uint64_t)range * scaling;
+    uint64_t r;
+    do r = mt_next(g); while (r >= past);
+    return (int32_t)(r / scaling) + a;
+}
+
+void orc_uniform_ints(uint32_t seed, int32_t lo, int32_t hi, int alg,
+                      size_t n, int32_t* out) {
+    mt19937_t g;
+    mt_seed(&g, seed);
+    for (size_t i = 0; i < n; i++) out[i] = uid_draw(&g, lo, hi, alg);
+}
+
+void orc_make_random_tensor(uint32_t rows, uint32_t cols, uint32_t seed,
+                            int32_t lo, int32_t hi, int alg, int16_t* out) {
+    mt19937_t g;
+    mt_seed(&g, seed);
+    for (size_t i = 0; i < (size_t)rows * cols; i++)
+        out[i] = (int16_t)uid_draw(&g, lo, hi, alg);
+}
+
+/* ------------------------------------------------------------------ */
+/* model                                                                */
+/* ------------------------------------------------------------------ */
+struct orc_model {
+    orc_shape_t s;
+    uint32_t kept;
+    int16_t** w; /* [kept * 7] row-major [out][in] */
+    int16_t* norms;
+    int16_t* embedding;
+};
+
+uint32_t orc_proj_in_dim(const orc_shape_t* s, uint32_t p) {
+    return p == ORC_PROJ_DOWN ? s->intermediate_size : s->hidden_size;
+}
+uint32_t orc_proj_out_dim(const orc_shape_t* s, uint32_t p) {
+    uint32_t d = s->hidden_size / s->num_heads;
+    switch (p) {
+    case ORC_PROJ_K: case ORC_PROJ_V: return s->num_kv_heads * d;
+    case ORC_PROJ_GATE: case ORC_PROJ_UP: return s->intermediate_size;
+    default: return s->hidden_size;
+    }
+}
+
+orc_model_t* orc_model_create(const orc_shape_t* shape, uint32_t kept,
+                              int with_embedding) {
+    orc_model_t* m = calloc(1, sizeof(*m));
+    m->s = *shape;
+    m->kept = kept;
+    m->w = calloc((size_t)kept * ORC_PROJ_COUNT, sizeof(int16_t*));
+    for (uint32_t l = 0; l < kept; l++)
+        for (uint32_t p = 0; p < ORC_PROJ_COUNT; p++)
+            m->w[l * ORC_PROJ_COUNT + p] = calloc(
+                (size_t)orc_proj_in_dim(shape, p) * orc_proj_out_dim(shape, p),
+                sizeof(int16_t));
+    m->norms = calloc((size_t)(2 * shape->num_layers + 1) * shape->hidden_size,
+                      sizeof(int16_t));
+    if (with_embedding)
+        m->embedding = calloc((size_t)shape->vocab_size * shape->hidden_size,
+                              sizeof(int16_t));
+    return m;
+}
+
+void orc_model_destroy(orc_model_t* m) {
+    if (!m) return;
+    for (uint32_t i = 0; i < m->kept * ORC_PROJ_COUNT; i++) free(m->w[i]);
+    free(m->w); free(m->norms); free(m->embedding); free(m);
+}
+
+int16_t* orc_model_weight(orc_model_t* m, uint32_t layer, uint32_t proj) {
+    if (layer >= m->kept || proj >= ORC_PROJ_COUNT) return NULL;
+    return m->w[layer * ORC_PROJ_COUNT + proj];
+}
+int16_t* orc_model_norms(orc_model_t* m) { return m->norms; }
+int16_t* orc_model_embedding(orc_model_t* m) { return m->embedding; }
+
+static uint64_t cdiv(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
+
+/* initialize_random_model (host:842-869) with the packed-tile accessor
+ * projection_weight_raw (host:899-935): 16x16 tiles, tile t of the whole
+ * model lives in shard group (t & 1), local block (t >> 1); lane
+ * (out%16)*16 + in%16 of the tile is word lane%32 of shard
+ * group*8 + lane/32. */
+void orc_model_init_reference_random(orc_model_t* m, uint32_t seed, int alg) {
+    const orc_shape_t* s = &m->s;
+    mt19937_t g;
+    mt_seed(&g, seed);
+    if (m->embedding) {
+        for (size_t i = 0; i < (size_t)s->vocab_size * s->hidden_size; i++)
+            m->embedding[i] = (int16_t)uid_draw(&g, -128, 128, alg);
+    } else {
+        for (size_t i = 0; i < (size_t)s->vocab_size * s->hidden_size; i++)
+            (void)uid_draw(&g, -128, 128, alg);
+    }
+    for (size_t i = 0; i < (size_t)(2 * s->num_layers + 1) * s->hidden_size; i++)
+        m->norms[i] = (int16_t)uid_draw(&g, 224, 288, alg);
+
+    uint64_t ptiles[ORC_PROJ_COUNT], pbase[ORC_PROJ_COUNT], layer_tiles = 0;
+    for (uint32_t p = 0; p < ORC_PROJ_COUNT; p++) {
+        ptiles[p] = cdiv(orc_proj_out_dim(s, p), 16) * cdiv(orc_proj_in_dim(s, p), 16);
+        pbase[p] = layer_tiles;
+        layer_tiles += ptiles[p];
+    }
+    uint64_t total_tiles = (uint64_t)s->num_layers * layer_tiles;
+    uint64_t shard_words = cdiv(total_tiles, 2);
+    for (uint32_t shard = 0; shard < 16; shard++) {
+        uint32_t group = shard / 8, tile_word = shard % 8;
+        for (uint64_t w = 0; w < shard_words; w++) {
+            uint64_t tile = 2 * w + group;
+            uint64_t layer = tile / layer_tiles;
+            uint64_t rem = tile % layer_tiles;
+            for (uint32_t lane = 0; lane < 32; lane++) {
+                int16_t val = (int16_t)uid_draw(&g, -64, 64, alg);
+                if (tile >= total_tiles || layer >= m->kept) continue;
+                uint32_t p = 0;
+                while (p + 1 < ORC_PROJ_COUNT && rem >= pbase[p + 1]) p++;
+                uint64_t t = rem - pbase[p];
+                uint32_t in_dim = orc_proj_in_dim(s, p);
+                uint32_t out_dim = orc_proj_out_dim(s, p);
+                uint64_t in_tiles = cdiv(in_dim, 16);
+                uint32_t lane_in_tile = tile_word * 32 + lane;
+                uint64_t out = (t / in_tiles) * 16 + lane_in_tile / 16;
+                uint64_t in = (t % in_tiles) * 16 + lane_in_tile % 16;
+                if (out < out_dim && in < in_dim)
+                    m->w[layer * ORC_PROJ_COUNT + p][out * in_dim + in] = val;
+            }
+        }
+    }
+}
+
+uint32_t orc_lm_head_argmax(const int16_t* table, uint32_t vocab,
+                            uint32_t hidden, const int16_t* h) {
+    int64_t best = INT64_MIN;
+    uint32_t best_tok = 0;
+    for (uint32_t t = 0; t < vocab; t++) {
+        const int16_t* row = table + (size_t)t * hidden;
+        int64_t sc = 0;
+        for (uint32_t e = 0; e < hidden; e++) sc += (int32_t)h[e] * row[e];
+        if (sc > best) { best = sc; best_tok = t; }
+    }
+    return best_tok;
+}
+
+uint64_t orc_checksum(const int16_t* v, size_t n) {
+    uint64_t c = 1469598103934665603ull;
+    for (size_t i = 0; i < n; i++) {
+        c ^= (uint16_t)v[i];
+        c *= 1099511628211ull;
+    }
+    return c;
+}
+
+/* ------------------------------------------------------------------ */
+/* resident tasks                                                       */
+/* ------------------------------------------------------------------ */
+static size_t kv_index(const orc_shape_t* s, uint32_t layer, uint32_t h,
+                       uint32_t pos) {
+    uint32_t d = s->hidden_size / s->num_heads;
+    return (((size_t)layer * s->num_kv_heads + h) * s->max_seq_len + pos) * d;
+}
+
+static void status_counters(const orc_shape_t* s, uint32_t op, uint32_t R,
+                            uint32_t position, orc_status_t* st);
+
+static void attention_sublayer(const orc_model_t* m, int16_t* kc, int16_t* vc,
+                               uint32_t layer, uint32_t R, uint32_t pos,
+                               const int16_t* in, int16_t* out, int sem) {
+    const orc_shape_t* s = &m->s;
+    uint32_t H = s->hidden_size, d = H / s->num_heads;
+    uint32_t Hkv = s->num_kv_heads, G = s->num_heads / Hkv, Ckv = Hkv * d;
+    int16_t* xn = malloc((size_t)R * H * 2);
+    int16_t* q = malloc((size_t)R * H * 2);
+    int16_t* k = malloc((size_t)R * Ckv * 2);
+    int16_t* v = malloc((size_t)R * Ckv * 2);
+    int16_t* attn = malloc((size_t)R * H * 2);
+    int16_t* o = malloc((size_t)R * H * 2);
+    int16_t* rope = malloc((size_t)d * 2);
+    orc_rmsnorm(in, R, H, m->norms + (size_t)(2 * layer) * H, xn);
+    orc_projection(xn, R, H, m->w[layer * 7 + ORC_PROJ_Q], H, q);
+    orc_projection(xn, R, H, m->w[layer * 7 + ORC_PROJ_K], Ckv, k);
+    orc_projection(xn, R, H, m->w[layer * 7 + ORC_PROJ_V], Ckv, v);
+    for (uint32_t t = 0; t < R; t++) {
+        uint32_t p = pos + t;
+        /* table row for position p, computed as the host table does */
+        for (uint32_t i = 0; i < d / 2; i++) {
+            double angle = p * (1.0 / pow(1000000.0, (double)(2 * i) / d));
+            rope[i] = orc_quantize_fix16(cos(angle));
+            rope[d / 2 + i] = orc_quantize_fix16(sin(angle));
+        }
+        orc_rope_apply(q + (size_t)t * H, s->num_heads, d, rope);
+        orc_rope_apply(k + (size_t)t * Ckv, Hkv, d, rope);
+        for (uint32_t h = 0; h < Hkv; h++) {
+            memcpy(kc + kv_index(s, layer, h, p), k + (size_t)t * Ckv + h * d, d * 2);
+            memcpy(vc + kv_index(s, layer, h, p), v + (size_t)t * Ckv + h * d, d * 2);
+        }
+        for (uint32_t h = 0; h < Hkv; h++)
+            orc_attention(q + (size_t)t * H + (size_t)h * G * d, G, d,
+                          kc + kv_index(s, layer, h, 0),
+                          vc + kv_index(s, layer, h, 0), p + 1, sem,
+                          attn + (size_t)t * H + (size_t)h * G * d);
+    }
+    orc_projection(attn, R, H, m->w[layer * 7 + ORC_PROJ_O], H, o);
+    orc_residual(in, o, (size_t)R * H, out);
+    free(xn); free(q); free(k); free(v); free(attn); free(o); free(rope);
+}
+
+static void ffn_sublayer(const orc_model_t* m, uint32_t layer, uint32_t R,
+                         const int16_t* in, int16_t* out) {
+    const orc_shape_t* s = &m->s;
+    uint32_t H = s->hidden_size, I = s->intermediate_size;
+    int16_t* xn = malloc((size_t)R * H * 2);
+    int16_t* g = malloc((size_t)R * I * 2);
+    int16_t* u = malloc((size_t)R * I * 2);
+    int16_t* dn = malloc((size_t)R * H * 2);
+    orc_rmsnorm(in, R, H, m->norms + (size_t)(2 * layer + 1) * H, xn);
+    orc_projection(xn, R, H, m->w[layer * 7 + ORC_PROJ_GATE], I, g);
+    orc_projection(xn, R, H, m->w[layer * 7 + ORC_PROJ_UP], I, u);
+    orc_silu_mul(g, u, (size_t)R * I, g);
+    orc_projection(g, R, I, m->w[layer * 7 + ORC_PROJ_DOWN], H, dn);
+    orc_residual(in, dn, (size_t)R * H, out);
+    free(xn); free(g); free(u); free(dn);
+}
+
+/* Command validation order of control_cache_8x64_dual_core
+ * (ctrl:5883-5957, :5974-5981, :6041-6054), resident-layer image. */
+int orc_task(const orc_model_t* m, int16_t* kc, int16_t* vc, uint32_t op,
+             uint32_t layer, uint32_t R, uint32_t pos, const int16_t* in,
+             int16_t* out, int sem, orc_status_t* st) {
+    const orc_shape_t* s = &m->s;
+    orc_status_t local;
+    if (!st) st = &local;
+    memset(st, 0, sizeof(*st));
+    st->token_count = R;
+    st->last_task = 1;
+    if (R > 8) { st->code = 2; return 2; }
+    st->op = op;
+    if (op > 20) { st->code = 1; return 1; }
+    if (op == 0) return 0;
+    if (layer >= s->num_layers) { st->code = 5; return 5; }
+    if (op == 20) {
+        if (R == 0) { st->code = 2; return 2; }
+        orc_rmsnorm(in, R, s->hidden_size,
+                    m->norms + (size_t)(2 * s->num_layers) * s->hidden_size, out);
+        status_counters(s, op, R, pos, st);
+        return 0;
+    }
+    if (op == 16 || op == 18 || op == 19) {
+        if (R == 0) { st->code = 2; return 2; }
+        if (pos >= s->max_seq_len || pos + R > s->max_seq_len) {
+            st->code = 4;
+            return 4;
+        }
+        if (layer >= m->kept) { st->code = 5; return 5; }
+        if (op == 18) {
+            attention_sublayer(m, kc, vc, layer, R, pos, in, out, sem);
+        } else if (op == 19) {
+            ffn_sublayer(m, layer, R, in, out);
+        } else {
+            int16_t* mid = malloc((size_t)R * s->hidden_size * 2);
+            attention_sublayer(m, kc, vc, layer, R, pos, in, mid, sem);
+            ffn_sublayer(m, layer, R, mid, out);
+            free(mid);
+        }
+        status_counters(s, op, R, pos, st);
+        return 0;
+    }
+    st->code = 1; /* per-operator diagnostics are not in this image */
+    return 1;
+}
+
+/* Schedule counters of the 8x64 controller, from its formulas
+ * (ctrl:5974-6029, :6165-6481, :5764, :1856-1929). */
+static void status_counters(const orc_shape_t* s, uint32_t op, uint32_t R,
+                            uint32_t pos, orc_status_t* st) {
+    uint32_t H = s->hidden_size, I = s->intermediate_size;
+    uint32_t d = H / s->num_heads, Ckv = s->num_kv_heads * d;
+    uint32_t vt = (R > 0 ? 1u : 0u) + (R > 4 ? 1u : 0u);
+    uint32_t hp = R * (uint32_t)cdiv(H, 16), ip = R * (uint32_t)cdiv(I, 16);
+    uint32_t waves = 0, mm = 0, vec = 0, pk = 0;
+    if (op == 20) {
+        st->vector_tasks = vt;
+        st->completed_packets = hp;
+        return;
+    }
+    vec += vt; pk += hp; /* first RMSNorm */
+    uint32_t begin = op == 19 ? 4 : 0, end = op == 18 ? 4 : 7;
+    for (uint32_t step = begin; step < end; step++) {
+        uint32_t out_dim = (step == 1 || step == 2) ? Ckv
+                         : (step == 4 || step == 5) ? I : H;
+        if (step == 3) {
+            uint32_t ow = (uint32_t)cdiv(d, 64), at = 0;
+            for (uint32_t t = 0; t < R; t++)
+                at += 2 * (uint32_t)cdiv(pos + t + 1, ATTN_TILE) * (1 + ow);
+            mm += at; pk += at * 32; waves += at / 2;
+        }
+        uint32_t w = (uint32_t)cdiv(out_dim, 128);
+        waves += w; mm += 2 * w; pk += 2 * w * 32;
+        if (step == 3) {
+            vec += vt; pk += hp;
+            if (op != 18) { vec += vt; pk += hp; }
+        } else if (step == 5) {
+            vec += vt; pk += ip;
+        } else if (step == 6) {
+            vec += vt; pk += hp;
+        }
+    }
+    st->output_waves = waves;
+    st->mm_tasks = mm;
+    st->vector_tasks = vec;
+    st->completed_packets = pk;
+}
+
+/* golden_prefill_decoder_layer_sequence (host:4854-4978). */
+void orc_prefill_layer_sequence(const orc_model_t* m, const int16_t* hidden,
+                                uint32_t rows, uint32_t layer, int sem,
+                                int16_t* post_attention, int16_t* out) {
+    const orc_shape_t* s = &m->s;
+    orc_shape_t one = *s;
+    uint32_t H = s->hidden_size, d = H / s->num_heads;
+    one.max_seq_len = rows;
+    size_t kvn = (size_t)s->num_kv_heads * rows * d;
+    int16_t* kc = calloc(kvn, 2);
+    int16_t* vc = calloc(kvn, 2);
+    int16_t* mid = malloc((size_t)rows * H * 2);
+    /* full-prefix recompute: all rows in one pass; KV indexed for layer 0
+     * of a one-layer, rows-long cache */
+    orc_model_t view = *m;
+    view.s = one;
+    view.s.num_layers = s->num_layers;
+    /* kv_index uses layer * Hkv * max_seq; use a layer-0 view */
+    view.w = m->w + (size_t)layer * ORC_PROJ_COUNT;
+    view.norms = m->norms + (size_t)(2 * layer) * H;
+    attention_sublayer(&view, kc, vc, 0, rows, 0, hidden, mid, sem);
+    if (post_attention) memcpy(post_attention, mid, (size_t)rows * H * 2);
+    ffn_sublayer(&view, 0, rows, mid, out);
+    free(kc); free(vc); free(mid);
+}

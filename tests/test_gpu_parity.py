@@ -1,0 +1,188 @@
+"""HIP path vs the CPU oracle, bit-exact: hidden states after every task,
+KV-cache contents and status records (reference contract: host
+verify-composed-prefill-block / generate --verify-e2e-golden,
+host/host_qwen_8x64.cpp:5227-5316, :9144-9249, where the reference
+observed max_raw_error 0 at the Qwen shape)."""
+import sys
+
+import numpy as np
+import pytest
+
+from oracle import orc
+import workloads
+from helpers import accel_shape, first_mismatch, oracle_from_synthetic, oracle_shape
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def _run_sequence(spec, layers, schedule, max_seq, seed=workloads.SEED,
+                  check_kv=True):
+    """schedule: list of (position, rows) blocks.  Runs T18/T19 per layer and
+    T20 on both paths, comparing after every task."""
+    import llm_accel
+    synth = workloads.SyntheticModel(spec, seed=seed, layers=layers)
+    oshape = oracle_shape(spec, layers=layers, max_seq=max_seq)
+    om = oracle_from_synthetic(synth, oshape)
+    kv = om.new_kv()
+    total_rows = sum(r for _, r in schedule)
+    hidden_all = synth.hidden_rows(total_rows)
+    with llm_accel.Accelerator(accel_shape(spec, layers=layers,
+                                           max_seq=max_seq)) as acc:
+        acc.load_model(synth)
+        row0 = 0
+        for pos, rows in schedule:
+            h = hidden_all[row0:row0 + rows]
+            row0 += rows
+            acc.upload(2, h)
+            cur = h
+            pair_in, pair_out = 2, 0
+            for layer in range(layers):
+                for op in (18, 19):
+                    _say(f"case {spec.name} L{layers} pos={pos} rows={rows} "
+                         f"layer={layer} op={op}")
+                    code, want, ost = om.task(kv, op, layer, cur, pos)
+                    assert code == 0
+                    rc, st = acc.task(op, layer, rows, pos, pair_in, pair_out)
+                    assert rc == 0
+                    got = acc.download(pair_out, rows)
+                    assert st.as_tuple() == ost.as_tuple()
+                    err = first_mismatch(got, want)
+                    assert err is None, f"op {op} layer {layer}: {err}"
+                    cur = want
+                    pair_in, pair_out = pair_out, pair_in
+            _say(f"case {spec.name} pos={pos} rows={rows} op=20")
+            code, want, ost = om.task(kv, 20, 0, cur, pos)
+            rc, st = acc.task(20, 0, rows, pos, pair_in, pair_out)
+            got = acc.download(pair_out, rows)
+            assert st.as_tuple() == ost.as_tuple()
+            assert first_mismatch(got, want) is None
+        if check_kv:
+            end = row0
+            for layer in range(layers):
+                for h in range(spec.kv_heads):
+                    k, v = acc.kv_read(layer, h, 0, end)
+                    err = first_mismatch(k, kv[0][layer, h, :end])
+                    assert err is None, f"K cache layer {layer} head {h}: {err}"
+                    err = first_mismatch(v, kv[1][layer, h, :end])
+                    assert err is None, f"V cache layer {layer} head {h}: {err}"
+
+
+def test_config_a_p8_then_decode():
+    # one P8 block then two single-row decode forwards.
+    _run_sequence(workloads.CONFIG_A, 1, [(0, 8), (8, 1), (9, 1)], max_seq=64)
+
+
+def test_config_a_two_layers_ragged_blocks():
+    # Ragged blocks (R = 3, 5, 8, 1) crossing the 64-position tile edge.
+    _run_sequence(workloads.CONFIG_A, 2, [(0, 3), (3, 5), (8, 8), (16, 1)],
+                  max_seq=128)
+
+
+def test_config_a_tile_boundary():
+    # A block straddling positions 60..67 exercises two tiles per row.
+    spec = workloads.CONFIG_A
+    blocks = [(p, 8) for p in range(0, 56, 8)] + [(56, 4), (60, 8), (68, 1)]
+    _run_sequence(spec, 1, blocks, max_seq=128)
+
+
+def test_config_b_p8_then_decode():
+    # one Qwen2.5-3B-shaped layer, P8 then one decode.
+    _run_sequence(workloads.CONFIG_B, 1, [(0, 8), (8, 1)], max_seq=64)
+
+
+def test_decoder_layer_op16_matches_18_19():
+    import llm_accel
+    spec = workloads.CONFIG_A
+    synth = workloads.SyntheticModel(spec, layers=1)
+    h = synth.hidden_rows(6)
+    with llm_accel.Accelerator(accel_shape(spec, layers=1, max_seq=64)) as a:
+        a.load_model(synth)
+        a.upload(2, h)
+        _say("case op16")
+        rc, st16 = a.task(16, 0, 6, 0, 2, 0)
+        got16 = a.download(0, 6)
+        a.kv_clear()
+        a.upload(2, h)
+        a.task(18, 0, 6, 0, 2, 0)
+        a.task(19, 0, 6, 0, 0, 1)
+        got = a.download(1, 6)
+        assert first_mismatch(got16, got) is None
+        oshape = oracle_shape(spec, layers=1, max_seq=64)
+        om = oracle_from_synthetic(synth, oshape)
+        code, want, ost = om.task(om.new_kv(), 16, 0, h, 0)
+        assert st16.as_tuple() == ost.as_tuple()
+
+
+def test_in_place_pairs():
+    import llm_accel
+    spec = workloads.CONFIG_A
+    synth = workloads.SyntheticModel(spec, layers=1)
+    h = synth.hidden_rows(4)
+    om = oracle_from_synthetic(synth, oracle_shape(spec, layers=1, max_seq=64))
+    kv = om.new_kv()
+    with llm_accel.Accelerator(accel_shape(spec, layers=1, max_seq=64)) as a:
+        a.load_model(synth)
+        a.upload(1, h)
+        _say("case in-place")
+        a.task(18, 0, 4, 0, 1, 1)
+        a.task(19, 0, 4, 0, 1, 1)
+        a.task(20, 0, 4, 0, 1, 1)
+        got = a.download(1, 4)
+    _, x, _ = om.task(kv, 18, 0, h, 0)
+    _, x, _ = om.task(kv, 19, 0, x, 0)
+    _, x, _ = om.task(kv, 20, 0, x, 0)
+    assert first_mismatch(got, x) is None
+
+
+def test_status_validation_matches_controller():
+    import llm_accel
+    spec = workloads.CONFIG_A
+    synth = workloads.SyntheticModel(spec, layers=1)
+    om = oracle_from_synthetic(synth, oracle_shape(spec, layers=1, max_seq=64))
+    kv = om.new_kv()
+    h = synth.hidden_rows(8)
+    cases = [
+        (18, 0, 9, 0), (18, 0, 0, 0), (21, 0, 1, 0), (5, 0, 1, 0),
+        (5, 3, 1, 0), (18, 1, 1, 0), (18, 0, 1, 64), (18, 0, 4, 62),
+        (20, 0, 0, 0), (20, 0, 8, 999), (0, 0, 3, 0), (17, 0, 2, 0),
+    ]
+    with llm_accel.Accelerator(accel_shape(spec, layers=1, max_seq=64)) as a:
+        a.load_model(synth)
+        a.upload(2, h)
+        for op, layer, rows, pos in cases:
+            _say(f"case status op={op} layer={layer} rows={rows} pos={pos}")
+            rc, st = a.task(op, layer, rows, pos, 2, 0)
+            code, _, ost = om.task(kv, op, layer, h[:max(rows, 1)] if rows <= 8
+                                   else h, pos, token_count=rows)
+            assert rc == code
+            assert st.as_tuple() == ost.as_tuple()
+
+
+def test_kv_preload_then_decode_long_context():
+    # BASELINE configs[3] shape at a reduced length: preload K/V, decode one.
+    import llm_accel
+    spec = workloads.CONFIG_B
+    n = 300
+    synth = workloads.SyntheticModel(spec, layers=1)
+    oshape = oracle_shape(spec, layers=1, max_seq=n + 8)
+    om = oracle_from_synthetic(synth, oshape)
+    kc, vc = om.new_kv()
+    with llm_accel.Accelerator(accel_shape(spec, layers=1, max_seq=n + 8)) as a:
+        a.load_model(synth)
+        for h in range(spec.kv_heads):
+            k, v = synth.kv_rows(n, seed_offset=10 + h)
+            kc[0, h, :n] = k
+            vc[0, h, :n] = v
+            a.kv_write(0, h, 0, k, v)
+        x = synth.hidden_rows(1)
+        a.upload(2, x)
+        _say(f"case preload n={n}")
+        a.task(18, 0, 1, n, 2, 0)
+        got = a.download(0, 1)
+    code, want, _ = om.task((kc, vc), 18, 0, x, n)
+    assert first_mismatch(got, want) is None
