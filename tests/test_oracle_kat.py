@@ -1,0 +1,183 @@
+"""The oracle against the reference's published known-answer values
+(tests/golden/kat.json, transcribed from the reference's result logs)."""
+import json
+import os
+import shutil
+import subprocess
+import tempfile
+
+import numpy as np
+import pytest
+
+from oracle import orc
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+KAT = json.load(open(os.path.join(HERE, "golden", "kat.json")))
+
+
+@pytest.fixture(autouse=True)
+def _floor_tables():
+    orc.set_exp_policy(orc.EXP_FLOOR, orc.EXP_FLOOR)
+    yield
+
+
+def test_mt19937_10000th_output():
+    # C++ [rand.predef]: the 10000th consecutive invocation of a
+    # default-constructed mt19937 produces 4123659995.
+    assert orc.lib.orc_mt19937_nth(5489, 10000) == 4123659995
+
+
+@pytest.mark.skipif(shutil.which("g++") is None, reason="needs g++")
+def test_uniform_int_lemire_matches_this_libstdcxx():
+    """This container's libstdc++ (GCC >= 11) implements
+    uniform_int_distribution with Lemire's method; the oracle's restatement
+    of that variant must reproduce it draw for draw."""
+    import ctypes
+    ver = subprocess.run(["g++", "-dumpversion"], capture_output=True,
+                         text=True).stdout.strip()
+    if int(ver.split(".")[0]) < 11:
+        pytest.skip("libstdc++ older than 11 uses divide-and-reject")
+    for lo, hi in ((-128, 128), (224, 288), (-64, 64), (-48, 48)):
+        src = (
+            "#include <random>\n#include <cstdio>\n"
+            "int main() { std::mt19937 g(20260718);"
+            " std::uniform_int_distribution<int> a(%d, %d);"
+            " for (int i = 0; i < 5000; i++) std::printf(\"%%d\\n\", a(g)); }\n"
+            % (lo, hi))
+        with tempfile.TemporaryDirectory() as d:
+            exe = os.path.join(d, "u")
+            open(exe + ".cpp", "w").write(src)
+            subprocess.run(["g++", "-O1", "-o", exe, exe + ".cpp"], check=True)
+            out = subprocess.run([exe], check=True, capture_output=True,
+                                 text=True)
+        ref = np.array(out.stdout.split(), dtype=np.int32)
+        buf = (ctypes.c_int32 * 5000)()
+        orc.lib.orc_uniform_ints(20260718, lo, hi, orc.UID_LEMIRE, 5000, buf)
+        assert np.array_equal(np.frombuffer(buf, np.int32), ref), (lo, hi)
+
+
+_kat1_cache = {}
+
+
+def _kat1(rows, uid=orc.UID_DIVREJ):
+    key = (rows, uid)
+    if key not in _kat1_cache:
+        k = KAT["kat1_qwen_layer_p8"]
+        m = orc.Model(orc.profile("qwen-layer"), 1, True)
+        m.init_reference_random(k["seed"], uid)
+        h = orc.make_random_tensor(rows, 2048, k["seed"] ^ k["hidden_seed_xor"],
+                                   -48, 48, uid)
+        post_p, out_p = m.prefill_sequence(h, 0, orc.SEM_RAW_PAYLOAD)
+        post_d, out_d = m.prefill_sequence(h, 0, orc.SEM_DIRECT)
+        post_l, _ = m.prefill_sequence(h, 0, orc.SEM_LEGACY_Q8_8)
+        fin_p = orc.rmsnorm(out_p, m.norms()[2])
+        fin_d = orc.rmsnorm(out_d, m.norms()[2])
+        _kat1_cache[key] = dict(post_p=post_p, post_d=post_d, post_l=post_l,
+                                out_p=out_p, out_d=out_d, fin_p=fin_p,
+                                fin_d=fin_d)
+    return _kat1_cache[key]
+
+
+def _fingerprint(a, b):
+    idx = np.argwhere(a != b)
+    first = [[int(r), int(c), int(a[r, c]), int(b[r, c])] for r, c in idx[:4]]
+    return len(idx), int(np.abs(a.astype(int) - b).max()), first
+
+
+def test_kat1_post_attention_fingerprint():
+    """Q2.14 raw-payload vs direct-multiply attention, P8 at the Qwen layer
+    shape: count, max error and the first four mismatches of the reference
+    log.  Pins the Q2.14 exp table, the tile recurrence, QK/PV banking,
+    RoPE, projections and the reference random model."""
+    k = KAT["kat1_qwen_layer_p8"]
+    r = _kat1(8)
+    n, mx, first = _fingerprint(r["post_p"], r["post_d"])
+    assert (n, mx, first) == (k["post_attention_mismatches"],
+                              k["post_attention_max_error"],
+                              k["post_attention_first"])
+
+
+def test_kat1_distribution_variant_is_pinned():
+    # Lemire draws (libstdc++ >= 11) give 118 post-attention mismatches, the
+    # divide-and-reject draws of the reference's GCC 9 host give 117.
+    r = _kat1(8, orc.UID_LEMIRE)
+    n, _, _ = _fingerprint(r["post_p"], r["post_d"])
+    assert n != KAT["kat1_qwen_layer_p8"]["post_attention_mismatches"]
+
+
+def test_kat1_p2_bit_identical_and_saturated_probes():
+    k = KAT["kat1_qwen_layer_p2"]
+    r = _kat1(2)
+    assert np.array_equal(r["post_p"], r["post_d"])
+    assert np.array_equal(r["out_p"], r["out_d"])
+    probes = [int(r["fin_p"][k["final_probe_row"], c]) for c in k["final_probe_cols"]]
+    assert probes == k["final_probe_raw_payload"]
+
+
+def test_p2_legacy_q8_8_attention_fingerprint():
+    """Q2.14 production vs legacy Q8.8-probability attention, row 1 of the
+    P2 block: pins the Q8.8 exp table at the entries that path uses."""
+    k = KAT["p2_legacy_q8_8_attention"]
+    r = _kat1(2)
+    a = r["post_p"][1:2]
+    b = r["post_l"][1:2]
+    n, mx, first = _fingerprint(a, b)
+    assert np.array_equal(r["post_p"][0], r["post_l"][0])
+    assert (n, mx, first) == (k["mismatches"], k["max_error"], k["first"])
+
+
+def test_kat1_silu_pinned_probes():
+    # Probes whose value does not move with the unpinned hls::exp<16,8>
+    # entries of SiLU.
+    k = KAT["kat1_qwen_layer_p8"]
+    r = _kat1(8)
+    row = k["final_probe_row"]
+    got_p = [int(r["fin_p"][row, c]) for c in k["final_probe_cols"]]
+    got_d = [int(r["fin_d"][row, c]) for c in k["final_probe_cols"]]
+    assert got_p[0] == k["final_probe_raw_payload"][0]
+    assert got_p[3] == k["final_probe_raw_payload"][3]
+    assert got_d[0] == k["final_probe_direct"][0]
+    assert got_d[3] == k["final_probe_direct"][3]
+
+
+@pytest.mark.xfail(strict=True, reason="parity unpinned: hls::exp<16,8> (SiLU) "
+                   "is not floor(e^x*256) at every entry; the HLS math library "
+                   "is not available to pin it")
+def test_kat1_post_ffn_fingerprint():
+    k = KAT["kat1_qwen_layer_p8"]
+    r = _kat1(8)
+    n, mx, first = _fingerprint(r["out_p"], r["out_d"])
+    assert (n, mx, first) == (k["post_ffn_mismatches"], k["post_ffn_max_error"],
+                              k["post_ffn_first"])
+
+
+def _run_generate(layers):
+    m = orc.Model(orc.profile("qwen2.5-3b"), layers, True)
+    m.init_reference_random(20260718, orc.UID_DIVREJ)
+    emb = m.embedding()
+    kv = m.new_kv()
+    h = emb[0:8].copy()
+    for layer in range(layers):
+        _, h, _ = m.task(kv, 18, layer, h, 0)
+        _, h, _ = m.task(kv, 19, layer, h, 0)
+    _, fin, _ = m.task(kv, 20, 0, h, 0)
+    tok0 = orc.lm_head_argmax(emb, fin[7])
+    h = emb[tok0:tok0 + 1].copy()
+    for layer in range(layers):
+        _, h, _ = m.task(kv, 18, layer, h, 8)
+        _, h, _ = m.task(kv, 19, layer, h, 8)
+    _, fin1, _ = m.task(kv, 20, 0, h, 8)
+    tok1 = orc.lm_head_argmax(emb, fin1[0])
+    return [tok0, tok1], fin
+
+
+@pytest.mark.slow
+def test_kat2_qwen3b_one_layer_tokens():
+    toks, _ = _run_generate(1)
+    assert toks == KAT["kat2_qwen3b_l1"]["generated"]
+
+
+@pytest.mark.slow
+def test_kat3_qwen3b_two_layer_tokens():
+    toks, _ = _run_generate(2)
+    assert toks == KAT["kat3_qwen3b_l2"]["generated"]
