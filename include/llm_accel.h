@@ -80,7 +80,9 @@ enum {
 
 /* Model shape (model_shape_t, host/host_qwen_8x64.cpp:110-118).
  * Requirements of this build: num_kv_heads >= 1, num_heads % num_kv_heads
- * == 0, head_dim even and <= 128, heads per KV group <= 16. */
+ * == 0, head_dim a multiple of 16 and <= 128, heads per KV group <= 16,
+ * hidden a multiple of 8, intermediate a multiple of 4 (every reference
+ * profile qualifies: host/host_qwen_8x64.cpp:309-343). */
 typedef struct {
     uint32_t vocab_size;
     uint32_t hidden_size;
@@ -175,11 +177,33 @@ void* llm_pair_device_ptr(llm_ctx_t* ctx, uint32_t pair);
 void* llm_stream(llm_ctx_t* ctx);
 int llm_sync(llm_ctx_t* ctx);
 
-/* HIP-event timing on the context stream: record into slot (0..63), and
+/* HIP-event timing on the context stream: record into slot (0..1023), and
  * the elapsed milliseconds between two recorded slots (synchronises). */
 int llm_event_record(llm_ctx_t* ctx, uint32_t slot);
 int llm_event_elapsed_ms(llm_ctx_t* ctx, uint32_t slot_a, uint32_t slot_b,
                          float* ms);
+
+/* Per-kernel timing for measurement: when enabled, every kernel launch of
+ * llm_task is bracketed by HIP events on the context stream; stats sum
+ * the measured durations per kernel kind since the last enable. */
+enum {
+    LLM_K_RMSNORM = 0,   /* attention / FFN / final RMSNorm          */
+    LLM_K_QKV = 1,       /* fused Q | K | V projection                */
+    LLM_K_ROPE = 2,      /* RoPE + KV-cache append                     */
+    LLM_K_ATTENTION = 3, /* tiled online-softmax attention             */
+    LLM_K_OPROJ = 4,     /* O projection + residual                    */
+    LLM_K_GATEUP = 5,    /* gate | up projection + SiLU * up           */
+    LLM_K_DOWN = 6,      /* down projection + residual                 */
+    LLM_K_COUNT = 7
+};
+int llm_kernel_timing(llm_ctx_t* ctx, int enable);
+int llm_kernel_stats(llm_ctx_t* ctx, uint32_t kernel, uint64_t* launches,
+                     double* total_ms);
+
+/* A plain device-to-device copy of `bytes` repeated `iters` times on the
+ * context stream (calibration reference for HBM counters and achievable
+ * bandwidth); *ms is the average duration of one copy. */
+int llm_bench_copy(llm_ctx_t* ctx, uint64_t bytes, uint32_t iters, float* ms);
 
 /* The two exp tables the kernels use, 2049 entries for x = -8 .. 0 in
  * Q8.8 steps: q8_8 = floor(e^x * 256) (SiLU), q2_14 = floor(e^x * 16384)

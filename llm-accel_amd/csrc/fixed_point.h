@@ -99,8 +99,11 @@ FX_HD int16_t fx_silu(int32_t x, const int16_t* e8) {
 }
 
 // fm(accum(1) / max(sum, 2^-12)) (host:3726-3730, ctrl:4093-4099): the
-// ap_fixed quotient truncates at 16 fraction bits, then AP_RND to Q8.8.
+// ap_fixed quotient floor(2^32 / b) (16 fraction bits) rounded to Q8.8 is
+// floor(2^24 / b + 1/2) = floor((2^25 + b) / (2b)), which saturates for
+// b <= 512 and otherwise fits 32-bit unsigned division.
 FX_HD int16_t fx_inv_sum(int32_t sum) {
-    int64_t b = sum < 16 ? 16 : sum;
-    return fx_sat16(fx_rnd(((int64_t)1 << 32) / b, 8));
+    const uint32_t b = sum < 16 ? 16u : (uint32_t)sum;
+    if (b <= 512) return INT16_MAX;
+    return (int16_t)(((1u << 25) + b) / (2u * b));
 }

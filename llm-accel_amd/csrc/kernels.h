@@ -26,44 +26,22 @@ struct ProjArgs {
     uint32_t n;         // valid output columns
     uint32_t rows;      // active rows (1..8)
     const int16_t* exp8;  // Q8.8 exp table, x = -2048..0 (EPI_SILU)
+    // EPI_RESID only, optional: RMSNorm of the output rows with a constant
+    // gain (norm_out[r][n] = rnd(out * gain * gamma[n], 16)).
+    int16_t* norm_out;
+    uint32_t ldn;
+    const int16_t* norm_gamma;
+    int32_t norm_gain;
 };
 
-struct RopeArgs {
-    const int16_t* qkv;  // [rows][ldqkv]: q | k | v projections
-    uint32_t ldqkv;
-    int16_t* q;          // rotated q [rows][ldq]
-    uint32_t ldq;
-    int16_t* kcache;     // page pool [pages][64][head_dim]
-    int16_t* vcache;
-    const int32_t* page_table;  // this layer: [kv_heads][tiles]
-    uint32_t tiles;
-    const int16_t* rope;  // [max_seq][head_dim] = cos d/2 | sin d/2
-    uint32_t pos0;
-    uint32_t num_heads, num_kv_heads, head_dim;
-};
-
-struct AttnArgs {
-    const int16_t* q;  // rotated q [rows][ldq]
-    uint32_t ldq;
-    const int16_t* kcache;
-    const int16_t* vcache;
-    const int32_t* page_table;  // this layer: [kv_heads][tiles]
-    uint32_t tiles;
-    uint32_t pos0;
-    uint32_t group, head_dim;
-    int32_t qk_scale;      // fm(1/sqrt(head_dim)) raw
-    const int16_t* exp14;  // Q2.14 exp table, x = -2048..0
-    int16_t* out;          // [rows][ldo]
-    uint32_t ldo;
-};
-
+hipError_t launch_copy(const uint4* src, uint4* dst, size_t n16,
+                       hipStream_t st);
 hipError_t launch_proj(const ProjArgs& a, int epi, int L, uint32_t blocks,
                        hipStream_t st);
+// RMSNorm of `rows` rows; const_gain > 0 selects the elementwise kernel
+// (the gain does not depend on the data when hidden >= 128).
 hipError_t launch_rmsnorm(const int16_t* x, uint32_t ldx, const int16_t* gamma,
                           uint32_t cols, int16_t* y, uint32_t ldy, uint32_t rows,
-                          hipStream_t st);
-hipError_t launch_rope_append(const RopeArgs& a, uint32_t rows, hipStream_t st);
-hipError_t launch_attention(const AttnArgs& a, uint32_t rows, uint32_t kv_heads,
-                            hipStream_t st);
+                          int32_t const_gain, hipStream_t st);
 
 }  // namespace llm

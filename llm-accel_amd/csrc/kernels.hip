@@ -8,8 +8,6 @@
 //            [4 rows][16 lanes][8 columns].  One wavefront load of 16 B per
 //            lane reads one contiguous 1 KiB step of a block.  N is padded
 //            to a multiple of 4 and K to a multiple of 128 with zeros.
-//   KV cache pages of 64 positions (one attention tile) x head_dim int16,
-//            addressed through a page table [layer][kv_head][tile].
 #include "kernels.h"
 
 #include "fixed_point.h"
@@ -54,6 +52,18 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(
     int16_t* yr = y + (size_t)blockIdx.x * ldy;
     for (uint32_t c = threadIdx.x; c < cols; c += 256)
         yr[c] = fx_sat16(fx_rnd((int64_t)xr[c] * g * gamma[c], 16));
+}
+
+// Constant-gain RMSNorm: one thread per element.
+__global__ __launch_bounds__(256) void rmsnorm_const_kernel(
+    const int16_t* __restrict__ x, uint32_t ldx,
+    const int16_t* __restrict__ gamma, uint32_t cols, int16_t* __restrict__ y,
+    uint32_t ldy, uint32_t total, int32_t gain) {
+    const uint32_t idx = blockIdx.x * 256 + threadIdx.x;
+    if (idx >= total) return;
+    const uint32_t r = idx / cols, c = idx % cols;
+    y[(size_t)r * ldy + c] =
+        fx_sat16(fx_rnd((int64_t)x[(size_t)r * ldx + c] * gain * gamma[c], 16));
 }
 
 // ---------------------------------------------------------------------
@@ -160,6 +170,9 @@ __global__ __launch_bounds__(256) void proj_kernel(ProjArgs a) {
             int16_t y = fx_narrow_projection(tot[0]);
             if (EPI == EPI_RESID) {
                 y = fx_sat16((int32_t)y + a.res[(size_t)r * a.ldr + n]);
+                if (a.norm_out)
+                    a.norm_out[(size_t)r * a.ldn + n] = fx_sat16(fx_rnd(
+                        (int64_t)y * a.norm_gain * a.norm_gamma[n], 16));
             } else if (EPI == EPI_SILU) {
                 int16_t up = fx_narrow_projection(tot[NM - 1]);
                 int16_t sg = fx_silu(y, a.exp8);
@@ -171,154 +184,14 @@ __global__ __launch_bounds__(256) void proj_kernel(ProjArgs a) {
 }
 
 // ---------------------------------------------------------------------
-// RoPE on Q and K, append K (rotated) and V to the paged cache.  One
-// workgroup per active row t at absolute position pos0 + t.
+// Plain copy (calibration reference for HBM counters).
 // ---------------------------------------------------------------------
-__global__ __launch_bounds__(256) void rope_append_kernel(RopeArgs a) {
-    const uint32_t t = blockIdx.x, pos = a.pos0 + t;
-    const uint32_t d = a.head_dim, half = d / 2;
-    const int16_t* rope = a.rope + (size_t)pos * d;
-    const int16_t* row = a.qkv + (size_t)t * a.ldqkv;
-    const uint32_t tile = pos / 64, slot = pos % 64;
-    for (uint32_t idx = threadIdx.x; idx < a.num_heads * half; idx += 256) {
-        const uint32_t h = idx / half, e = idx % half;
-        const int32_t x0 = row[h * d + e], x1 = row[h * d + half + e];
-        const int32_t c = rope[e], s = rope[half + e];
-        int16_t* qo = a.q + (size_t)t * a.ldq + h * d;
-        qo[e] = fx_sat16(fx_rnd((int64_t)x0 * c - (int64_t)x1 * s, 8));
-        qo[half + e] = fx_sat16(fx_rnd((int64_t)x1 * c + (int64_t)x0 * s, 8));
-    }
-    const int16_t* krow = row + a.num_heads * d;
-    const int16_t* vrow = krow + a.num_kv_heads * d;
-    for (uint32_t idx = threadIdx.x; idx < a.num_kv_heads * half; idx += 256) {
-        const uint32_t h = idx / half, e = idx % half;
-        const int32_t x0 = krow[h * d + e], x1 = krow[h * d + half + e];
-        const int32_t c = rope[e], s = rope[half + e];
-        const int32_t page = a.page_table[h * a.tiles + tile];
-        int16_t* ko = a.kcache + ((size_t)page * 64 + slot) * d;
-        ko[e] = fx_sat16(fx_rnd((int64_t)x0 * c - (int64_t)x1 * s, 8));
-        ko[half + e] = fx_sat16(fx_rnd((int64_t)x1 * c + (int64_t)x0 * s, 8));
-    }
-    for (uint32_t idx = threadIdx.x; idx < a.num_kv_heads * d; idx += 256) {
-        const uint32_t h = idx / d, e = idx % d;
-        const int32_t page = a.page_table[h * a.tiles + tile];
-        a.vcache[((size_t)page * 64 + slot) * d + e] = vrow[h * d + e];
-    }
-}
-
-// ---------------------------------------------------------------------
-// Tiled online-softmax attention, one workgroup per (active row, KV head):
-// the GQA group's G query heads share every K/V tile staged in LDS.
-// Arithmetic: golden_tiled_flash_attention_q2_14 (raw payload), host
-// :3609-3738 == controller :5491-5765.
-// ---------------------------------------------------------------------
-__global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
-    constexpr int MAXG = 16, MAXD = 128, TILE = 64;
-    const uint32_t t = blockIdx.x, h = blockIdx.y;
-    const uint32_t G = a.group, d = a.head_dim, Gd = G * d;
-    const uint32_t n = a.pos0 + t + 1;
-    __shared__ int16_t qs[MAXG * MAXD];
-    __shared__ int16_t ks[TILE * MAXD];
-    __shared__ int16_t vs[TILE * MAXD];
-    __shared__ int16_t sc[MAXG * TILE];
-    __shared__ int16_t pr[MAXG * TILE];
-    __shared__ int16_t mx[MAXG];
-    __shared__ int32_t sm[MAXG];
-    __shared__ int32_t old[MAXG];
-
-    const int16_t* qsrc = a.q + (size_t)t * a.ldq + (size_t)h * Gd;
-    for (uint32_t idx = threadIdx.x; idx < Gd; idx += 256) qs[idx] = qsrc[idx];
-    if (threadIdx.x < G) {
-        mx[threadIdx.x] = INT16_MIN;  // fm(-128)
-        sm[threadIdx.x] = 0;
-    }
-    int32_t acc[MAXG * MAXD / 256];
-#pragma unroll
-    for (int k = 0; k < MAXG * MAXD / 256; k++) acc[k] = 0;
-    const int64_t scale = (int64_t)a.qk_scale << 8;  // accum(fm(1/sqrt d))
-
-    for (uint32_t tb = 0, tile = 0; tb < n; tb += TILE, tile++) {
-        const uint32_t tl = n - tb < TILE ? n - tb : TILE;
-        const int32_t page = a.page_table[h * a.tiles + tile];
-        const int16_t* kp = a.kcache + (size_t)page * TILE * d;
-        const int16_t* vp = a.vcache + (size_t)page * TILE * d;
-        __syncthreads();
-        for (uint32_t idx = threadIdx.x; idx < tl * d; idx += 256) {
-            ks[idx] = kp[idx];
-            vs[idx] = vp[idx];
-        }
-        __syncthreads();
-        // QK scores: four k-mod-4 banks of AP_RND(Q8.8 x Q4.12) products.
-        // d <= 128 gives <= 32 terms per bank, so only a bank's final sum
-        // can leave the Q16.16 range; clamping the exact sum is therefore
-        // the same as saturating every accumulation.
-        for (uint32_t idx = threadIdx.x; idx < G * TILE; idx += 256) {
-            const uint32_t g = idx / TILE, p = idx % TILE;
-            if (p >= tl) continue;
-            int64_t bank[4] = {0, 0, 0, 0};
-            for (uint32_t e = 0; e < d; e++) {
-                int32_t w = fx_fm_to_wt(ks[p * d + e]);
-                bank[e & 3] += fx_rnd((int64_t)qs[g * d + e] * w, 4);
-            }
-            int64_t total = (int64_t)fx_sat32(bank[0]) + fx_sat32(bank[1]) +
-                            fx_sat32(bank[2]) + fx_sat32(bank[3]);
-            int32_t tq = fx_sat32(total);
-            tq = fx_sat32(fx_rnd((int64_t)tq * scale, 16));
-            sc[g * TILE + p] = fx_sat16(fx_rnd(tq, 8));
-        }
-        __syncthreads();
-        // Online softmax state per query head (Q2.14 probabilities).
-        if (threadIdx.x < G) {
-            const uint32_t g = threadIdx.x;
-            int32_t m = mx[g];
-            for (uint32_t p = 0; p < tl; p++)
-                m = sc[g * TILE + p] > m ? sc[g * TILE + p] : m;
-            int32_t diff = fx_sat16((int32_t)mx[g] - m);
-            diff = diff < -2048 ? -2048 : diff;
-            const int64_t o = (int64_t)a.exp14[diff + 2048] << 2;
-            int64_t tsum = 0;
-            for (uint32_t p = 0; p < tl; p++) {
-                int32_t x = fx_sat16((int32_t)sc[g * TILE + p] - m);
-                x = x < -2048 ? -2048 : x;
-                int16_t pv = a.exp14[x + 2048];
-                pr[g * TILE + p] = pv;
-                tsum += (int64_t)pv << 2;
-            }
-            sm[g] = fx_sat32(fx_rnd((int64_t)sm[g] * o + (tsum << 16), 16));
-            mx[g] = (int16_t)m;
-            old[g] = (int32_t)o;
-        }
-        __syncthreads();
-        // Rescale accumulators, then add this tile's PV (payload = Q2.14
-        // bits read as Q8.8, x fm(1/64), narrowed to Q8.8 per tile).
-#pragma unroll
-        for (int k = 0; k < MAXG * MAXD / 256; k++) {
-            const uint32_t idx = threadIdx.x + 256 * k;
-            if (idx >= Gd) break;
-            const uint32_t g = idx / d, e = idx % d;
-            int32_t av = fx_sat32(fx_rnd((int64_t)acc[k] * old[g], 16));
-            int64_t bank[4] = {0, 0, 0, 0};
-            for (uint32_t p = 0; p < tl; p++) {
-                int32_t w = fx_fm_to_wt(vs[p * d + e]);
-                bank[p & 3] += fx_rnd((int64_t)pr[g * TILE + p] * w, 4);
-            }
-            int32_t tot = fx_sat32((int64_t)fx_sat32(bank[0]) + fx_sat32(bank[1]) +
-                                   fx_sat32(bank[2]) + fx_sat32(bank[3]));
-            tot = fx_sat32(fx_rnd((int64_t)tot * 1024, 16));
-            const int32_t tv = fx_sat16(fx_rnd(tot, 8));
-            acc[k] = fx_sat32((int64_t)av + ((int64_t)tv << 8));
-        }
-    }
-    __syncthreads();
-    int16_t* dst = a.out + (size_t)t * a.ldo + (size_t)h * Gd;
-#pragma unroll
-    for (int k = 0; k < MAXG * MAXD / 256; k++) {
-        const uint32_t idx = threadIdx.x + 256 * k;
-        if (idx >= Gd) break;
-        const uint32_t g = idx / d;
-        const int64_t inv = fx_inv_sum(sm[g]);
-        dst[idx] = fx_sat16(fx_rnd((int64_t)acc[k] * inv, 16));
-    }
+__global__ __launch_bounds__(256) void copy_kernel(const uint4* __restrict__ src,
+                                                   uint4* __restrict__ dst,
+                                                   size_t n16) {
+    for (size_t i = blockIdx.x * 256ull + threadIdx.x; i < n16;
+         i += (size_t)gridDim.x * 256)
+        dst[i] = src[i];
 }
 
 // ---------------------------------------------------------------------
@@ -355,21 +228,22 @@ hipError_t launch_proj(const ProjArgs& a, int epi, int L, uint32_t blocks,
     }
 }
 
+hipError_t launch_copy(const uint4* src, uint4* dst, size_t n16,
+                       hipStream_t st) {
+    copy_kernel<<<2048, 256, 0, st>>>(src, dst, n16);
+    return hipGetLastError();
+}
+
 hipError_t launch_rmsnorm(const int16_t* x, uint32_t ldx, const int16_t* gamma,
                           uint32_t cols, int16_t* y, uint32_t ldy, uint32_t rows,
-                          hipStream_t st) {
-    rmsnorm_kernel<<<rows, 256, 0, st>>>(x, ldx, gamma, cols, y, ldy);
-    return hipGetLastError();
-}
-
-hipError_t launch_rope_append(const RopeArgs& a, uint32_t rows, hipStream_t st) {
-    rope_append_kernel<<<rows, 256, 0, st>>>(a);
-    return hipGetLastError();
-}
-
-hipError_t launch_attention(const AttnArgs& a, uint32_t rows, uint32_t kv_heads,
-                            hipStream_t st) {
-    attention_kernel<<<dim3(rows, kv_heads), 256, 0, st>>>(a);
+                          int32_t const_gain, hipStream_t st) {
+    if (const_gain > 0) {
+        const uint32_t total = rows * cols;
+        rmsnorm_const_kernel<<<(total + 255) / 256, 256, 0, st>>>(
+            x, ldx, gamma, cols, y, ldy, total, const_gain);
+    } else {
+        rmsnorm_kernel<<<rows, 256, 0, st>>>(x, ldx, gamma, cols, y, ldy);
+    }
     return hipGetLastError();
 }
 

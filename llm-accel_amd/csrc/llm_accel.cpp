@@ -17,6 +17,8 @@
 #include <string>
 #include <vector>
 
+#include "attention.h"
+#include "fixed_point.h"
 #include "kernels.h"
 
 namespace {
@@ -85,18 +87,82 @@ struct llm_ctx {
     int32_t* page_table = nullptr;     // [layer][kv_head][tile]
     std::vector<int32_t> host_pages;
     std::vector<int16_t*> pairs;       // [8][Hp]
-    int16_t* xn = nullptr;             // [8][Hp]
+    int16_t* xn_attn = nullptr;        // [8][Hp] attention-norm output
+    int16_t* xn_ffn = nullptr;         // [8][Hp] FFN-norm output
     int16_t* qkv = nullptr;            // [8][Nqkv]
-    int16_t* q = nullptr;              // [8][H]
     int16_t* attn = nullptr;           // [8][Hp]
     int16_t* act = nullptr;            // [8][Ip]
+    // attention split-path scratch
+    uint32_t chunk_tiles = 2;
+    int16_t* s_scores = nullptr;
+    int16_t* s_tmax = nullptr;
+    int32_t* s_tsum = nullptr;
+    int16_t* s_tval = nullptr;
+    uint32_t* counters = nullptr;
+    // RMSNorm gain: > 0 when it is the same for every row (hidden >= 128:
+    // fm_t(hidden) saturates, recip() returns 0, the mean square is 0 and
+    // the gain is rsqrt(0)); 0 selects the per-row reduction.
+    int32_t const_gain = 0;
+    // Normalised copies of a pair computed in a producing epilogue: valid
+    // while that pair is not written again.  pair < 0 means empty.
+    struct NormCache { int pair = -1; uint32_t layer = 0; };
+    NormCache attn_cache, ffn_cache;
     std::vector<void*> allocations;
     std::vector<hipEvent_t> events;
+    // per-launch timing (measurement only)
+    bool timing = false;
+    std::vector<hipEvent_t> ev_pool;
+    struct Timed { int kid; hipEvent_t a, b; };
+    std::vector<Timed> pending;
+    double kernel_ms[LLM_K_COUNT] = {};
+    uint64_t kernel_n[LLM_K_COUNT] = {};
 
     Matrix& mat(uint32_t layer, int m) { return mats[layer * M_COUNT + m]; }
 };
 
 namespace {
+
+// Brackets one kernel launch with events when timing is enabled.
+struct TimedScope {
+    llm_ctx* c;
+    int kid;
+    hipEvent_t a = nullptr;
+    TimedScope(llm_ctx* ctx, int k) : c(ctx), kid(k) {
+        if (!c->timing) return;
+        a = take();
+        (void)hipEventRecord(a, c->stream);
+    }
+    ~TimedScope() {
+        if (!c->timing || !a) return;
+        hipEvent_t b = take();
+        (void)hipEventRecord(b, c->stream);
+        c->pending.push_back({kid, a, b});
+    }
+    hipEvent_t take() {
+        if (c->ev_pool.empty()) {
+            hipEvent_t e;
+            (void)hipEventCreate(&e);
+            return e;
+        }
+        hipEvent_t e = c->ev_pool.back();
+        c->ev_pool.pop_back();
+        return e;
+    }
+};
+
+void harvest_timing(llm_ctx* c) {
+    (void)hipStreamSynchronize(c->stream);
+    for (auto& t : c->pending) {
+        float ms = 0;
+        if (hipEventElapsedTime(&ms, t.a, t.b) == hipSuccess) {
+            c->kernel_ms[t.kid] += ms;
+            c->kernel_n[t.kid] += 1;
+        }
+        c->ev_pool.push_back(t.a);
+        c->ev_pool.push_back(t.b);
+    }
+    c->pending.clear();
+}
 
 int dev_alloc(llm_ctx* c, void** p, size_t bytes) {
     hipError_t e = hipMalloc(p, bytes);
@@ -205,6 +271,13 @@ void fill_counters(const llm_ctx* c, uint32_t op, uint32_t R, uint32_t pos,
     st->completed_packets = pk;
 }
 
+// A write to `pair` (task output, upload, device-pointer hand-out) drops
+// every normalised copy derived from it.
+void invalidate_pair(llm_ctx* c, int pair) {
+    if (c->attn_cache.pair == pair) c->attn_cache.pair = -1;
+    if (c->ffn_cache.pair == pair) c->ffn_cache.pair = -1;
+}
+
 int check_layer_loaded(llm_ctx* c, uint32_t layer, bool attn, bool ffn) {
     if (!c->norms_loaded) return fail(LLM_E_STATE, "norm table not loaded");
     for (uint32_t p = 0; p < 7; p++) {
@@ -218,52 +291,65 @@ int check_layer_loaded(llm_ctx* c, uint32_t layer, bool attn, bool ffn) {
 }
 
 int enqueue_attention_sublayer(llm_ctx* c, uint32_t layer, uint32_t R,
-                               uint32_t pos, const int16_t* in, int16_t* out) {
+                               uint32_t pos, int in_pair, int out_pair) {
     hipStream_t st = c->stream;
-    HIP_TRY(llm::launch_rmsnorm(in, c->Hp, c->norms + (size_t)(2 * layer) * c->H,
-                                c->H, c->xn, c->Hp, R, st));
+    const int16_t* in = c->pairs[in_pair];
+    int16_t* out = c->pairs[out_pair];
+    const bool cached = c->const_gain > 0 && c->attn_cache.pair == in_pair &&
+                        c->attn_cache.layer == layer;
+    if (!cached) {
+        TimedScope ts(c, LLM_K_RMSNORM);
+        HIP_TRY(llm::launch_rmsnorm(in, c->Hp,
+                                    c->norms + (size_t)(2 * layer) * c->H, c->H,
+                                    c->xn_attn, c->Hp, R, c->const_gain, st));
+    }
     const Matrix& mq = c->mat(layer, M_QKV);
     llm::ProjArgs a{};
     a.w0 = mq.d;
     a.steps = mq.steps;
-    a.x = c->xn;
+    a.x = c->xn_attn;
     a.ldx = c->Hp;
     a.out = c->qkv;
     a.ldo = c->Nqkv;
     a.n = mq.n;
     a.rows = R;
-    HIP_TRY(llm::launch_proj(a, llm::EPI_STORE, mq.L, mq.n_pad / 4, st));
-    const int32_t* pt = c->page_table + (size_t)layer * c->Hkv * c->tiles;
-    llm::RopeArgs r{};
-    r.qkv = c->qkv;
-    r.ldqkv = c->Nqkv;
-    r.q = c->q;
-    r.ldq = c->H;
-    r.kcache = c->kcache;
-    r.vcache = c->vcache;
-    r.page_table = pt;
-    r.tiles = c->tiles;
-    r.rope = c->rope;
-    r.pos0 = pos;
-    r.num_heads = c->Hq;
-    r.num_kv_heads = c->Hkv;
-    r.head_dim = c->d;
-    HIP_TRY(llm::launch_rope_append(r, R, st));
+    {
+        TimedScope ts(c, LLM_K_QKV);
+        HIP_TRY(llm::launch_proj(a, llm::EPI_STORE, mq.L, mq.n_pad / 4, st));
+    }
     llm::AttnArgs at{};
-    at.q = c->q;
-    at.ldq = c->H;
+    at.qkv = c->qkv;
+    at.ldqkv = c->Nqkv;
+    at.rope = c->rope;
     at.kcache = c->kcache;
     at.vcache = c->vcache;
-    at.page_table = pt;
+    at.page_table = c->page_table + (size_t)layer * c->Hkv * c->tiles;
     at.tiles = c->tiles;
     at.pos0 = pos;
+    at.num_heads = c->Hq;
+    at.num_kv_heads = c->Hkv;
     at.group = c->G;
     at.head_dim = c->d;
     at.qk_scale = c->qk_scale;
     at.exp14 = c->exp14;
     at.out = c->attn;
     at.ldo = c->Hp;
-    HIP_TRY(llm::launch_attention(at, R, c->Hkv, st));
+    at.chunk_tiles = c->chunk_tiles;
+    at.max_tiles = c->tiles;
+    at.s_scores = c->s_scores;
+    at.s_tmax = c->s_tmax;
+    at.s_tsum = c->s_tsum;
+    at.s_tval = c->s_tval;
+    at.counters = c->counters;
+    const uint32_t last_tiles = (uint32_t)cdiv(pos + R, llm::kTile);
+    static_assert(llm::kTile == 64, "attention tiles are 64 positions");
+    if (c->chunk_tiles == 0 || c->chunk_tiles > 64)  // page-index span in LDS
+        return fail(LLM_E_STATE, "attention chunk must be 1..64 tiles");
+    const uint32_t chunks = (uint32_t)cdiv(last_tiles, c->chunk_tiles);
+    {
+        TimedScope ts(c, LLM_K_ATTENTION);
+        HIP_TRY(llm::launch_attention(at, R, c->Hkv, chunks, st));
+    }
     const Matrix& mo = c->mat(layer, M_O);
     llm::ProjArgs o{};
     o.w0 = mo.d;
@@ -276,31 +362,52 @@ int enqueue_attention_sublayer(llm_ctx* c, uint32_t layer, uint32_t R,
     o.ldr = c->Hp;
     o.n = mo.n;
     o.rows = R;
-    HIP_TRY(llm::launch_proj(o, llm::EPI_RESID, mo.L, mo.n_pad / 4, st));
+    if (c->const_gain > 0) {  // FFN norm of this sublayer's output
+        o.norm_out = c->xn_ffn;
+        o.ldn = c->Hp;
+        o.norm_gamma = c->norms + (size_t)(2 * layer + 1) * c->H;
+        o.norm_gain = c->const_gain;
+    }
+    {
+        TimedScope ts(c, LLM_K_OPROJ);
+        HIP_TRY(llm::launch_proj(o, llm::EPI_RESID, mo.L, mo.n_pad / 4, st));
+    }
+    invalidate_pair(c, out_pair);
+    if (c->const_gain > 0) c->ffn_cache = {out_pair, layer};
     return 0;
 }
 
-int enqueue_ffn_sublayer(llm_ctx* c, uint32_t layer, uint32_t R,
-                         const int16_t* in, int16_t* out) {
+int enqueue_ffn_sublayer(llm_ctx* c, uint32_t layer, uint32_t R, int in_pair,
+                         int out_pair) {
     hipStream_t st = c->stream;
-    HIP_TRY(llm::launch_rmsnorm(in, c->Hp,
-                                c->norms + (size_t)(2 * layer + 1) * c->H,
-                                c->H, c->xn, c->Hp, R, st));
+    const int16_t* in = c->pairs[in_pair];
+    int16_t* out = c->pairs[out_pair];
+    const bool cached = c->const_gain > 0 && c->ffn_cache.pair == in_pair &&
+                        c->ffn_cache.layer == layer;
+    if (!cached) {
+        TimedScope ts(c, LLM_K_RMSNORM);
+        HIP_TRY(llm::launch_rmsnorm(in, c->Hp,
+                                    c->norms + (size_t)(2 * layer + 1) * c->H,
+                                    c->H, c->xn_ffn, c->Hp, R, c->const_gain, st));
+    }
     const Matrix& mg = c->mat(layer, M_GATE);
     const Matrix& mu = c->mat(layer, M_UP);
     llm::ProjArgs a{};
     a.w0 = mg.d;
     a.w1 = mu.d;
     a.steps = mg.steps;
-    a.x = c->xn;
+    a.x = c->xn_ffn;
     a.ldx = c->Hp;
     a.out = c->act;
     a.ldo = c->Ip;
     a.n = mg.n;
     a.rows = R;
     a.exp8 = c->exp8;
-    HIP_TRY(llm::launch_proj(a, llm::EPI_SILU, std::min(mg.L, mu.L) == 0 ? 0 :
-                             std::min(mg.L, mu.L), mg.n_pad / 4, st));
+    {
+        TimedScope ts(c, LLM_K_GATEUP);
+        HIP_TRY(llm::launch_proj(a, llm::EPI_SILU, std::min(mg.L, mu.L),
+                                 mg.n_pad / 4, st));
+    }
     const Matrix& md = c->mat(layer, M_DOWN);
     llm::ProjArgs dn{};
     dn.w0 = md.d;
@@ -313,7 +420,19 @@ int enqueue_ffn_sublayer(llm_ctx* c, uint32_t layer, uint32_t R,
     dn.ldr = c->Hp;
     dn.n = md.n;
     dn.rows = R;
-    HIP_TRY(llm::launch_proj(dn, llm::EPI_RESID, md.L, md.n_pad / 4, st));
+    const bool next = c->const_gain > 0 && layer + 1 < c->L;
+    if (next) {  // attention norm of the next layer
+        dn.norm_out = c->xn_attn;
+        dn.ldn = c->Hp;
+        dn.norm_gamma = c->norms + (size_t)(2 * (layer + 1)) * c->H;
+        dn.norm_gain = c->const_gain;
+    }
+    {
+        TimedScope ts(c, LLM_K_DOWN);
+        HIP_TRY(llm::launch_proj(dn, llm::EPI_RESID, md.L, md.n_pad / 4, st));
+    }
+    invalidate_pair(c, out_pair);
+    if (next) c->attn_cache = {out_pair, layer + 1};
     return 0;
 }
 
@@ -334,10 +453,11 @@ int llm_ctx_create(const llm_shape_t* shape, int device, uint32_t num_pairs,
         return fail(LLM_E_ARG, "inconsistent shape");
     const uint32_t d = s.hidden_size / s.num_heads;
     const uint32_t G = s.num_heads / s.num_kv_heads;
-    if (d % 2 != 0 || d > 128 || G > 16 || G * d > 2048)
-        return fail(LLM_E_ARG, "head_dim must be even and <= 128, group <= 16");
-    if (s.hidden_size % 4 || s.intermediate_size % 4 || (s.num_kv_heads * d) % 4)
-        return fail(LLM_E_ARG, "hidden, intermediate and KV widths must be multiples of 4");
+    if (d % 16 != 0 || d > 128 || G > 16 || G * d > 2048)
+        return fail(LLM_E_ARG,
+                    "head_dim must be a multiple of 16 and <= 128, group <= 16");
+    if (s.hidden_size % 8 || s.intermediate_size % 4)
+        return fail(LLM_E_ARG, "hidden must be a multiple of 8, intermediate of 4");
     if (num_pairs < 2) return fail(LLM_E_ARG, "need at least two hidden pairs");
     int ndev = 0;
     if (hipGetDeviceCount(&ndev) != hipSuccess || ndev == 0)
@@ -401,8 +521,8 @@ int llm_ctx_create(const llm_shape_t* shape, int device, uint32_t num_pairs,
                         (size_t)(2 * c->L + 1) * c->H * sizeof(int16_t))) ||
         (rc = dev_alloc(c, (void**)&c->rope,
                         (size_t)c->max_seq * d * sizeof(int16_t))) ||
-        (rc = dev_alloc(c, (void**)&c->exp8, 2049 * sizeof(int16_t))) ||
-        (rc = dev_alloc(c, (void**)&c->exp14, 2049 * sizeof(int16_t))))
+        (rc = dev_alloc(c, (void**)&c->exp8, 2056 * sizeof(int16_t))) ||
+        (rc = dev_alloc(c, (void**)&c->exp14, 2056 * sizeof(int16_t))))
         return cleanup(rc);
     {
         // aux1 RoPE table exactly as initialize_persistent_auxiliary_data
@@ -443,12 +563,20 @@ int llm_ctx_create(const llm_shape_t* shape, int device, uint32_t num_pairs,
     for (auto& p : c->pairs)
         if ((rc = dev_alloc(c, (void**)&p, (size_t)8 * c->Hp * 2)))
             return cleanup(rc);
-    if ((rc = dev_alloc(c, (void**)&c->xn, (size_t)8 * c->Hp * 2)) ||
+    const size_t rht = (size_t)8 * c->Hkv * c->tiles * c->G;  // rows*heads*tiles*group
+    if ((rc = dev_alloc(c, (void**)&c->xn_attn, (size_t)8 * c->Hp * 2)) ||
+        (rc = dev_alloc(c, (void**)&c->xn_ffn, (size_t)8 * c->Hp * 2)) ||
         (rc = dev_alloc(c, (void**)&c->qkv, (size_t)8 * c->Nqkv * 2)) ||
-        (rc = dev_alloc(c, (void**)&c->q, (size_t)8 * c->H * 2)) ||
         (rc = dev_alloc(c, (void**)&c->attn, (size_t)8 * c->Hp * 2)) ||
-        (rc = dev_alloc(c, (void**)&c->act, (size_t)8 * c->Ip * 2)))
+        (rc = dev_alloc(c, (void**)&c->act, (size_t)8 * c->Ip * 2)) ||
+        (rc = dev_alloc(c, (void**)&c->s_scores, rht * llm::kTile * 2)) ||
+        (rc = dev_alloc(c, (void**)&c->s_tmax, rht * 2)) ||
+        (rc = dev_alloc(c, (void**)&c->s_tsum, rht * 4)) ||
+        (rc = dev_alloc(c, (void**)&c->s_tval, rht * d * 2)) ||
+        (rc = dev_alloc(c, (void**)&c->counters, (size_t)8 * c->Hkv * 4)))
         return cleanup(rc);
+    if (fx_recip(fx_sat16((int64_t)c->H * 256)) == 0)
+        c->const_gain = fx_rmsnorm_gain(0, c->H);
     *out = c;
     return 0;
 }
@@ -458,6 +586,11 @@ void llm_ctx_destroy(llm_ctx_t* c) {
     (void)hipSetDevice(c->device);
     if (c->stream) (void)hipStreamSynchronize(c->stream);
     for (auto e : c->events) (void)hipEventDestroy(e);
+    for (auto e : c->ev_pool) (void)hipEventDestroy(e);
+    for (auto& t : c->pending) {
+        (void)hipEventDestroy(t.a);
+        (void)hipEventDestroy(t.b);
+    }
     for (void* p : c->allocations) (void)hipFree(p);
     if (c->stream) (void)hipStreamDestroy(c->stream);
     delete c;
@@ -550,6 +683,7 @@ int llm_hidden_upload(llm_ctx_t* c, uint32_t pair, const int16_t* rows,
     if (!c || !rows || pair >= c->pairs.size() || n > 8)
         return fail(LLM_E_ARG, "bad hidden upload arguments");
     HIP_TRY(hipSetDevice(c->device));
+    invalidate_pair(c, (int)pair);
     HIP_TRY(hipMemcpy2DAsync(c->pairs[pair], (size_t)c->Hp * 2, rows,
                              (size_t)c->H * 2, (size_t)c->H * 2, n,
                              hipMemcpyHostToDevice, c->stream));
@@ -624,14 +758,20 @@ int llm_task(llm_ctx_t* c, uint32_t op, uint32_t layer, uint32_t token_count,
     if (layer >= c->L) return reject(LLM_STATUS_BAD_LAYER);
     const int16_t* in = c->pairs[in_pair];
     int16_t* out = c->pairs[out_pair];
+    const int ip = (int)in_pair, opr = (int)out_pair;
     if (hipSetDevice(c->device) != hipSuccess)
         return fail(LLM_E_HIP, "hipSetDevice failed");
     if (op == LLM_OP_FINAL_NORM) {
         if (token_count == 0) return reject(LLM_STATUS_BAD_TOKEN_COUNT);
         if (!c->norms_loaded) return fail(LLM_E_STATE, "norm table not loaded");
-        HIP_TRY(llm::launch_rmsnorm(in, c->Hp,
-                                    c->norms + (size_t)(2 * c->L) * c->H, c->H,
-                                    out, c->Hp, token_count, c->stream));
+        {
+            TimedScope ts(c, LLM_K_RMSNORM);
+            HIP_TRY(llm::launch_rmsnorm(in, c->Hp,
+                                        c->norms + (size_t)(2 * c->L) * c->H,
+                                        c->H, out, c->Hp, token_count,
+                                        c->const_gain, c->stream));
+        }
+        invalidate_pair(c, opr);
         fill_counters(c, op, token_count, position, st);
         return LLM_STATUS_OK;
     }
@@ -644,12 +784,12 @@ int llm_task(llm_ctx_t* c, uint32_t op, uint32_t layer, uint32_t token_count,
                                     op != LLM_OP_ATTENTION_SUBLAYER);
         if (rc) return rc;
         if (op == LLM_OP_ATTENTION_SUBLAYER) {
-            rc = enqueue_attention_sublayer(c, layer, token_count, position, in, out);
+            rc = enqueue_attention_sublayer(c, layer, token_count, position, ip, opr);
         } else if (op == LLM_OP_FFN_SUBLAYER) {
-            rc = enqueue_ffn_sublayer(c, layer, token_count, in, out);
+            rc = enqueue_ffn_sublayer(c, layer, token_count, ip, opr);
         } else {
-            rc = enqueue_attention_sublayer(c, layer, token_count, position, in, out);
-            if (rc == 0) rc = enqueue_ffn_sublayer(c, layer, token_count, out, out);
+            rc = enqueue_attention_sublayer(c, layer, token_count, position, ip, opr);
+            if (rc == 0) rc = enqueue_ffn_sublayer(c, layer, token_count, opr, opr);
         }
         if (rc) return rc;
         fill_counters(c, op, token_count, position, st);
@@ -660,24 +800,63 @@ int llm_task(llm_ctx_t* c, uint32_t op, uint32_t layer, uint32_t token_count,
     return reject(LLM_STATUS_BAD_OPERATOR);
 }
 
+}  // extern "C"
+
+namespace {
+
+// Cache pages hold 64 positions of one (layer, KV head): K as rows [64][d]
+// with every row's elements in the bank-paired order [0 4 1 5 2 6 3 7] of
+// each group of 8, V transposed [d][64] with positions in that order.
+uint32_t paired_index(uint32_t e) {
+    static const uint32_t slot[8] = {0, 2, 4, 6, 1, 3, 5, 7};
+    return (e & ~7u) | slot[e & 7u];
+}
+
+// Copy positions [pos0, pos0 + n) between host rows [n][d] and the pages;
+// to_device selects the direction.  Works page by page through a host
+// staging copy of each touched page.
+int kv_transfer(llm_ctx* c, uint32_t layer, uint32_t h, uint32_t pos0,
+                uint32_t n, int16_t* k, int16_t* v, bool to_device) {
+    const uint32_t d = c->d;
+    std::vector<int16_t> page((size_t)64 * d);
+    for (uint32_t p = pos0; p < pos0 + n;) {
+        const uint32_t tile = p / 64, slot0 = p % 64;
+        const uint32_t cnt = std::min(64 - slot0, pos0 + n - p);
+        const size_t pg = c->host_pages[((size_t)layer * c->Hkv + h) * c->tiles + tile];
+        for (int which = 0; which < 2; which++) {
+            int16_t* rows = which == 0 ? k : v;
+            if (!rows) continue;
+            int16_t* dev = (which == 0 ? c->kcache : c->vcache) + pg * 64 * d;
+            HIP_TRY(hipMemcpy(page.data(), dev, page.size() * 2, hipMemcpyDeviceToHost));
+            for (uint32_t s = slot0; s < slot0 + cnt; s++) {
+                int16_t* row = rows + (size_t)(tile * 64 + s - pos0) * d;
+                for (uint32_t e = 0; e < d; e++) {
+                    int16_t& cell = which == 0 ? page[(size_t)s * d + paired_index(e)]
+                                               : page[(size_t)e * 64 + paired_index(s)];
+                    if (to_device) cell = row[e];
+                    else row[e] = cell;
+                }
+            }
+            if (to_device)
+                HIP_TRY(hipMemcpy(dev, page.data(), page.size() * 2,
+                                  hipMemcpyHostToDevice));
+        }
+        p += cnt;
+    }
+    return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
 int llm_kv_read(llm_ctx_t* c, uint32_t layer, uint32_t h, uint32_t pos0,
                 uint32_t n, int16_t* k, int16_t* v) {
     if (!c || layer >= c->L || h >= c->Hkv || pos0 + n > c->max_seq)
         return fail(LLM_E_ARG, "bad KV read arguments");
     HIP_TRY(hipSetDevice(c->device));
     HIP_TRY(hipStreamSynchronize(c->stream));
-    for (uint32_t p = pos0; p < pos0 + n;) {
-        const uint32_t tile = p / 64, slot = p % 64;
-        const uint32_t cnt = std::min(64 - slot, pos0 + n - p);
-        const size_t page = c->host_pages[((size_t)layer * c->Hkv + h) * c->tiles + tile];
-        const size_t off = (page * 64 + slot) * c->d;
-        if (k) HIP_TRY(hipMemcpy(k + (size_t)(p - pos0) * c->d, c->kcache + off,
-                                 (size_t)cnt * c->d * 2, hipMemcpyDeviceToHost));
-        if (v) HIP_TRY(hipMemcpy(v + (size_t)(p - pos0) * c->d, c->vcache + off,
-                                 (size_t)cnt * c->d * 2, hipMemcpyDeviceToHost));
-        p += cnt;
-    }
-    return 0;
+    return kv_transfer(c, layer, h, pos0, n, k, v, false);
 }
 
 int llm_kv_write(llm_ctx_t* c, uint32_t layer, uint32_t h, uint32_t pos0,
@@ -686,18 +865,8 @@ int llm_kv_write(llm_ctx_t* c, uint32_t layer, uint32_t h, uint32_t pos0,
         return fail(LLM_E_ARG, "bad KV write arguments");
     HIP_TRY(hipSetDevice(c->device));
     HIP_TRY(hipStreamSynchronize(c->stream));
-    for (uint32_t p = pos0; p < pos0 + n;) {
-        const uint32_t tile = p / 64, slot = p % 64;
-        const uint32_t cnt = std::min(64 - slot, pos0 + n - p);
-        const size_t page = c->host_pages[((size_t)layer * c->Hkv + h) * c->tiles + tile];
-        const size_t off = (page * 64 + slot) * c->d;
-        if (k) HIP_TRY(hipMemcpy(c->kcache + off, k + (size_t)(p - pos0) * c->d,
-                                 (size_t)cnt * c->d * 2, hipMemcpyHostToDevice));
-        if (v) HIP_TRY(hipMemcpy(c->vcache + off, v + (size_t)(p - pos0) * c->d,
-                                 (size_t)cnt * c->d * 2, hipMemcpyHostToDevice));
-        p += cnt;
-    }
-    return 0;
+    return kv_transfer(c, layer, h, pos0, n, const_cast<int16_t*>(k),
+                       const_cast<int16_t*>(v), true);
 }
 
 int llm_kv_clear(llm_ctx_t* c) {
@@ -711,7 +880,9 @@ int llm_kv_clear(llm_ctx_t* c) {
 }
 
 void* llm_pair_device_ptr(llm_ctx_t* c, uint32_t pair) {
-    return (c && pair < c->pairs.size()) ? c->pairs[pair] : nullptr;
+    if (!c || pair >= c->pairs.size()) return nullptr;
+    invalidate_pair(c, (int)pair);  // the caller may write through it
+    return c->pairs[pair];
 }
 
 void* llm_stream(llm_ctx_t* c) { return c ? (void*)c->stream : nullptr; }
@@ -724,10 +895,10 @@ int llm_sync(llm_ctx_t* c) {
 }
 
 int llm_event_record(llm_ctx_t* c, uint32_t slot) {
-    if (!c || slot >= 64) return fail(LLM_E_ARG, "bad event slot");
+    if (!c || slot >= 1024) return fail(LLM_E_ARG, "bad event slot");
     HIP_TRY(hipSetDevice(c->device));
     if (c->events.empty()) {
-        c->events.resize(64);
+        c->events.resize(1024);
         for (auto& e : c->events) HIP_TRY(hipEventCreate(&e));
     }
     HIP_TRY(hipEventRecord(c->events[slot], c->stream));
@@ -739,6 +910,57 @@ int llm_event_elapsed_ms(llm_ctx_t* c, uint32_t a, uint32_t b, float* ms) {
         return fail(LLM_E_ARG, "bad event slots");
     HIP_TRY(hipEventSynchronize(c->events[b]));
     HIP_TRY(hipEventElapsedTime(ms, c->events[a], c->events[b]));
+    return 0;
+}
+
+int llm_kernel_timing(llm_ctx_t* c, int enable) {
+    if (!c) return fail(LLM_E_ARG, "null context");
+    HIP_TRY(hipSetDevice(c->device));
+    harvest_timing(c);
+    for (int k = 0; k < LLM_K_COUNT; k++) c->kernel_ms[k] = 0, c->kernel_n[k] = 0;
+    c->timing = enable != 0;
+    return 0;
+}
+
+int llm_kernel_stats(llm_ctx_t* c, uint32_t kernel, uint64_t* launches,
+                     double* total_ms) {
+    if (!c || kernel >= LLM_K_COUNT) return fail(LLM_E_ARG, "bad kernel id");
+    HIP_TRY(hipSetDevice(c->device));
+    harvest_timing(c);
+    if (launches) *launches = c->kernel_n[kernel];
+    if (total_ms) *total_ms = c->kernel_ms[kernel];
+    return 0;
+}
+
+int llm_bench_copy(llm_ctx_t* c, uint64_t bytes, uint32_t iters, float* ms) {
+    if (!c || !ms || bytes < 16 || iters == 0)
+        return fail(LLM_E_ARG, "bad copy arguments");
+    HIP_TRY(hipSetDevice(c->device));
+    const size_t n16 = bytes / 16;
+    void *src = nullptr, *dst = nullptr;
+    HIP_TRY(hipMalloc(&src, n16 * 16));
+    if (hipMalloc(&dst, n16 * 16) != hipSuccess) {
+        (void)hipFree(src);
+        return fail(LLM_E_NOMEM, "copy buffer");
+    }
+    (void)hipMemsetAsync(src, 1, n16 * 16, c->stream);
+    hipEvent_t a, b;
+    (void)hipEventCreate(&a);
+    (void)hipEventCreate(&b);
+    hipError_t e = llm::launch_copy((const uint4*)src, (uint4*)dst, n16, c->stream);
+    (void)hipEventRecord(a, c->stream);
+    for (uint32_t i = 0; i < iters && e == hipSuccess; i++)
+        e = llm::launch_copy((const uint4*)src, (uint4*)dst, n16, c->stream);
+    (void)hipEventRecord(b, c->stream);
+    (void)hipEventSynchronize(b);
+    float t = 0;
+    (void)hipEventElapsedTime(&t, a, b);
+    *ms = t / iters;
+    (void)hipEventDestroy(a);
+    (void)hipEventDestroy(b);
+    (void)hipFree(src);
+    (void)hipFree(dst);
+    if (e != hipSuccess) return fail(LLM_E_HIP, hipGetErrorString(e));
     return 0;
 }
 

@@ -31,7 +31,9 @@ EXPORTS = (
     "llm_hidden_download_ports", "llm_task", "llm_kv_read", "llm_kv_write",
     "llm_kv_clear", "llm_pair_device_ptr", "llm_stream", "llm_sync",
     "llm_event_record", "llm_event_elapsed_ms", "llm_exp_tables",
+    "llm_kernel_timing", "llm_kernel_stats", "llm_bench_copy",
 )
+KERNELS = ("rmsnorm", "qkv", "rope", "attention", "oproj", "gateup", "down")
 
 
 class Shape(ctypes.Structure):
@@ -101,6 +103,12 @@ def load_library(path=LIB_PATH):
         "llm_event_elapsed_ms": (ctypes.c_int, [vp, _u32, _u32,
                                                 ctypes.POINTER(ctypes.c_float)]),
         "llm_exp_tables": (ctypes.c_int, [_i16p, _i16p]),
+        "llm_kernel_timing": (ctypes.c_int, [vp, ctypes.c_int]),
+        "llm_kernel_stats": (ctypes.c_int, [vp, _u32,
+                                            ctypes.POINTER(ctypes.c_uint64),
+                                            ctypes.POINTER(ctypes.c_double)]),
+        "llm_bench_copy": (ctypes.c_int, [vp, ctypes.c_uint64, _u32,
+                                          ctypes.POINTER(ctypes.c_float)]),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)
@@ -236,6 +244,27 @@ class Accelerator:
 
     def record(self, slot):
         self._check(lib().llm_event_record(self._ctx, slot), "event_record")
+
+    def kernel_timing(self, enable):
+        self._check(lib().llm_kernel_timing(self._ctx, 1 if enable else 0),
+                    "kernel_timing")
+
+    def kernel_stats(self):
+        """{kernel name: (launches, total_ms)} since timing was enabled."""
+        out = {}
+        for i, name in enumerate(KERNELS):
+            n = ctypes.c_uint64()
+            ms = ctypes.c_double()
+            self._check(lib().llm_kernel_stats(self._ctx, i, ctypes.byref(n),
+                                               ctypes.byref(ms)), "stats")
+            out[name] = (n.value, ms.value)
+        return out
+
+    def bench_copy(self, nbytes, iters):
+        ms = ctypes.c_float()
+        self._check(lib().llm_bench_copy(self._ctx, nbytes, iters,
+                                         ctypes.byref(ms)), "bench_copy")
+        return ms.value
 
     def elapsed_ms(self, a, b):
         ms = ctypes.c_float()

@@ -186,3 +186,84 @@ def test_kv_preload_then_decode_long_context():
         got = a.download(0, 1)
     code, want, _ = om.task((kc, vc), 18, 0, x, n)
     assert first_mismatch(got, want) is None
+
+
+def test_split_attention_p8_block_late_position():
+    # 8 rows at positions 200..207: 4 tiles per row, split over workgroups.
+    import llm_accel
+    spec = workloads.CONFIG_A
+    n = 200
+    synth = workloads.SyntheticModel(spec, layers=1)
+    om = oracle_from_synthetic(synth, oracle_shape(spec, layers=1, max_seq=256))
+    kc, vc = om.new_kv()
+    with llm_accel.Accelerator(accel_shape(spec, layers=1, max_seq=256)) as a:
+        a.load_model(synth)
+        for h in range(spec.kv_heads):
+            k, v = synth.kv_rows(n, seed_offset=20 + h)
+            kc[0, h, :n], vc[0, h, :n] = k, v
+            a.kv_write(0, h, 0, k, v)
+        x = synth.hidden_rows(8)
+        a.upload(2, x)
+        _say("case split P8 at 200")
+        a.task(18, 0, 8, n, 2, 0)
+        got = a.download(0, 8)
+        kg, vg = a.kv_read(0, 1, 0, n + 8)
+    code, want, _ = om.task((kc, vc), 18, 0, x, n)
+    assert first_mismatch(got, want) is None
+    assert first_mismatch(kg, kc[0, 1, :n + 8]) is None
+    assert first_mismatch(vg, vc[0, 1, :n + 8]) is None
+
+
+@pytest.mark.parametrize("n", [40, 150])
+def test_saturating_kv_takes_exact_path(n):
+    # K/V values beyond +-8.0 saturate in Q4.12; the kernel must switch to
+    # the per-product path on those tiles (fused for n=40, split for 150).
+    import llm_accel
+    spec = workloads.CONFIG_B
+    synth = workloads.SyntheticModel(spec, layers=1)
+    om = oracle_from_synthetic(synth, oracle_shape(spec, layers=1, max_seq=n + 8))
+    kc, vc = om.new_kv()
+    rng = np.random.default_rng(n)
+    with llm_accel.Accelerator(accel_shape(spec, layers=1, max_seq=n + 8)) as a:
+        a.load_model(synth)
+        for h in range(spec.kv_heads):
+            k = rng.integers(-9000, 9000, (n, spec.head_dim), dtype=np.int16)
+            v = rng.integers(-9000, 9000, (n, spec.head_dim), dtype=np.int16)
+            k[: n // 2] //= 8  # first tiles mostly in range
+            kc[0, h, :n], vc[0, h, :n] = k, v
+            a.kv_write(0, h, 0, k, v)
+        x = synth.hidden_rows(2)
+        a.upload(2, x)
+        _say(f"case saturating kv n={n}")
+        a.task(18, 0, 2, n, 2, 0)
+        got = a.download(0, 2)
+    code, want, _ = om.task((kc, vc), 18, 0, x, n)
+    assert first_mismatch(got, want) is None
+
+
+def test_norm_cache_invalidation():
+    # T18 writes pair 0 and derives its FFN norm; uploading new rows into
+    # pair 0 before T19 must discard that copy.  T19 into pair 1 derives the
+    # next layer's attention norm; T18 on a different pair must not use it.
+    import llm_accel
+    spec = workloads.CONFIG_A
+    synth = workloads.SyntheticModel(spec, layers=2)
+    om = oracle_from_synthetic(synth, oracle_shape(spec, layers=2, max_seq=64))
+    kv = om.new_kv()
+    h = synth.hidden_rows(12)
+    with llm_accel.Accelerator(accel_shape(spec, layers=2, max_seq=64)) as a:
+        a.load_model(synth)
+        a.upload(2, h[:4])
+        a.task(18, 0, 4, 0, 2, 0)
+        a.upload(0, h[4:8])           # overwrite T18's output
+        a.task(19, 0, 4, 0, 0, 1)
+        got19 = a.download(1, 4)
+        a.upload(3, h[8:12])
+        a.task(18, 1, 4, 0, 3, 2)     # layer 1 on a pair T19 did not write
+        got18 = a.download(2, 4)
+        _say("case norm cache")
+    _, _, _ = om.task(kv, 18, 0, h[:4], 0)
+    _, want19, _ = om.task(kv, 19, 0, h[4:8], 0)
+    _, want18, _ = om.task(kv, 18, 1, h[8:12], 0)
+    assert first_mismatch(got19, want19) is None
+    assert first_mismatch(got18, want18) is None
