@@ -200,6 +200,14 @@ int llm_kernel_timing(llm_ctx_t* ctx, int enable);
 int llm_kernel_stats(llm_ctx_t* ctx, uint32_t kernel, uint64_t* launches,
                      double* total_ms);
 
+/* Back-to-back launches of one projection kernel (kernel = LLM_K_QKV,
+ * LLM_K_OPROJ, LLM_K_GATEUP or LLM_K_DOWN) on `rows` resident rows,
+ * cycling over layers [0, layers); *avg_us is the mean duration of one
+ * launch measured with HIP events on the context stream.  Outputs go to
+ * scratch; hidden pairs and the KV cache are untouched. */
+int llm_bench_projection(llm_ctx_t* ctx, uint32_t kernel, uint32_t rows,
+                         uint32_t layers, uint32_t iters, float* avg_us);
+
 /* A plain device-to-device copy of `bytes` repeated `iters` times on the
  * context stream (calibration reference for HBM counters and achievable
  * bandwidth); *ms is the average duration of one copy. */

@@ -932,6 +932,61 @@ int llm_kernel_stats(llm_ctx_t* c, uint32_t kernel, uint64_t* launches,
     return 0;
 }
 
+int llm_bench_projection(llm_ctx_t* c, uint32_t kernel, uint32_t rows,
+                         uint32_t layers, uint32_t iters, float* avg_us) {
+    if (!c || !avg_us || rows == 0 || rows > 8 || layers == 0 ||
+        layers > c->L || iters == 0)
+        return fail(LLM_E_ARG, "bad projection benchmark arguments");
+    if (kernel != LLM_K_QKV && kernel != LLM_K_OPROJ &&
+        kernel != LLM_K_GATEUP && kernel != LLM_K_DOWN)
+        return fail(LLM_E_ARG, "not a projection kernel");
+    HIP_TRY(hipSetDevice(c->device));
+    auto launch = [&](uint32_t layer) -> hipError_t {
+        llm::ProjArgs a{};
+        a.rows = rows;
+        int epi = llm::EPI_STORE, L = 16;
+        uint32_t blocks = 0;
+        if (kernel == LLM_K_QKV) {
+            const Matrix& m = c->mat(layer, M_QKV);
+            a.w0 = m.d; a.steps = m.steps; a.x = c->xn_attn; a.ldx = c->Hp;
+            a.out = c->qkv; a.ldo = c->Nqkv; a.n = m.n; L = m.L; blocks = m.n_pad / 4;
+        } else if (kernel == LLM_K_OPROJ || kernel == LLM_K_DOWN) {
+            const Matrix& m = c->mat(layer, kernel == LLM_K_OPROJ ? M_O : M_DOWN);
+            a.w0 = m.d; a.steps = m.steps;
+            a.x = kernel == LLM_K_OPROJ ? c->attn : c->act;
+            a.ldx = kernel == LLM_K_OPROJ ? c->Hp : c->Ip;
+            // output into a buffer the launch does not read
+            a.out = c->qkv; a.ldo = c->Nqkv; a.res = c->xn_ffn; a.ldr = c->Hp;
+            a.n = m.n; L = m.L; blocks = m.n_pad / 4; epi = llm::EPI_RESID;
+        } else {
+            const Matrix& g = c->mat(layer, M_GATE);
+            const Matrix& u = c->mat(layer, M_UP);
+            a.w0 = g.d; a.w1 = u.d; a.steps = g.steps; a.x = c->xn_ffn;
+            a.ldx = c->Hp; a.out = c->act; a.ldo = c->Ip; a.n = g.n;
+            a.exp8 = c->exp8; L = std::min(g.L, u.L); blocks = g.n_pad / 4;
+            epi = llm::EPI_SILU;
+        }
+        return llm::launch_proj(a, epi, L, blocks, c->stream);
+    };
+    hipEvent_t e0, e1;
+    HIP_TRY(hipEventCreate(&e0));
+    HIP_TRY(hipEventCreate(&e1));
+    hipError_t e = launch(0);  // warm the instruction cache
+    (void)hipEventRecord(e0, c->stream);
+    for (uint32_t i = 0; i < iters && e == hipSuccess; i++) e = launch(i % layers);
+    (void)hipEventRecord(e1, c->stream);
+    (void)hipEventSynchronize(e1);
+    float ms = 0;
+    (void)hipEventElapsedTime(&ms, e0, e1);
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    // scratch rows were overwritten: drop derived norm copies
+    c->attn_cache.pair = c->ffn_cache.pair = -1;
+    if (e != hipSuccess) return fail(LLM_E_HIP, hipGetErrorString(e));
+    *avg_us = ms * 1000.0f / iters;
+    return 0;
+}
+
 int llm_bench_copy(llm_ctx_t* c, uint64_t bytes, uint32_t iters, float* ms) {
     if (!c || !ms || bytes < 16 || iters == 0)
         return fail(LLM_E_ARG, "bad copy arguments");

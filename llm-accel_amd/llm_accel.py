@@ -32,6 +32,7 @@ EXPORTS = (
     "llm_kv_clear", "llm_pair_device_ptr", "llm_stream", "llm_sync",
     "llm_event_record", "llm_event_elapsed_ms", "llm_exp_tables",
     "llm_kernel_timing", "llm_kernel_stats", "llm_bench_copy",
+    "llm_bench_projection",
 )
 KERNELS = ("rmsnorm", "qkv", "rope", "attention", "oproj", "gateup", "down")
 
@@ -109,6 +110,8 @@ def load_library(path=LIB_PATH):
                                             ctypes.POINTER(ctypes.c_double)]),
         "llm_bench_copy": (ctypes.c_int, [vp, ctypes.c_uint64, _u32,
                                           ctypes.POINTER(ctypes.c_float)]),
+        "llm_bench_projection": (ctypes.c_int, [vp, _u32, _u32, _u32, _u32,
+                                                ctypes.POINTER(ctypes.c_float)]),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)
@@ -211,6 +214,24 @@ class Accelerator:
                     "download")
         return out
 
+    def upload_ports(self, pair, port0, port1, rows, stride_words):
+        """Rows in the reference's packed feature ports: rows 0-3 in port0,
+        rows 4-7 in port1, each row `stride_words` 64-byte words."""
+        port0 = np.ascontiguousarray(port0, np.int16)
+        port1 = np.ascontiguousarray(port1, np.int16)
+        self._check(lib().llm_hidden_upload_ports(
+            self._ctx, pair, _p16(port0), _p16(port1), rows, stride_words),
+            "upload_ports")
+
+    def download_ports(self, pair, rows, stride_words, port0=None, port1=None):
+        n = 4 * stride_words * 32
+        port0 = np.zeros(n, np.int16) if port0 is None else port0
+        port1 = np.zeros(n, np.int16) if port1 is None else port1
+        self._check(lib().llm_hidden_download_ports(
+            self._ctx, pair, _p16(port0), _p16(port1), rows, stride_words),
+            "download_ports")
+        return port0, port1
+
     # --- tasks ------------------------------------------------------------
     def task(self, op, layer, token_count, position, in_pair, out_pair,
              tile_len=0):
@@ -259,6 +280,13 @@ class Accelerator:
                                                ctypes.byref(ms)), "stats")
             out[name] = (n.value, ms.value)
         return out
+
+    def bench_projection(self, kernel, rows, layers, iters):
+        us = ctypes.c_float()
+        self._check(lib().llm_bench_projection(self._ctx, KERNELS.index(kernel),
+                                               rows, layers, iters,
+                                               ctypes.byref(us)), "bench_projection")
+        return us.value
 
     def bench_copy(self, nbytes, iters):
         ms = ctypes.c_float()

@@ -521,6 +521,49 @@ static uint64_t cdiv(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
  * model lives in shard group (t & 1), local block (t >> 1); lane
  * (out%16)*16 + in%16 of the tile is word lane%32 of shard
  * group*8 + lane/32. */
+/* Packed-tile layout of one shape: tiles per projection and their base
+ * within a layer (projection_spec, host:325-376). */
+typedef struct {
+    uint64_t base[ORC_PROJ_COUNT + 1];
+    uint64_t layer_tiles, total_tiles;
+} tile_map_t;
+
+static void tile_map(const orc_shape_t* s, tile_map_t* t) {
+    t->layer_tiles = 0;
+    for (uint32_t p = 0; p < ORC_PROJ_COUNT; p++) {
+        t->base[p] = t->layer_tiles;
+        t->layer_tiles += cdiv(orc_proj_out_dim(s, p), 16) *
+                          cdiv(orc_proj_in_dim(s, p), 16);
+    }
+    t->base[ORC_PROJ_COUNT] = t->layer_tiles;
+    t->total_tiles = (uint64_t)s->num_layers * t->layer_tiles;
+}
+
+/* Inverse of projection_weight_raw (host:899-935): lane `lane` of word `w`
+ * of shard `shard` holds element (out, in) of projection p of `layer`.
+ * Returns 0 when the slot is padding (beyond the last tile or outside the
+ * matrix). */
+static int shard_slot(const orc_shape_t* s, const tile_map_t* t,
+                      uint32_t shard, uint64_t w, uint32_t lane,
+                      uint64_t* layer, uint32_t* p, uint64_t* out,
+                      uint64_t* in) {
+    const uint32_t group = shard / 8, tile_word = shard % 8;
+    const uint64_t tile = 2 * w + group;
+    if (tile >= t->total_tiles) return 0;
+    *layer = tile / t->layer_tiles;
+    const uint64_t rem = tile % t->layer_tiles;
+    uint32_t q = 0;
+    while (q + 1 < ORC_PROJ_COUNT && rem >= t->base[q + 1]) q++;
+    const uint64_t tt = rem - t->base[q];
+    const uint32_t in_dim = orc_proj_in_dim(s, q);
+    const uint64_t in_tiles = cdiv(in_dim, 16);
+    const uint32_t lane_in_tile = tile_word * 32 + lane;
+    *p = q;
+    *out = (tt / in_tiles) * 16 + lane_in_tile / 16;
+    *in = (tt % in_tiles) * 16 + lane_in_tile % 16;
+    return *out < orc_proj_out_dim(s, q) && *in < in_dim;
+}
+
 void orc_model_init_reference_random(orc_model_t* m, uint32_t seed, int alg) {
     const orc_shape_t* s = &m->s;
     mt19937_t g;
@@ -535,37 +578,66 @@ void orc_model_init_reference_random(orc_model_t* m, uint32_t seed, int alg) {
     for (size_t i = 0; i < (size_t)(2 * s->num_layers + 1) * s->hidden_size; i++)
         m->norms[i] = (int16_t)uid_draw(&g, 224, 288, alg);
 
-    uint64_t ptiles[ORC_PROJ_COUNT], pbase[ORC_PROJ_COUNT], layer_tiles = 0;
-    for (uint32_t p = 0; p < ORC_PROJ_COUNT; p++) {
-        ptiles[p] = cdiv(orc_proj_out_dim(s, p), 16) * cdiv(orc_proj_in_dim(s, p), 16);
-        pbase[p] = layer_tiles;
-        layer_tiles += ptiles[p];
-    }
-    uint64_t total_tiles = (uint64_t)s->num_layers * layer_tiles;
-    uint64_t shard_words = cdiv(total_tiles, 2);
+    tile_map_t t;
+    tile_map(s, &t);
+    const uint64_t shard_words = cdiv(t.total_tiles, 2);
     for (uint32_t shard = 0; shard < 16; shard++) {
-        uint32_t group = shard / 8, tile_word = shard % 8;
         for (uint64_t w = 0; w < shard_words; w++) {
-            uint64_t tile = 2 * w + group;
-            uint64_t layer = tile / layer_tiles;
-            uint64_t rem = tile % layer_tiles;
             for (uint32_t lane = 0; lane < 32; lane++) {
                 int16_t val = (int16_t)uid_draw(&g, -64, 64, alg);
-                if (tile >= total_tiles || layer >= m->kept) continue;
-                uint32_t p = 0;
-                while (p + 1 < ORC_PROJ_COUNT && rem >= pbase[p + 1]) p++;
-                uint64_t t = rem - pbase[p];
-                uint32_t in_dim = orc_proj_in_dim(s, p);
-                uint32_t out_dim = orc_proj_out_dim(s, p);
-                uint64_t in_tiles = cdiv(in_dim, 16);
-                uint32_t lane_in_tile = tile_word * 32 + lane;
-                uint64_t out = (t / in_tiles) * 16 + lane_in_tile / 16;
-                uint64_t in = (t % in_tiles) * 16 + lane_in_tile % 16;
-                if (out < out_dim && in < in_dim)
-                    m->w[layer * ORC_PROJ_COUNT + p][out * in_dim + in] = val;
+                uint64_t layer, out, in;
+                uint32_t p;
+                if (!shard_slot(s, &t, shard, w, lane, &layer, &p, &out, &in) ||
+                    layer >= m->kept)
+                    continue;
+                m->w[layer * ORC_PROJ_COUNT + p][out * orc_proj_in_dim(s, p) + in] = val;
             }
         }
     }
+}
+
+int orc_reference_random_shards(const orc_shape_t* s, uint32_t seed, int alg,
+                                uint64_t shard_words, int16_t* const out[16]) {
+    tile_map_t t;
+    tile_map(s, &t);
+    if (shard_words != cdiv(t.total_tiles, 2)) return -1;
+    mt19937_t g;
+    mt_seed(&g, seed);
+    for (size_t i = 0; i < (size_t)s->vocab_size * s->hidden_size; i++)
+        (void)uid_draw(&g, -128, 128, alg);
+    for (size_t i = 0; i < (size_t)(2 * s->num_layers + 1) * s->hidden_size; i++)
+        (void)uid_draw(&g, 224, 288, alg);
+    for (uint32_t shard = 0; shard < 16; shard++)
+        for (uint64_t w = 0; w < shard_words; w++)
+            for (uint32_t lane = 0; lane < 32; lane++)
+                out[shard][w * 32 + lane] = (int16_t)uid_draw(&g, -64, 64, alg);
+    return 0;
+}
+
+uint64_t orc_shard_words(const orc_shape_t* s) {
+    tile_map_t t;
+    tile_map(s, &t);
+    return cdiv(t.total_tiles, 2);
+}
+
+int orc_model_load_shards(orc_model_t* m, const int16_t* const shards[16],
+                          uint64_t shard_words) {
+    const orc_shape_t* s = &m->s;
+    tile_map_t t;
+    tile_map(s, &t);
+    if (shard_words < cdiv(t.total_tiles, 2)) return -1;
+    for (uint32_t shard = 0; shard < 16; shard++)
+        for (uint64_t w = 0; w < shard_words; w++)
+            for (uint32_t lane = 0; lane < 32; lane++) {
+                uint64_t layer, out, in;
+                uint32_t p;
+                if (!shard_slot(s, &t, shard, w, lane, &layer, &p, &out, &in) ||
+                    layer >= m->kept)
+                    continue;
+                m->w[layer * ORC_PROJ_COUNT + p][out * orc_proj_in_dim(s, p) + in] =
+                    shards[shard][w * 32 + lane];
+            }
+    return 0;
 }
 
 uint32_t orc_lm_head_argmax(const int16_t* table, uint32_t vocab,

@@ -143,6 +143,18 @@ uint32_t orc_proj_out_dim(const orc_shape_t* s, uint32_t proj);
  * of the shape are consumed; only kept_layers are stored. */
 void orc_model_init_reference_random(orc_model_t* m, uint32_t seed,
                                      int uid_algorithm);
+/* Weights from the reference's 16 packed shards (the layout
+ * projection_weight_raw reads, host:899-935): shard i is `shard_words`
+ * words of 32 int16 lanes.  Returns -1 when shard_words is too small. */
+int orc_model_load_shards(orc_model_t* m, const int16_t* const shards[16],
+                          uint64_t shard_words);
+/* The 16 weight shards initialize_random_model fills (host:842-869), in
+ * the reference's draw order (the embedding and norm draws are consumed
+ * first); shard_words must equal orc_shard_words(s). */
+int orc_reference_random_shards(const orc_shape_t* s, uint32_t seed, int alg,
+                                uint64_t shard_words, int16_t* const out[16]);
+/* Words per shard of a shape: ceil(layers * tiles per layer / 2). */
+uint64_t orc_shard_words(const orc_shape_t* s);
 /* make_random_tensor (host:3089-3103). */
 void orc_make_random_tensor(uint32_t rows, uint32_t cols, uint32_t seed,
                             int32_t lo, int32_t hi, int uid_algorithm,

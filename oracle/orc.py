@@ -91,6 +91,13 @@ def _load():
         "orc_uniform_ints": (None, [_u32, ctypes.c_int32, ctypes.c_int32,
                                     ctypes.c_int, ctypes.c_size_t, _i32p]),
         "orc_set_threads": (None, [ctypes.c_int]),
+        "orc_reference_random_shards": (ctypes.c_int, [
+            ctypes.c_void_p, _u32, ctypes.c_int, ctypes.c_uint64,
+            ctypes.POINTER(_i16p)]),
+        "orc_shard_words": (ctypes.c_uint64, [ctypes.c_void_p]),
+        "orc_model_load_shards": (ctypes.c_int, [ctypes.c_void_p,
+                                                 ctypes.POINTER(_i16p),
+                                                 ctypes.c_uint64]),
         "orc_task": (ctypes.c_int, [ctypes.c_void_p, _i16p, _i16p, _u32,
                                     _u32, _u32, _u32, _i16p, _i16p,
                                     ctypes.c_int, ctypes.POINTER(Status)]),
@@ -223,6 +230,23 @@ def lm_head_argmax(table, h):
                                       table.shape[1], p16(h)))
 
 
+def shard_words(shape):
+    """64-byte words per packed weight shard of a shape."""
+    return int(lib.orc_shard_words(ctypes.byref(shape)))
+
+
+def reference_random_shards(shape, seed, uid=UID_DIVREJ):
+    """The reference's 16 packed weight shards for `seed`, each
+    [words][32] int16 (initialize_random_model's draw order)."""
+    words = shard_words(shape)
+    shards = [np.zeros((words, 32), np.int16) for _ in range(16)]
+    arr = (_i16p * 16)(*[p16(x) for x in shards])
+    rc = lib.orc_reference_random_shards(ctypes.byref(shape), seed, uid,
+                                         words, arr)
+    assert rc == 0
+    return shards
+
+
 class Model:
     """Row-major fixed-point model held by the oracle."""
 
@@ -265,6 +289,14 @@ class Model:
 
     def init_reference_random(self, seed, uid=UID_DIVREJ):
         lib.orc_model_init_reference_random(self._h, seed, uid)
+
+    def load_shards(self, shards):
+        """Weights from 16 packed shards, each [words][32] int16."""
+        shards = [np.ascontiguousarray(x, np.int16) for x in shards]
+        arr = (_i16p * 16)(*[p16(x) for x in shards])
+        rc = lib.orc_model_load_shards(self._h, arr, shards[0].size // 32)
+        if rc:
+            raise ValueError("shards too small for the shape")
 
     def new_kv(self):
         s = self.shape

@@ -1,0 +1,181 @@
+"""HIP path on the reference's own random models, loaded through the packed
+16-shard weight format (llm_load_packed_shards), against the published
+known answers and the oracle.
+
+Models: initialize_random_model(seed) (host/host_qwen_8x64.cpp:842-869) on
+the reference profiles small / medium / qwen-layer (host:309-343); hidden
+rows from make_random_tensor (host:3089-3103) as in the reference's payload
+regression (host:5046-5061)."""
+import json
+import os
+import sys
+
+import numpy as np
+import pytest
+
+from oracle import orc
+from helpers import first_mismatch
+
+pytestmark = pytest.mark.gpu
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+KAT = json.load(open(os.path.join(HERE, "golden", "kat.json")))
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(autouse=True)
+def _floor_tables():
+    orc.set_exp_policy(orc.EXP_FLOOR, orc.EXP_FLOOR)
+    yield
+
+
+def _accelerator(s, seed):
+    import llm_accel
+    shape = llm_accel.Shape(s.vocab_size, s.hidden_size, s.intermediate_size,
+                            s.num_layers, s.num_heads, s.num_kv_heads,
+                            s.max_seq_len, 1e6)
+    acc = llm_accel.Accelerator(shape)
+    acc.load_packed_shards(orc.reference_random_shards(s, seed))
+    om = orc.Model(s, s.num_layers, True)
+    om.init_reference_random(seed)
+    acc.load_norms(om.norms())
+    return acc, om
+
+
+def _forward(acc, rows, pos, layers):
+    """T18/T19 per layer then T20, pairs 1 -> 0 -> 1 ... as the reference
+    binds them; returns the outputs of every task."""
+    outs = []
+    pin, pout = 1, 0
+    for layer in range(layers):
+        for op in (18, 19):
+            rc, st = acc.task(op, layer, rows, pos, pin, pout)
+            assert rc == 0 and st.code == 0 and st.last_task == 1
+            outs.append(acc.download(pout, rows))
+            pin, pout = pout, pin
+    rc, st = acc.task(20, 0, rows, pos, pin, pout)
+    assert rc == 0 and st.last_task == 1
+    outs.append(acc.download(pout, rows))
+    return outs
+
+
+def test_kat1_qwen_layer_p2_final_probes():
+    """P2 block at the Qwen layer shape: the final-norm probes the
+    reference's payload regression prints (KAT-1, P2)."""
+    k1 = KAT["kat1_qwen_layer_p8"]
+    k = KAT["kat1_qwen_layer_p2"]
+    s = orc.profile("qwen-layer")
+    _say("case kat1 qwen-layer P2")
+    acc, om = _accelerator(s, k1["seed"])
+    with acc:
+        h = orc.make_random_tensor(2, s.hidden_size,
+                                   k1["seed"] ^ k1["hidden_seed_xor"], -48, 48)
+        acc.upload(1, h)
+        outs = _forward(acc, 2, 0, 1)
+        fin = outs[-1]
+        probes = [int(fin[k["final_probe_row"], c]) for c in k["final_probe_cols"]]
+        assert probes == k["final_probe_raw_payload"]
+        post, out = om.prefill_sequence(h, 0, orc.SEM_RAW_PAYLOAD)
+        assert first_mismatch(outs[0], post) is None
+        assert first_mismatch(outs[1], out) is None
+        assert first_mismatch(fin, orc.rmsnorm(out, om.norms()[2])) is None
+
+
+def test_kat1_qwen_layer_p8_matches_pinned_oracle():
+    """P8 block at the Qwen layer shape.  The oracle's post-attention rows
+    for this model reproduce the reference's raw-payload vs direct
+    fingerprint (117 mismatches, max error 1, first four listed); the GPU
+    must equal them bit for bit, and the later tasks too."""
+    k = KAT["kat1_qwen_layer_p8"]
+    s = orc.profile("qwen-layer")
+    _say("case kat1 qwen-layer P8")
+    acc, om = _accelerator(s, k["seed"])
+    with acc:
+        h = orc.make_random_tensor(8, s.hidden_size,
+                                   k["seed"] ^ k["hidden_seed_xor"], -48, 48)
+        acc.upload(1, h)
+        outs = _forward(acc, 8, 0, 1)
+        post, out = om.prefill_sequence(h, 0, orc.SEM_RAW_PAYLOAD)
+        post_d, _ = om.prefill_sequence(h, 0, orc.SEM_DIRECT)
+        diff = np.argwhere(outs[0] != post_d)
+        assert len(diff) == k["post_attention_mismatches"]
+        assert first_mismatch(outs[0], post) is None
+        assert first_mismatch(outs[1], out) is None
+        assert first_mismatch(outs[2], orc.rmsnorm(out, om.norms()[2])) is None
+        okv = om.new_kv()
+        code, _, _ = om.task(okv, 18, 0, h, 0)
+        assert code == 0
+        for head in range(s.num_kv_heads):
+            kc, vc = acc.kv_read(0, head, 0, 8)
+            assert first_mismatch(kc, okv[0][0, head, :8]) is None
+            assert first_mismatch(vc, okv[1][0, head, :8]) is None
+
+
+@pytest.mark.parametrize("profile", ["small", "medium"])
+def test_reference_profiles_blocks_and_decode(profile):
+    """Two-layer reference profiles: a P8 block, a ragged P3 block and two
+    decode forwards, every task and the KV cache compared with the
+    oracle."""
+    s = orc.profile(profile)
+    seed = 20260718
+    _say(f"case {profile} blocks")
+    acc, om = _accelerator(s, seed)
+    kv = om.new_kv()
+    hidden = orc.make_random_tensor(13, s.hidden_size, seed ^ 0x5eed, -128, 128)
+    with acc:
+        row0 = 0
+        for pos, rows in ((0, 8), (8, 3), (11, 1), (12, 1)):
+            h = hidden[row0:row0 + rows]
+            row0 += rows
+            acc.upload(1, h)
+            outs = _forward(acc, rows, pos, s.num_layers)
+            cur, i = h, 0
+            for layer in range(s.num_layers):
+                for op in (18, 19):
+                    code, cur, _ = om.task(kv, op, layer, cur, pos)
+                    assert code == 0
+                    err = first_mismatch(outs[i], cur)
+                    assert err is None, f"{profile} pos {pos} layer {layer} op {op}: {err}"
+                    i += 1
+            code, fin, _ = om.task(kv, 20, 0, cur, pos)
+            assert first_mismatch(outs[-1], fin) is None
+        for layer in range(s.num_layers):
+            for head in range(s.num_kv_heads):
+                k, v = acc.kv_read(layer, head, 0, row0)
+                assert first_mismatch(k, kv[0][layer, head, :row0]) is None
+                assert first_mismatch(v, kv[1][layer, head, :row0]) is None
+
+
+def _pack_feature(rows, stride_words, fill):
+    """pack_feature (host:2062-2080): token t goes to port t // 4 at word
+    (t % 4) * stride + e // 32, lane e % 32."""
+    p0 = np.full(4 * stride_words * 32, fill, np.int16)
+    p1 = p0.copy()
+    for t, row in enumerate(rows):
+        dst = p0 if t < 4 else p1
+        for e, v in enumerate(row):
+            dst[((t % 4) * stride_words + e // 32) * 32 + e % 32] = v
+    return p0, p1
+
+
+@pytest.mark.parametrize("n", [1, 5, 8])
+def test_feature_ports_round_trip(n):
+    s = orc.profile("medium")
+    stride = -(-max(s.hidden_size, s.intermediate_size) // 32)
+    _say(f"case ports n={n}")
+    acc, _ = _accelerator(s, 5)
+    rng = np.random.default_rng(n)
+    rows = rng.integers(-32768, 32767, (n, s.hidden_size), dtype=np.int16)
+    with acc:
+        p0, p1 = _pack_feature(rows, stride, 0)
+        acc.upload_ports(1, p0, p1, n, stride)
+        assert first_mismatch(acc.download(1, n), rows) is None
+        acc.upload(0, rows)
+        q0, q1 = acc.download_ports(0, n, stride,
+                                    np.full_like(p0, 7), np.full_like(p1, 7))
+        w0, w1 = _pack_feature(rows, stride, 7)
+        assert np.array_equal(q0, w0) and np.array_equal(q1, w1)
