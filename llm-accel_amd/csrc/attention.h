@@ -10,10 +10,11 @@ struct AttnArgs {
     const int16_t* qkv;   // projections of the active rows: q | k | v
     uint32_t ldqkv;
     const int16_t* rope;  // [max_seq][head_dim] = cos d/2 | sin d/2 (Q8.8)
-    int16_t* kcache;      // page pool [pages][64][head_dim], K after RoPE
-    int16_t* vcache;      // page pool [pages][64][head_dim], V
-    const int32_t* page_table;  // this layer: [kv_heads][tiles]
-    uint32_t tiles;       // page-table tiles per (layer, head)
+    int16_t* kcache;      // this layer's K pages [kv_heads][tiles][64][head_dim]
+                          // (after RoPE, rows bank-paired)
+    int16_t* vcache;      // this layer's V pages [kv_heads][tiles][head_dim][64]
+                          // (positions bank-paired)
+    uint32_t tiles;       // pages per (layer, KV head)
     uint32_t pos0;        // absolute position of active row 0
     uint32_t num_heads, num_kv_heads, group, head_dim;
     int32_t qk_scale;     // fm(1/sqrt(head_dim)) raw

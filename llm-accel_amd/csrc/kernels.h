@@ -6,7 +6,11 @@
 
 namespace llm {
 
-enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SILU = 2 };
+// Epilogues: STORE the narrowed sums; RESID add a residual row (and
+// optionally write a constant-gain RMSNorm of the result); SILU store
+// silu(gate) * up; STORE_NORM_IN like STORE on inputs normalised while they
+// are loaded (constant-gain RMSNorm of the raw rows).
+enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SILU = 2, EPI_STORE_NORM_IN = 3 };
 
 // Rows per weight block and columns per k-step of the "tile4x128" layout.
 constexpr uint32_t kBlockRows = 4;
@@ -32,6 +36,16 @@ struct ProjArgs {
     uint32_t ldn;
     const int16_t* norm_gamma;
     int32_t norm_gain;
+    // EPI_RESID, optional: the final RMSNorm (constant gain norm_gain) of
+    // the output rows into final_out [8][ldn]; its rows rows..7 copy the
+    // same rows of the residual, so final_out holds a whole pair.
+    int16_t* final_out;
+    const int16_t* final_gamma;
+    // EPI_STORE_NORM_IN: x[r][k] is replaced by rnd(x * in_gain * in_gamma[k],
+    // 16) for k < in_cols and by 0 beyond.
+    const int16_t* in_gamma;
+    int32_t in_gain;
+    uint32_t in_cols;
 };
 
 hipError_t launch_copy(const uint4* src, uint4* dst, size_t n16,

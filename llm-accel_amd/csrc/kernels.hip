@@ -74,6 +74,28 @@ __global__ __launch_bounds__(256) void rmsnorm_const_kernel(
 // products, bounded by the host), then widen to int64; the 16 lanes of a
 // row and the 4 wavefronts reduce in int64.
 // ---------------------------------------------------------------------
+// Eight inputs normalised with a constant gain: rnd(x * gain * gamma, 16),
+// zero at columns >= cols.
+// |x * gain * gamma| < 2^15 * 2^13 * 2^15, so the product shifted right by 16
+// fits 32 bits before the saturation.
+__device__ __forceinline__ int32_t norm1(int32_t x, int32_t gg) {
+    const int32_t y = (int32_t)(((int64_t)x * gg + 32768) >> 16);
+    return y < -32768 ? -32768 : (y > 32767 ? 32767 : y);
+}
+// Eight inputs normalised with a constant gain: rnd(x * gain * gamma, 16);
+// columns >= cols have gamma 0 (the caller zeroes g there).
+__device__ __forceinline__ uint4 norm8(uint4 x, uint4 g, int32_t gain) {
+    uint32_t w[4] = {x.x, x.y, x.z, x.w};
+    const uint32_t gw[4] = {g.x, g.y, g.z, g.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int32_t lo = norm1((int16_t)(w[i] & 0xffff), gain * (int16_t)(gw[i] & 0xffff));
+        const int32_t hi = norm1((int16_t)(w[i] >> 16), gain * (int16_t)(gw[i] >> 16));
+        w[i] = (uint32_t)(uint16_t)lo | ((uint32_t)hi << 16);
+    }
+    return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
 template <int RT, int L, int EPI>
 __global__ __launch_bounds__(256) void proj_kernel(ProjArgs a) {
     constexpr int NM = EPI == EPI_SILU ? 2 : 1;
@@ -110,6 +132,14 @@ __global__ __launch_bounds__(256) void proj_kernel(ProjArgs a) {
 #pragma unroll
             for (int r = 0; r < RT; r++)
                 xv[r] = *(const uint4*)(xp + (size_t)r * a.ldx);
+            if (EPI == EPI_STORE_NORM_IN) {
+                const uint32_t k0 = s * 128 + j * 8;
+                const uint4 gv = k0 < a.in_cols ? *(const uint4*)(a.in_gamma + k0)
+                                                : make_uint4(0, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < RT; r++)
+                    xv[r] = norm8(xv[r], gv, a.in_gain);
+            }
             xp += 128;
 #pragma unroll
             for (int m = 0; m < NM; m++)
@@ -173,6 +203,9 @@ __global__ __launch_bounds__(256) void proj_kernel(ProjArgs a) {
                 if (a.norm_out)
                     a.norm_out[(size_t)r * a.ldn + n] = fx_sat16(fx_rnd(
                         (int64_t)y * a.norm_gain * a.norm_gamma[n], 16));
+                if (a.final_out)
+                    a.final_out[(size_t)r * a.ldn + n] = fx_sat16(fx_rnd(
+                        (int64_t)y * a.norm_gain * a.final_gamma[n], 16));
             } else if (EPI == EPI_SILU) {
                 int16_t up = fx_narrow_projection(tot[NM - 1]);
                 int16_t sg = fx_silu(y, a.exp8);
@@ -180,6 +213,12 @@ __global__ __launch_bounds__(256) void proj_kernel(ProjArgs a) {
             }
             a.out[(size_t)r * a.ldo + n] = y;
         }
+    }
+    if (EPI == EPI_RESID && a.final_out && t < 32) {
+        const int ii = t >> 3, r = t & 7;
+        const uint32_t n = b * 4 + ii;
+        if ((uint32_t)r >= a.rows && n < a.n)
+            a.final_out[(size_t)r * a.ldn + n] = a.res[(size_t)r * a.ldr + n];
     }
 }
 
@@ -224,6 +263,7 @@ hipError_t launch_proj(const ProjArgs& a, int epi, int L, uint32_t blocks,
     switch (epi) {
     case EPI_STORE: return launch_proj_epi<EPI_STORE>(a, L, blocks, st);
     case EPI_RESID: return launch_proj_epi<EPI_RESID>(a, L, blocks, st);
+    case EPI_STORE_NORM_IN: return launch_proj_epi<EPI_STORE_NORM_IN>(a, L, blocks, st);
     default: return launch_proj_epi<EPI_SILU>(a, L, blocks, st);
     }
 }

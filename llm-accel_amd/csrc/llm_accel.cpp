@@ -84,8 +84,6 @@ struct llm_ctx {
     int16_t* exp14 = nullptr;
     int16_t* kcache = nullptr;
     int16_t* vcache = nullptr;
-    int32_t* page_table = nullptr;     // [layer][kv_head][tile]
-    std::vector<int32_t> host_pages;
     std::vector<int16_t*> pairs;       // [8][Hp]
     int16_t* xn_attn = nullptr;        // [8][Hp] attention-norm output
     int16_t* xn_ffn = nullptr;         // [8][Hp] FFN-norm output
@@ -107,6 +105,15 @@ struct llm_ctx {
     // while that pair is not written again.  pair < 0 means empty.
     struct NormCache { int pair = -1; uint32_t layer = 0; };
     NormCache attn_cache, ffn_cache;
+    // Final RMSNorm of pair `pair` (the last layer's FFN output, `rows`
+    // rows) held in xn_final, whose rows rows..7 are those of pair `src`
+    // (that layer's FFN input): a Task 20 from `pair` into `src` with the
+    // same row count becomes an exchange of buffers.
+    struct FinalCache { int pair = -1, src = -1; uint32_t rows = 0; };
+    FinalCache final_cache;
+    int16_t* xn_final = nullptr;        // [8][Hp]
+    // Pairs whose device address was handed out keep their buffer.
+    std::vector<char> exported;
     std::vector<void*> allocations;
     std::vector<hipEvent_t> events;
     // per-launch timing (measurement only)
@@ -276,6 +283,8 @@ void fill_counters(const llm_ctx* c, uint32_t op, uint32_t R, uint32_t pos,
 void invalidate_pair(llm_ctx* c, int pair) {
     if (c->attn_cache.pair == pair) c->attn_cache.pair = -1;
     if (c->ffn_cache.pair == pair) c->ffn_cache.pair = -1;
+    if (c->final_cache.pair == pair || c->final_cache.src == pair)
+        c->final_cache.pair = c->final_cache.src = -1;
 }
 
 int check_layer_loaded(llm_ctx* c, uint32_t layer, bool attn, bool ffn) {
@@ -297,7 +306,10 @@ int enqueue_attention_sublayer(llm_ctx* c, uint32_t layer, uint32_t R,
     int16_t* out = c->pairs[out_pair];
     const bool cached = c->const_gain > 0 && c->attn_cache.pair == in_pair &&
                         c->attn_cache.layer == layer;
-    if (!cached) {
+    // With a constant gain the projection normalises the raw rows itself
+    // (for one or two rows; larger blocks amortise a separate pass).
+    const bool norm_in = !cached && c->const_gain > 0 && R <= 2;
+    if (!cached && !norm_in) {
         TimedScope ts(c, LLM_K_RMSNORM);
         HIP_TRY(llm::launch_rmsnorm(in, c->Hp,
                                     c->norms + (size_t)(2 * layer) * c->H, c->H,
@@ -307,23 +319,29 @@ int enqueue_attention_sublayer(llm_ctx* c, uint32_t layer, uint32_t R,
     llm::ProjArgs a{};
     a.w0 = mq.d;
     a.steps = mq.steps;
-    a.x = c->xn_attn;
+    a.x = norm_in ? in : c->xn_attn;
     a.ldx = c->Hp;
     a.out = c->qkv;
     a.ldo = c->Nqkv;
     a.n = mq.n;
     a.rows = R;
+    if (norm_in) {
+        a.in_gamma = c->norms + (size_t)(2 * layer) * c->H;
+        a.in_gain = c->const_gain;
+        a.in_cols = c->H;
+    }
     {
         TimedScope ts(c, LLM_K_QKV);
-        HIP_TRY(llm::launch_proj(a, llm::EPI_STORE, mq.L, mq.n_pad / 4, st));
+        HIP_TRY(llm::launch_proj(a, norm_in ? llm::EPI_STORE_NORM_IN : llm::EPI_STORE,
+                                 mq.L, mq.n_pad / 4, st));
     }
     llm::AttnArgs at{};
     at.qkv = c->qkv;
     at.ldqkv = c->Nqkv;
     at.rope = c->rope;
-    at.kcache = c->kcache;
-    at.vcache = c->vcache;
-    at.page_table = c->page_table + (size_t)layer * c->Hkv * c->tiles;
+    const size_t layer_off = (size_t)layer * c->Hkv * c->tiles * llm::kTile * c->d;
+    at.kcache = c->kcache + layer_off;
+    at.vcache = c->vcache + layer_off;
     at.tiles = c->tiles;
     at.pos0 = pos;
     at.num_heads = c->Hq;
@@ -421,11 +439,17 @@ int enqueue_ffn_sublayer(llm_ctx* c, uint32_t layer, uint32_t R, int in_pair,
     dn.n = md.n;
     dn.rows = R;
     const bool next = c->const_gain > 0 && layer + 1 < c->L;
-    if (next) {  // attention norm of the next layer
-        dn.norm_out = c->xn_attn;
+    if (c->const_gain > 0) {
         dn.ldn = c->Hp;
-        dn.norm_gamma = c->norms + (size_t)(2 * (layer + 1)) * c->H;
         dn.norm_gain = c->const_gain;
+        if (next) {  // attention norm of the next layer
+            dn.norm_out = c->xn_attn;
+            dn.norm_gamma = c->norms + (size_t)(2 * (layer + 1)) * c->H;
+        }
+        // final norm (row 2L): a Task 20 may follow any layer's FFN
+        // (run_composed_decoder_stack, host/host_qwen_8x64.cpp:1258-1445)
+        dn.final_out = c->xn_final;
+        dn.final_gamma = c->norms + (size_t)(2 * c->L) * c->H;
     }
     {
         TimedScope ts(c, LLM_K_DOWN);
@@ -433,6 +457,7 @@ int enqueue_ffn_sublayer(llm_ctx* c, uint32_t layer, uint32_t R, int in_pair,
     }
     invalidate_pair(c, out_pair);
     if (next) c->attn_cache = {out_pair, layer + 1};
+    if (c->const_gain > 0) c->final_cache = {out_pair, in_pair, R};
     return 0;
 }
 
@@ -545,26 +570,21 @@ int llm_ctx_create(const llm_shape_t* shape, int device, uint32_t num_pairs,
             hipMemcpy(c->exp14, e14, sizeof(e14), hipMemcpyHostToDevice))
             return cleanup(fail(LLM_E_HIP, "exp table upload"));
     }
-    // paged KV cache: pages of 64 positions per (layer, kv head); the
-    // default page table maps tile t of (layer, head) to page
-    // (layer * Hkv + head) * tiles + t.
+    // KV cache: pages of 64 positions per (layer, kv head); tile t of
+    // (layer, head) is page (layer * Hkv + head) * tiles + t.
     const size_t pages = (size_t)c->L * c->Hkv * c->tiles;
     if ((rc = dev_alloc(c, (void**)&c->kcache, pages * llm::kTile * d * 2)) ||
-        (rc = dev_alloc(c, (void**)&c->vcache, pages * llm::kTile * d * 2)) ||
-        (rc = dev_alloc(c, (void**)&c->page_table, pages * sizeof(int32_t))))
+        (rc = dev_alloc(c, (void**)&c->vcache, pages * llm::kTile * d * 2)))
         return cleanup(rc);
-    c->host_pages.resize(pages);
-    for (size_t i = 0; i < pages; i++) c->host_pages[i] = (int32_t)i;
-    if (hipMemcpy(c->page_table, c->host_pages.data(), pages * 4,
-                  hipMemcpyHostToDevice))
-        return cleanup(fail(LLM_E_HIP, "page table upload"));
     // hidden pairs and scratch
     c->pairs.resize(num_pairs);
     for (auto& p : c->pairs)
         if ((rc = dev_alloc(c, (void**)&p, (size_t)8 * c->Hp * 2)))
             return cleanup(rc);
     const size_t rht = (size_t)8 * c->Hkv * c->tiles * c->G;  // rows*heads*tiles*group
+    c->exported.assign(num_pairs, 0);
     if ((rc = dev_alloc(c, (void**)&c->xn_attn, (size_t)8 * c->Hp * 2)) ||
+        (rc = dev_alloc(c, (void**)&c->xn_final, (size_t)8 * c->Hp * 2)) ||
         (rc = dev_alloc(c, (void**)&c->xn_ffn, (size_t)8 * c->Hp * 2)) ||
         (rc = dev_alloc(c, (void**)&c->qkv, (size_t)8 * c->Nqkv * 2)) ||
         (rc = dev_alloc(c, (void**)&c->attn, (size_t)8 * c->Hp * 2)) ||
@@ -764,7 +784,12 @@ int llm_task(llm_ctx_t* c, uint32_t op, uint32_t layer, uint32_t token_count,
     if (op == LLM_OP_FINAL_NORM) {
         if (token_count == 0) return reject(LLM_STATUS_BAD_TOKEN_COUNT);
         if (!c->norms_loaded) return fail(LLM_E_STATE, "norm table not loaded");
-        {
+        const auto& fc = c->final_cache;
+        if (fc.pair == ip && fc.src == opr && fc.rows == token_count &&
+            !c->exported[opr]) {
+            // xn_final already holds what the norm would leave in out_pair
+            std::swap(c->pairs[opr], c->xn_final);
+        } else {
             TimedScope ts(c, LLM_K_RMSNORM);
             HIP_TRY(llm::launch_rmsnorm(in, c->Hp,
                                         c->norms + (size_t)(2 * c->L) * c->H,
@@ -822,7 +847,7 @@ int kv_transfer(llm_ctx* c, uint32_t layer, uint32_t h, uint32_t pos0,
     for (uint32_t p = pos0; p < pos0 + n;) {
         const uint32_t tile = p / 64, slot0 = p % 64;
         const uint32_t cnt = std::min(64 - slot0, pos0 + n - p);
-        const size_t pg = c->host_pages[((size_t)layer * c->Hkv + h) * c->tiles + tile];
+        const size_t pg = ((size_t)layer * c->Hkv + h) * c->tiles + tile;
         for (int which = 0; which < 2; which++) {
             int16_t* rows = which == 0 ? k : v;
             if (!rows) continue;
@@ -882,6 +907,7 @@ int llm_kv_clear(llm_ctx_t* c) {
 void* llm_pair_device_ptr(llm_ctx_t* c, uint32_t pair) {
     if (!c || pair >= c->pairs.size()) return nullptr;
     invalidate_pair(c, (int)pair);  // the caller may write through it
+    c->exported[pair] = 1;          // and keeps using this address
     return c->pairs[pair];
 }
 

@@ -267,3 +267,64 @@ def test_norm_cache_invalidation():
     _, want18, _ = om.task(kv, 18, 1, h[8:12], 0)
     assert first_mismatch(got19, want19) is None
     assert first_mismatch(got18, want18) is None
+
+
+def test_final_norm_rows_beyond_token_count_unchanged():
+    # Task 20 writes rows < token_count of its output pair and leaves the
+    # other rows as they were, whichever way the library produces it
+    # (buffer exchange after the last layer's FFN, or the norm kernel when
+    # the row count differs or the pair's address was handed out).
+    import llm_accel
+    spec = workloads.CONFIG_A
+    layers = 2
+    synth = workloads.SyntheticModel(spec, layers=layers)
+    om = oracle_from_synthetic(synth, oracle_shape(spec, layers=layers, max_seq=64))
+    kv = om.new_kv()
+    h = synth.hidden_rows(15)
+    final_gamma = synth.norms()[2 * layers]
+
+    def forward(a, x, rows, pos):
+        a.upload(1, x)
+        for layer in range(layers):
+            a.task(18, layer, rows, pos, 1, 0)
+            a.task(19, layer, rows, pos, 0, 1)
+
+    def oracle_forward(x, pos):
+        for layer in range(layers):
+            _, x, _ = om.task(kv, 18, layer, x, pos)
+            _, x, _ = om.task(kv, 19, layer, x, pos)
+        return x
+
+    with llm_accel.Accelerator(accel_shape(spec, layers=layers, max_seq=64)) as a:
+        a.load_model(synth)
+        _say("case final norm exchange P8")
+        forward(a, h[:8], 8, 0)
+        a.task(20, 0, 8, 0, 1, 0)
+        got8 = a.download(0, 8)
+        x8 = oracle_forward(h[:8], 0)
+        assert first_mismatch(got8, orc.rmsnorm(x8, final_gamma)) is None
+        _say("case final norm exchange decode")
+        forward(a, h[8:9], 1, 8)
+        before = a.download(0, 8)
+        a.task(20, 0, 1, 8, 1, 0)
+        after = a.download(0, 8)
+        x9 = oracle_forward(h[8:9], 8)
+        assert first_mismatch(after[:1], orc.rmsnorm(x9, final_gamma)) is None
+        assert first_mismatch(after[1:], before[1:]) is None
+        _say("case final norm row-count mismatch")
+        forward(a, h[9:12], 3, 9)
+        before = a.download(0, 8)
+        a.task(20, 0, 2, 9, 1, 0)
+        after = a.download(0, 8)
+        x12 = oracle_forward(h[9:12], 9)
+        assert first_mismatch(after[:2], orc.rmsnorm(x12[:2], final_gamma)) is None
+        assert first_mismatch(after[2:], before[2:]) is None
+        _say("case final norm exported pair")
+        ptr = llm_accel.lib().llm_pair_device_ptr(a._ctx, 0)
+        assert ptr
+        forward(a, h[12:15], 3, 12)
+        a.task(20, 0, 3, 12, 1, 0)
+        assert llm_accel.lib().llm_pair_device_ptr(a._ctx, 0) == ptr
+        after = a.download(0, 3)
+        x15 = oracle_forward(h[12:15], 12)
+        assert first_mismatch(after, orc.rmsnorm(x15, final_gamma)) is None
