@@ -49,6 +49,7 @@
 // waiting).
 #include "attention.h"
 
+#include "coherent.h"
 #include "fixed_point.h"
 
 namespace llm {
@@ -153,7 +154,7 @@ struct __attribute__((aligned(16))) Smem {
     int16_t app_v[D];        // the appended V row
     int32_t wflags[NW];      // per wave: bit 0 K tile has a value >= 2048,
                              // bit 1 V tile has one
-    int32_t last;            // this workgroup finishes the scan
+    uint32_t last;           // this workgroup finishes the scan
 };
 
 // Each wave publishes whether its lanes staged a saturating K / V value;
@@ -713,7 +714,7 @@ __global__ __launch_bounds__(NT) void attention_pv_kernel(AttnArgs a) {
                 const int32_t pr = lane < tl ? prob(sm.e14, sc[gi] - mn) : 0;
                 put_prob<D>(sm, g, lane, pr);
                 const int32_t ts = wave_sum(pr);
-                if (lane == 0) a.s_tsum[(rh * a.max_tiles + tile) * G + g] = ts;
+                if (lane == 0) st_coherent(&a.s_tsum[(rh * a.max_tiles + tile) * G + g], ts);
             }
         }
         __syncthreads();  // probabilities staged
@@ -722,8 +723,8 @@ __global__ __launch_bounds__(NT) void attention_pv_kernel(AttnArgs a) {
             v4u vr[TILE / 8];
             load_v_row<D>(sm, e, vr);
             const size_t base = (rh * a.max_tiles + tile) * G + g;
-            a.s_tval[base * D + e] =
-                (int16_t)row_pv(sm.p + g * TILE, sm.cp + g * TILE, vr, vcorr);
+            st_coherent(&a.s_tval[base * D + e],
+                        (int16_t)row_pv(sm.p + g * TILE, sm.cp + g * TILE, vr, vcorr));
         }
         __syncthreads();  // tile consumed
         if (threadIdx.x < G) {
@@ -733,15 +734,7 @@ __global__ __launch_bounds__(NT) void attention_pv_kernel(AttnArgs a) {
     }
     if (own / TILE >= t0 && own / TILE < t1) store_appended<D>(a, sm, h, own, false, true);
     // Publish, then let the last chunk of this (row, head) finish.
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const uint32_t prev = atomicAdd(&a.counters[rh], 1u);
-        sm.last = prev == nchunks - 1;
-    }
-    __syncthreads();
-    if (!sm.last) return;
-    __threadfence();
+    if (!arrive_last(&a.counters[rh], nchunks, &sm.last)) return;
     constexpr int SB = 16;  // tiles whose values are in flight together
     for (uint32_t idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
         const uint32_t g = idx / D, e = idx % D;
@@ -753,9 +746,9 @@ __global__ __launch_bounds__(NT) void attention_pv_kernel(AttnArgs a) {
                 const uint32_t j = j0 + u;
                 if (j < ntiles) {
                     const size_t base = (rh * a.max_tiles + j) * G + g;
-                    tv[u] = a.s_tval[base * D + e];
+                    tv[u] = ld_coherent(&a.s_tval[base * D + e]);
                     tmx[u] = a.s_tmax[base];
-                    tsm[u] = a.s_tsum[base];
+                    tsm[u] = ld_coherent(&a.s_tsum[base]);
                 }
             }
 #pragma unroll
@@ -774,7 +767,6 @@ __global__ __launch_bounds__(NT) void attention_pv_kernel(AttnArgs a) {
         a.out[(size_t)t * a.ldo + (size_t)h * G * D + idx] =
             fx_sat16(fx_rnd((int64_t)acc * inv, 16));
     }
-    if (threadIdx.x == 0) a.counters[rh] = 0;  // ready for the next launch
 }
 
 template <int D>

@@ -46,10 +46,44 @@ struct ProjArgs {
     const int16_t* in_gamma;
     int32_t in_gain;
     uint32_t in_cols;
+    // Byte-plane copies of the weights for the matrix-core path ("mfma16x64",
+    // see proj_mfma_kernel) and their per-output (sum hi, sum lo) pairs;
+    // null when absent.  kq = K_pad / 64, nc = N_pad / 16.
+    const int8_t* mf0;
+    const int8_t* mf1;
+    const int32_t* ms0;
+    const int32_t* ms1;
+    uint32_t kq, nc;
+    // Split of the K chunks over workgroups (matrix-core path): partial
+    // sums of part p of chunk c go to mf_part, the last workgroup of a
+    // chunk to arrive (mf_count) finishes it.
+    int32_t* mf_part;
+    uint32_t* mf_count;
 };
+
+// Matrix-core layout: record (c, q) of 2048 bytes holds outputs 16c..16c+15
+// and inputs 64q..64q+63: bytes [0, 1024) the high bytes w >> 8, bytes
+// [1024, 2048) the low bytes (w & 255) - 128, both as int8; lane l, byte b
+// of a plane is output 16c + l % 16, input 64q + 16 (l / 16) + b.  Records
+// are ordered [c][q].
+constexpr uint32_t kMfRows = 16;
+constexpr uint32_t kMfCols = 64;
+constexpr uint32_t kMfRecord = 2048;
 
 hipError_t launch_copy(const uint4* src, uint4* dst, size_t n16,
                        hipStream_t st);
+// Blocks of at least kMfMinRows rows run on the matrix cores when the
+// byte-plane layout is present; others on the VALU dot2 kernel.
+constexpr uint32_t kMfMinRows = 3;
+// Workgroup shape of the matrix-core kernel for a matrix: KS wavefronts
+// per workgroup, P workgroups per 16-output chunk.
+struct MfSplit {
+    uint32_t ks, parts;
+};
+MfSplit mf_split(uint32_t nc, uint32_t kq);
+// int32 words of partial sums per (chunk, part) record.
+constexpr uint32_t mf_part_words(uint32_t nm) { return nm * 3 * 256 + 32; }
+bool proj_uses_mfma(const ProjArgs& a, int epi);
 hipError_t launch_proj(const ProjArgs& a, int epi, int L, uint32_t blocks,
                        hipStream_t st);
 // RMSNorm of `rows` rows; const_gain > 0 selects the elementwise kernel

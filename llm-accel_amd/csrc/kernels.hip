@@ -10,6 +10,7 @@
 //            to a multiple of 4 and K to a multiple of 128 with zeros.
 #include "kernels.h"
 
+#include "coherent.h"
 #include "fixed_point.h"
 
 namespace llm {
@@ -94,6 +95,28 @@ __device__ __forceinline__ uint4 norm8(uint4 x, uint4 g, int32_t gain) {
         w[i] = (uint32_t)(uint16_t)lo | ((uint32_t)hi << 16);
     }
     return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// Output (r, n) of a projection from its exact sums (gate and up for
+// EPI_SILU): the reference's narrowing, then the epilogue.
+template <int EPI>
+__device__ __forceinline__ void proj_out(const ProjArgs& a, uint32_t r, uint32_t n,
+                                         int64_t t0, int64_t t1) {
+    int16_t y = fx_narrow_projection(t0);
+    if (EPI == EPI_RESID) {
+        y = fx_sat16((int32_t)y + a.res[(size_t)r * a.ldr + n]);
+        if (a.norm_out)
+            a.norm_out[(size_t)r * a.ldn + n] = fx_sat16(fx_rnd(
+                (int64_t)y * a.norm_gain * a.norm_gamma[n], 16));
+        if (a.final_out)
+            a.final_out[(size_t)r * a.ldn + n] = fx_sat16(fx_rnd(
+                (int64_t)y * a.norm_gain * a.final_gamma[n], 16));
+    } else if (EPI == EPI_SILU) {
+        const int16_t up = fx_narrow_projection(t1);
+        const int16_t sg = fx_silu(y, a.exp8);
+        y = fx_sat16(fx_rnd((int64_t)sg * up, 8));
+    }
+    a.out[(size_t)r * a.ldo + n] = y;
 }
 
 template <int RT, int L, int EPI>
@@ -197,21 +220,7 @@ __global__ __launch_bounds__(256) void proj_kernel(ProjArgs a) {
             for (int m = 0; m < NM; m++)
                 tot[m] = red[0][m][ii][r] + red[1][m][ii][r] +
                          red[2][m][ii][r] + red[3][m][ii][r];
-            int16_t y = fx_narrow_projection(tot[0]);
-            if (EPI == EPI_RESID) {
-                y = fx_sat16((int32_t)y + a.res[(size_t)r * a.ldr + n]);
-                if (a.norm_out)
-                    a.norm_out[(size_t)r * a.ldn + n] = fx_sat16(fx_rnd(
-                        (int64_t)y * a.norm_gain * a.norm_gamma[n], 16));
-                if (a.final_out)
-                    a.final_out[(size_t)r * a.ldn + n] = fx_sat16(fx_rnd(
-                        (int64_t)y * a.norm_gain * a.final_gamma[n], 16));
-            } else if (EPI == EPI_SILU) {
-                int16_t up = fx_narrow_projection(tot[NM - 1]);
-                int16_t sg = fx_silu(y, a.exp8);
-                y = fx_sat16(fx_rnd((int64_t)sg * up, 8));
-            }
-            a.out[(size_t)r * a.ldo + n] = y;
+            proj_out<EPI>(a, r, n, tot[0], tot[NM - 1]);
         }
     }
     if (EPI == EPI_RESID && a.final_out && t < 32) {
@@ -219,6 +228,181 @@ __global__ __launch_bounds__(256) void proj_kernel(ProjArgs a) {
         const uint32_t n = b * 4 + ii;
         if ((uint32_t)r >= a.rows && n < a.n)
             a.final_out[(size_t)r * a.ldn + n] = a.res[(size_t)r * a.ldr + n];
+    }
+}
+
+// ---------------------------------------------------------------------
+// Projection on the matrix cores, for blocks of several rows.
+//
+// int16 operands are split into bytes, w = 256 a + b + 128 and
+// x = 256 c + d + 128 with a = w >> 8 and b = (w & 255) - 128 in [-128, 127]
+// (likewise c, d), so that
+//   sum w x = 65536 sum ac + 256 (sum ad + sum bc) + sum bd
+//           + 32768 sum a + 128 sum b + 32768 sum c + 128 sum d + 16384 K
+// over the padded K (zero weights pad; whatever the activations hold there
+// enters both sides alike).  The three sums of products run on
+// v_mfma_i32_16x16x64_i8 (A = 16 activation rows, rows >= `rows` zero;
+// B = 16 outputs), each bounded by 2^15 K < 2^31 for K <= 32768; the
+// weight sums come with the layout, the activation sums from v_dot4.
+// Workgroup = KS wavefronts on one 16-output chunk, splitting the K
+// chunks; LDS reduction, then the shared epilogue.
+// ---------------------------------------------------------------------
+typedef int32_t v4i __attribute__((ext_vector_type(4)));
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+
+// 16 int16 activations (two 16-byte loads) -> high bytes and biased low
+// bytes, element e in byte e.
+__device__ __forceinline__ void split16(const v4u& x0, const v4u& x1, v4i& hi, v4i& lo) {
+    hi.x = (int32_t)__builtin_amdgcn_perm(x0.y, x0.x, 0x07050301u);
+    hi.y = (int32_t)__builtin_amdgcn_perm(x0.w, x0.z, 0x07050301u);
+    hi.z = (int32_t)__builtin_amdgcn_perm(x1.y, x1.x, 0x07050301u);
+    hi.w = (int32_t)__builtin_amdgcn_perm(x1.w, x1.z, 0x07050301u);
+    lo.x = (int32_t)(__builtin_amdgcn_perm(x0.y, x0.x, 0x06040200u) ^ 0x80808080u);
+    lo.y = (int32_t)(__builtin_amdgcn_perm(x0.w, x0.z, 0x06040200u) ^ 0x80808080u);
+    lo.z = (int32_t)(__builtin_amdgcn_perm(x1.y, x1.x, 0x06040200u) ^ 0x80808080u);
+    lo.w = (int32_t)(__builtin_amdgcn_perm(x1.w, x1.z, 0x06040200u) ^ 0x80808080u);
+}
+__device__ __forceinline__ int32_t byte_sum(const v4i& v, int32_t acc) {
+    acc = __builtin_amdgcn_sdot4(v.x, 0x01010101, acc, false);
+    acc = __builtin_amdgcn_sdot4(v.y, 0x01010101, acc, false);
+    acc = __builtin_amdgcn_sdot4(v.z, 0x01010101, acc, false);
+    return __builtin_amdgcn_sdot4(v.w, 0x01010101, acc, false);
+}
+
+template <int NM, int KS, int EPI>
+__global__ __launch_bounds__(64 * KS) void proj_mfma_kernel(ProjArgs a, uint32_t parts) {
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t c = blockIdx.x / parts, p = blockIdx.x % parts, KQ = a.kq;
+    const uint32_t pq0 = p * KQ / parts, pq1 = (p + 1) * KQ / parts;
+    const uint32_t q0 = pq0 + wave * (pq1 - pq0) / KS;
+    const uint32_t q1 = pq0 + (wave + 1) * (pq1 - pq0) / KS;
+    const uint32_t i = lane & 15, g = lane >> 4;
+    const bool xrow = i < a.rows;
+    const int16_t* xp = a.x + (size_t)(xrow ? i : 0) * a.ldx + 16 * g;
+    const int8_t* bp[NM];
+    bp[0] = a.mf0 + (size_t)c * KQ * kMfRecord + lane * 16;
+    if (NM == 2) bp[NM - 1] = a.mf1 + (size_t)c * KQ * kMfRecord + lane * 16;
+    v4i cac[NM], cmix[NM], cbd[NM];
+#pragma unroll
+    for (int m = 0; m < NM; m++) cac[m] = cmix[m] = cbd[m] = v4i{0, 0, 0, 0};
+    int32_t sc = 0, sd = 0;
+#pragma unroll 4
+    for (uint32_t q = q0; q < q1; q++) {
+        v4i bh[NM], bl[NM];
+#pragma unroll
+        for (int m = 0; m < NM; m++) {
+            bh[m] = *(const v4i*)(bp[m] + (size_t)q * kMfRecord);
+            bl[m] = *(const v4i*)(bp[m] + (size_t)q * kMfRecord + 1024);
+        }
+        v4u x0 = v4u{0, 0, 0, 0}, x1 = x0;
+        if (xrow) {
+            x0 = *(const v4u*)(xp + 64 * q);
+            x1 = *(const v4u*)(xp + 64 * q + 8);
+        }
+        v4i ah, al;
+        split16(x0, x1, ah, al);
+        sc = byte_sum(ah, sc);
+        sd = byte_sum(al, sd);
+#pragma unroll
+        for (int m = 0; m < NM; m++) {
+            cac[m] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, bh[m], cac[m], 0, 0, 0);
+            cmix[m] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, bl[m], cmix[m], 0, 0, 0);
+            cmix[m] = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, bh[m], cmix[m], 0, 0, 0);
+            cbd[m] = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, bl[m], cbd[m], 0, 0, 0);
+        }
+    }
+    // C lane l holds rows 4 (l / 16) + s, column l % 16.
+    __shared__ v4i red[KS][NM][3][64];
+    __shared__ int32_t rsum[KS][2][64];
+    __shared__ uint32_t last;
+#pragma unroll
+    for (int m = 0; m < NM; m++) {
+        red[wave][m][0][lane] = cac[m];
+        red[wave][m][1][lane] = cmix[m];
+        red[wave][m][2][lane] = cbd[m];
+    }
+    rsum[wave][0][lane] = sc;
+    rsum[wave][1][lane] = sd;
+    __syncthreads();
+    // This workgroup's sums of element t = 16 r + j: [m][type] and the
+    // activation row sums, in int32 (each below 2^15 * K).
+    constexpr uint32_t W = mf_part_words(NM);
+    int32_t* part = a.mf_part + (size_t)(c * parts + p) * W;
+    if (parts > 1) {
+        for (uint32_t t = threadIdx.x; t < 256; t += 64 * KS) {
+            const uint32_t r = t >> 4, j = t & 15, cl = 16 * (r >> 2) + j, s = r & 3;
+#pragma unroll
+            for (int m = 0; m < NM; m++)
+#pragma unroll
+                for (int ty = 0; ty < 3; ty++) {
+                    int32_t v = 0;
+#pragma unroll
+                    for (int w = 0; w < KS; w++) v += red[w][m][ty][cl][s];
+                    st_coherent(&part[(m * 3 + ty) * 256 + t], v);
+                }
+            if (j < 2) {
+                int32_t v = 0;
+#pragma unroll
+                for (int w = 0; w < KS; w++)
+#pragma unroll
+                    for (int gg = 0; gg < 4; gg++) v += rsum[w][j][r + 16 * gg];
+                st_coherent(&part[NM * 3 * 256 + 2 * r + j], v);
+            }
+        }
+        if (!arrive_last(&a.mf_count[c], parts, &last)) return;
+    }
+    const int64_t k64 = (int64_t)KQ * kMfCols;
+    for (uint32_t t = threadIdx.x; t < 256; t += 64 * KS) {
+        const uint32_t r = t >> 4, j = t & 15, n = c * kMfRows + j;
+        if (n >= a.n) continue;
+        if (r < a.rows) {
+            const uint32_t cl = 16 * (r >> 2) + j, s = r & 3;
+            int64_t sums[NM][3], rc = 0, rd = 0;
+            if (parts > 1) {
+#pragma unroll
+                for (int m = 0; m < NM; m++)
+#pragma unroll
+                    for (int ty = 0; ty < 3; ty++) sums[m][ty] = 0;
+                for (uint32_t pp = 0; pp < parts; pp++) {
+                    const int32_t* q = a.mf_part + (size_t)(c * parts + pp) * W;
+#pragma unroll
+                    for (int m = 0; m < NM; m++)
+#pragma unroll
+                        for (int ty = 0; ty < 3; ty++)
+                            sums[m][ty] += ld_coherent(&q[(m * 3 + ty) * 256 + t]);
+                    rc += ld_coherent(&q[NM * 3 * 256 + 2 * r]);
+                    rd += ld_coherent(&q[NM * 3 * 256 + 2 * r + 1]);
+                }
+            } else {
+#pragma unroll
+                for (int m = 0; m < NM; m++)
+#pragma unroll
+                    for (int ty = 0; ty < 3; ty++) {
+                        int64_t v = 0;
+#pragma unroll
+                        for (int w = 0; w < KS; w++) v += red[w][m][ty][cl][s];
+                        sums[m][ty] = v;
+                    }
+#pragma unroll
+                for (int w = 0; w < KS; w++)
+#pragma unroll
+                    for (int gg = 0; gg < 4; gg++) {
+                        rc += rsum[w][0][r + 16 * gg];
+                        rd += rsum[w][1][r + 16 * gg];
+                    }
+            }
+            int64_t tot[NM];
+#pragma unroll
+            for (int m = 0; m < NM; m++) {
+                const int32_t* ms = m == 0 ? a.ms0 : a.ms1;
+                tot[m] = 65536 * sums[m][0] + 256 * sums[m][1] + sums[m][2] +
+                         32768 * (int64_t)ms[2 * n] + 128 * (int64_t)ms[2 * n + 1] +
+                         32768 * rc + 128 * rd + 16384 * k64;
+            }
+            proj_out<EPI>(a, r, n, tot[0], tot[NM - 1]);
+        } else if (EPI == EPI_RESID && a.final_out && r < 8) {
+            a.final_out[(size_t)r * a.ldn + n] = a.res[(size_t)r * a.ldr + n];
+        }
     }
 }
 
@@ -258,8 +442,38 @@ static hipError_t launch_proj_epi(const ProjArgs& a, int L, uint32_t blocks,
     return launch_proj_rt<8, EPI>(a, L, blocks, st);
 }
 
+MfSplit mf_split(uint32_t nc, uint32_t kq) {
+    // about 512 workgroups, at least two K chunks per wavefront
+    MfSplit s{4, 1};
+    while (nc * s.parts < 512 && kq / (s.parts * 2) >= s.ks * 2) s.parts *= 2;
+    if (kq / s.parts >= 8 * 4) s.ks = 8;
+    return s;
+}
+
+template <int NM, int EPI>
+static hipError_t launch_mfma_epi(const ProjArgs& a, hipStream_t st) {
+    const MfSplit sp = mf_split(a.nc, a.kq);
+    if (sp.ks == 8)
+        proj_mfma_kernel<NM, 8, EPI><<<a.nc * sp.parts, 64 * 8, 0, st>>>(a, sp.parts);
+    else
+        proj_mfma_kernel<NM, 4, EPI><<<a.nc * sp.parts, 64 * 4, 0, st>>>(a, sp.parts);
+    return hipGetLastError();
+}
+
+bool proj_uses_mfma(const ProjArgs& a, int epi) {
+    return a.rows >= kMfMinRows && a.mf0 && a.mf_part && epi != EPI_STORE_NORM_IN &&
+           a.kq * kMfCols <= 32768;
+}
+
 hipError_t launch_proj(const ProjArgs& a, int epi, int L, uint32_t blocks,
                        hipStream_t st) {
+    if (proj_uses_mfma(a, epi)) {
+        switch (epi) {
+        case EPI_STORE: return launch_mfma_epi<1, EPI_STORE>(a, st);
+        case EPI_RESID: return launch_mfma_epi<1, EPI_RESID>(a, st);
+        default: return launch_mfma_epi<2, EPI_SILU>(a, st);
+        }
+    }
     switch (epi) {
     case EPI_STORE: return launch_proj_epi<EPI_STORE>(a, L, blocks, st);
     case EPI_RESID: return launch_proj_epi<EPI_RESID>(a, L, blocks, st);

@@ -45,6 +45,12 @@ uint64_t cdiv(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
 struct Matrix {
     int16_t* d = nullptr;
     uint32_t n = 0, k = 0, n_pad = 0, k_pad = 0, steps = 0;
+    // matrix-core copy: byte-plane records and (sum hi, sum lo) per output
+    int8_t* mf = nullptr;
+    int32_t* ms = nullptr;
+    uint32_t nc = 0, kq = 0;
+    int32_t* ctx_part = nullptr;     // the context's split scratch
+    uint32_t* ctx_count = nullptr;
     int maxw[3] = {0, 0, 0};  // per stored projection (qkv keeps three)
     int L = 16;               // int32 widening interval in k-steps
     size_t elems() const { return (size_t)n_pad * k_pad; }
@@ -112,6 +118,9 @@ struct llm_ctx {
     struct FinalCache { int pair = -1, src = -1; uint32_t rows = 0; };
     FinalCache final_cache;
     int16_t* xn_final = nullptr;        // [8][Hp]
+    // partial sums / arrival counters of the split matrix-core projection
+    int32_t* mf_part = nullptr;
+    uint32_t* mf_count = nullptr;
     // Pairs whose device address was handed out keep their buffer.
     std::vector<char> exported;
     std::vector<void*> allocations;
@@ -220,6 +229,40 @@ int upload_rows(llm_ctx* c, Matrix& m, uint32_t row0, uint32_t rows,
     const size_t off = (size_t)(row0 / 4) * S * 512;
     HIP_TRY(hipMemcpy(m.d + off, buf.data(), buf.size() * sizeof(int16_t),
                       hipMemcpyHostToDevice));
+    if (m.mf) {
+        // byte-plane records of the chunks these rows cover
+        if (row0 % llm::kMfRows != 0)
+            return fail(LLM_E_ARG, "projection rows not aligned to 16");
+        const uint32_t c0 = row0 / llm::kMfRows;
+        const uint32_t c1 = (uint32_t)cdiv(row0 + rows, llm::kMfRows);
+        const uint32_t KQ = m.kq;
+        std::vector<int8_t> rec((size_t)(c1 - c0) * KQ * llm::kMfRecord);
+        std::vector<int32_t> sums((size_t)(c1 - c0) * llm::kMfRows * 2, 0);
+        for (uint32_t cc = c0; cc < c1; cc++)
+            for (uint32_t jj = 0; jj < llm::kMfRows; jj++) {
+                const uint32_t local = cc * llm::kMfRows + jj - row0;
+                const bool valid = local < rows;
+                int32_t* sm = &sums[((size_t)(cc - c0) * llm::kMfRows + jj) * 2];
+                for (uint32_t q = 0; q < KQ; q++)
+                    for (uint32_t g = 0; g < 4; g++)
+                        for (uint32_t b = 0; b < 16; b++) {
+                            const uint32_t k = q * llm::kMfCols + 16 * g + b;
+                            const int32_t v = valid && k < m.k ? w[(size_t)local * m.k + k] : 0;
+                            const int8_t hi = (int8_t)(v >> 8);
+                            const int8_t lo = (int8_t)((v & 255) ^ 0x80);
+                            const size_t o = ((size_t)(cc - c0) * KQ + q) * llm::kMfRecord +
+                                             (16 * g + jj) * 16 + b;
+                            rec[o] = hi;
+                            rec[o + 1024] = lo;
+                            sm[0] += hi;
+                            sm[1] += lo;
+                        }
+            }
+        HIP_TRY(hipMemcpy(m.mf + (size_t)c0 * KQ * llm::kMfRecord, rec.data(),
+                          rec.size(), hipMemcpyHostToDevice));
+        HIP_TRY(hipMemcpy(m.ms + (size_t)c0 * llm::kMfRows * 2, sums.data(),
+                          sums.size() * sizeof(int32_t), hipMemcpyHostToDevice));
+    }
     m.maxw[which] = maxw;
     m.L = widening_interval(std::max({m.maxw[0], m.maxw[1], m.maxw[2]}));
     return 0;
@@ -299,6 +342,20 @@ int check_layer_loaded(llm_ctx* c, uint32_t layer, bool attn, bool ffn) {
     return 0;
 }
 
+// Matrix-core copies of the matrix (and of the up matrix for gate|up).
+void set_mf(llm::ProjArgs& a, const Matrix& m, const Matrix* m2 = nullptr) {
+    a.mf_part = m.ctx_part;
+    a.mf_count = m.ctx_count;
+    a.mf0 = m.mf;
+    a.ms0 = m.ms;
+    a.kq = m.kq;
+    a.nc = m.nc;
+    if (m2) {
+        a.mf1 = m2->mf;
+        a.ms1 = m2->ms;
+    }
+}
+
 int enqueue_attention_sublayer(llm_ctx* c, uint32_t layer, uint32_t R,
                                uint32_t pos, int in_pair, int out_pair) {
     hipStream_t st = c->stream;
@@ -325,6 +382,7 @@ int enqueue_attention_sublayer(llm_ctx* c, uint32_t layer, uint32_t R,
     a.ldo = c->Nqkv;
     a.n = mq.n;
     a.rows = R;
+    set_mf(a, mq);
     if (norm_in) {
         a.in_gamma = c->norms + (size_t)(2 * layer) * c->H;
         a.in_gain = c->const_gain;
@@ -380,6 +438,7 @@ int enqueue_attention_sublayer(llm_ctx* c, uint32_t layer, uint32_t R,
     o.ldr = c->Hp;
     o.n = mo.n;
     o.rows = R;
+    set_mf(o, mo);
     if (c->const_gain > 0) {  // FFN norm of this sublayer's output
         o.norm_out = c->xn_ffn;
         o.ldn = c->Hp;
@@ -421,6 +480,7 @@ int enqueue_ffn_sublayer(llm_ctx* c, uint32_t layer, uint32_t R, int in_pair,
     a.n = mg.n;
     a.rows = R;
     a.exp8 = c->exp8;
+    set_mf(a, mg, &mu);
     {
         TimedScope ts(c, LLM_K_GATEUP);
         HIP_TRY(llm::launch_proj(a, llm::EPI_SILU, std::min(mg.L, mu.L),
@@ -438,6 +498,7 @@ int enqueue_ffn_sublayer(llm_ctx* c, uint32_t layer, uint32_t R, int in_pair,
     dn.ldr = c->Hp;
     dn.n = md.n;
     dn.rows = R;
+    set_mf(dn, md);
     const bool next = c->const_gain > 0 && layer + 1 < c->L;
     if (c->const_gain > 0) {
         dn.ldn = c->Hp;
@@ -540,6 +601,14 @@ int llm_ctx_create(const llm_shape_t* shape, int device, uint32_t num_pairs,
     for (auto& mt : c->mats) {
         mt.d = c->arena + off;
         off += mt.elems();
+        // byte-plane copy for multi-row blocks on the matrix cores
+        mt.nc = (uint32_t)cdiv(mt.n, llm::kMfRows);
+        mt.kq = (uint32_t)cdiv(mt.k, llm::kMfCols);
+        if ((rc = dev_alloc(c, (void**)&mt.mf, (size_t)mt.nc * mt.kq * llm::kMfRecord)) ||
+            (rc = dev_alloc(c, (void**)&mt.ms, (size_t)mt.nc * llm::kMfRows * 2 * 4)))
+            return cleanup(rc);
+        if (hipMemset(mt.ms, 0, (size_t)mt.nc * llm::kMfRows * 2 * 4) != hipSuccess)
+            return cleanup(fail(LLM_E_HIP, "hipMemset failed"));
     }
     // tables
     if ((rc = dev_alloc(c, (void**)&c->norms,
@@ -595,6 +664,26 @@ int llm_ctx_create(const llm_shape_t* shape, int device, uint32_t num_pairs,
         (rc = dev_alloc(c, (void**)&c->s_tval, rht * d * 2)) ||
         (rc = dev_alloc(c, (void**)&c->counters, (size_t)8 * c->Hkv * 4)))
         return cleanup(rc);
+    {
+        // split matrix-core scratch: the largest (chunks x parts x record)
+        size_t words = 0, chunks = 0;
+        for (uint32_t m = 0; m < M_COUNT; m++) {
+            const Matrix& mt = c->mat(0, m);
+            const llm::MfSplit sp = llm::mf_split(mt.nc, mt.kq);
+            const uint32_t nm = (m == M_GATE || m == M_UP) ? 2 : 1;
+            words = std::max(words, (size_t)mt.nc * sp.parts * llm::mf_part_words(nm));
+            chunks = std::max(chunks, (size_t)mt.nc);
+        }
+        if ((rc = dev_alloc(c, (void**)&c->mf_part, words * 4)) ||
+            (rc = dev_alloc(c, (void**)&c->mf_count, chunks * 4)))
+            return cleanup(rc);
+        if (hipMemset(c->mf_count, 0, chunks * 4) != hipSuccess)
+            return cleanup(fail(LLM_E_HIP, "hipMemset failed"));
+        for (auto& mt : c->mats) {
+            mt.ctx_part = c->mf_part;
+            mt.ctx_count = c->mf_count;
+        }
+    }
     if (fx_recip(fx_sat16((int64_t)c->H * 256)) == 0)
         c->const_gain = fx_rmsnorm_gain(0, c->H);
     *out = c;
@@ -976,6 +1065,7 @@ int llm_bench_projection(llm_ctx_t* c, uint32_t kernel, uint32_t rows,
             const Matrix& m = c->mat(layer, M_QKV);
             a.w0 = m.d; a.steps = m.steps; a.x = c->xn_attn; a.ldx = c->Hp;
             a.out = c->qkv; a.ldo = c->Nqkv; a.n = m.n; L = m.L; blocks = m.n_pad / 4;
+            set_mf(a, m);
         } else if (kernel == LLM_K_OPROJ || kernel == LLM_K_DOWN) {
             const Matrix& m = c->mat(layer, kernel == LLM_K_OPROJ ? M_O : M_DOWN);
             a.w0 = m.d; a.steps = m.steps;
@@ -984,6 +1074,7 @@ int llm_bench_projection(llm_ctx_t* c, uint32_t kernel, uint32_t rows,
             // output into a buffer the launch does not read
             a.out = c->qkv; a.ldo = c->Nqkv; a.res = c->xn_ffn; a.ldr = c->Hp;
             a.n = m.n; L = m.L; blocks = m.n_pad / 4; epi = llm::EPI_RESID;
+            set_mf(a, m);
         } else {
             const Matrix& g = c->mat(layer, M_GATE);
             const Matrix& u = c->mat(layer, M_UP);
@@ -991,6 +1082,7 @@ int llm_bench_projection(llm_ctx_t* c, uint32_t kernel, uint32_t rows,
             a.ldx = c->Hp; a.out = c->act; a.ldo = c->Ip; a.n = g.n;
             a.exp8 = c->exp8; L = std::min(g.L, u.L); blocks = g.n_pad / 4;
             epi = llm::EPI_SILU;
+            set_mf(a, g, &u);
         }
         return llm::launch_proj(a, epi, L, blocks, c->stream);
     };

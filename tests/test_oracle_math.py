@@ -359,3 +359,33 @@ def test_status_validation_order():
         c, _, st = m.task(kv, op, layer, h, pos, token_count=rows)
         assert (st.op, st.code, c, st.last_task) == (sop, code, code, 1)
         assert st.token_count == rows
+
+
+def test_byte_split_dot_product_identity():
+    """The matrix-core projection computes sum w*x from byte planes:
+    w = 256a + b + 128, x = 256c + d + 128 with a = w >> 8,
+    b = (w & 255) - 128 (c, d likewise), all in [-128, 127], and
+    sum wx = 65536 sum ac + 256 (sum ad + sum bc) + sum bd + 32768 sum a
+             + 128 sum b + 32768 sum c + 128 sum d + 16384 K.
+    Checked on random and extreme int16 vectors against the direct sum."""
+    rng = np.random.default_rng(11)
+    extremes = np.array([-32768, -32767, -256, -129, -128, -1, 0, 1, 127,
+                         128, 255, 256, 32512, 32639, 32640, 32767], np.int64)
+    for trial in range(200):
+        k = int(rng.integers(1, 300))
+        if trial % 3 == 0:
+            w = rng.choice(extremes, k)
+            x = rng.choice(extremes, k)
+        else:
+            w = rng.integers(-32768, 32768, k)
+            x = rng.integers(-32768, 32768, k)
+        a, b = w >> 8, (w & 255) - 128
+        c, d = x >> 8, (x & 255) - 128
+        for v in (a, b, c, d):
+            assert v.min() >= -128 and v.max() <= 127
+        got = (65536 * (a * c).sum() + 256 * ((a * d).sum() + (b * c).sum())
+               + (b * d).sum() + 32768 * a.sum() + 128 * b.sum()
+               + 32768 * c.sum() + 128 * d.sum() + 16384 * k)
+        assert got == int((w * x).sum())
+        # bounds the kernel relies on: each plane product <= 2^14 in size
+        assert np.abs(a * c).max() <= 1 << 14
