@@ -13,6 +13,26 @@
 #include "coherent.h"
 #include "fixed_point.h"
 
+// Launch shapes (measured choices; overridable at build time for sweeps).
+#ifndef LLM_PROJ_WPB
+#define LLM_PROJ_WPB 4      // wavefronts per 4-row block (VALU kernel)
+#endif
+#ifndef LLM_PROJ_WPB_SILU
+#define LLM_PROJ_WPB_SILU 8 // the same for gate|up (twice the loads per step)
+#endif
+#ifndef LLM_PROJ_UNROLL
+#define LLM_PROJ_UNROLL 2   // k-steps whose loads are issued together
+#endif
+#ifndef LLM_MF_LOADFIRST
+#define LLM_MF_LOADFIRST 0  // matrix-core kernel: all loads before products
+#endif
+#ifndef LLM_MF_WG_TARGET
+#define LLM_MF_WG_TARGET 256  // matrix-core kernel: workgroups to aim for
+#endif
+#ifndef LLM_MF_KS_MAX
+#define LLM_MF_KS_MAX 16    // matrix-core kernel: wavefronts per workgroup
+#endif
+
 namespace llm {
 
 typedef short s16x2 __attribute__((ext_vector_type(2)));
@@ -119,14 +139,14 @@ __device__ __forceinline__ void proj_out(const ProjArgs& a, uint32_t r, uint32_t
     a.out[(size_t)r * a.ldo + n] = y;
 }
 
-template <int RT, int L, int EPI>
-__global__ __launch_bounds__(256) void proj_kernel(ProjArgs a) {
+template <int RT, int L, int EPI, int WPB>
+__global__ __launch_bounds__(64 * WPB) void proj_kernel(ProjArgs a) {
     constexpr int NM = EPI == EPI_SILU ? 2 : 1;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int i = lane >> 4, j = lane & 15;
     const uint32_t b = blockIdx.x;
     const uint32_t S = a.steps;
-    const uint32_t s0 = wave * S / 4, s1 = (wave + 1) * S / 4;
+    const uint32_t s0 = wave * S / WPB, s1 = (wave + 1) * S / WPB;
 
     int64_t acc[NM][RT];
     int32_t part[NM][RT];
@@ -142,7 +162,7 @@ __global__ __launch_bounds__(256) void proj_kernel(ProjArgs a) {
 
     for (uint32_t s = s0; s < s1;) {
         const uint32_t lim = (L == 0) ? s1 : (s + L < s1 ? s + L : s1);
-#pragma unroll 2
+#pragma unroll LLM_PROJ_UNROLL
         for (; s < lim; s++) {
             uint4 wv[NM];
             wv[0] = *(const uint4*)(wp0);
@@ -202,7 +222,7 @@ __global__ __launch_bounds__(256) void proj_kernel(ProjArgs a) {
             for (int off = 8; off > 0; off >>= 1)
                 acc[m][r] += __shfl_xor(acc[m][r], off, 64);
 
-    __shared__ int64_t red[4][NM][4][RT];
+    __shared__ int64_t red[WPB][NM][4][RT];
     if (j == 0) {
 #pragma unroll
         for (int m = 0; m < NM; m++)
@@ -217,9 +237,11 @@ __global__ __launch_bounds__(256) void proj_kernel(ProjArgs a) {
         if ((uint32_t)r < a.rows && n < a.n) {
             int64_t tot[NM];
 #pragma unroll
-            for (int m = 0; m < NM; m++)
-                tot[m] = red[0][m][ii][r] + red[1][m][ii][r] +
-                         red[2][m][ii][r] + red[3][m][ii][r];
+            for (int m = 0; m < NM; m++) {
+                tot[m] = 0;
+#pragma unroll
+                for (int w = 0; w < WPB; w++) tot[m] += red[w][m][ii][r];
+            }
             proj_out<EPI>(a, r, n, tot[0], tot[NM - 1]);
         }
     }
@@ -269,7 +291,38 @@ __device__ __forceinline__ int32_t byte_sum(const v4i& v, int32_t acc) {
     return __builtin_amdgcn_sdot4(v.w, 0x01010101, acc, false);
 }
 
-template <int NM, int KS, int EPI>
+// One K chunk: activations (normalised first for EPI_STORE_NORM_IN) split
+// into bytes, their sums, and the four products per matrix.
+template <int NM, int EPI>
+__device__ __forceinline__ void mf_chunk(const ProjArgs& a, uint32_t q, uint32_t g,
+                                         v4u x0, v4u x1, const v4i* bh, const v4i* bl,
+                                         v4i* cac, v4i* cmix, v4i* cbd,
+                                         int32_t& sc, int32_t& sd) {
+    if (EPI == EPI_STORE_NORM_IN) {
+        const uint32_t k0 = 64 * q + 16 * g;
+        const uint4 ga = k0 < a.in_cols ? *(const uint4*)(a.in_gamma + k0)
+                                        : make_uint4(0, 0, 0, 0);
+        const uint4 gb = k0 + 8 < a.in_cols ? *(const uint4*)(a.in_gamma + k0 + 8)
+                                            : make_uint4(0, 0, 0, 0);
+        const uint4 n0 = norm8(make_uint4(x0.x, x0.y, x0.z, x0.w), ga, a.in_gain);
+        const uint4 n1 = norm8(make_uint4(x1.x, x1.y, x1.z, x1.w), gb, a.in_gain);
+        x0 = v4u{n0.x, n0.y, n0.z, n0.w};
+        x1 = v4u{n1.x, n1.y, n1.z, n1.w};
+    }
+    v4i ah, al;
+    split16(x0, x1, ah, al);
+    sc = byte_sum(ah, sc);
+    sd = byte_sum(al, sd);
+#pragma unroll
+    for (int m = 0; m < NM; m++) {
+        cac[m] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, bh[m], cac[m], 0, 0, 0);
+        cmix[m] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, bl[m], cmix[m], 0, 0, 0);
+        cmix[m] = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, bh[m], cmix[m], 0, 0, 0);
+        cbd[m] = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, bl[m], cbd[m], 0, 0, 0);
+    }
+}
+
+template <int NM, int KS, int QM, int EPI>
 __global__ __launch_bounds__(64 * KS) void proj_mfma_kernel(ProjArgs a, uint32_t parts) {
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t c = blockIdx.x / parts, p = blockIdx.x % parts, KQ = a.kq;
@@ -286,6 +339,34 @@ __global__ __launch_bounds__(64 * KS) void proj_mfma_kernel(ProjArgs a, uint32_t
 #pragma unroll
     for (int m = 0; m < NM; m++) cac[m] = cmix[m] = cbd[m] = v4i{0, 0, 0, 0};
     int32_t sc = 0, sd = 0;
+#if LLM_MF_LOADFIRST
+    // every load of this wavefront's K chunks is issued before the first
+    // product (q1 - q0 <= QM)
+    v4i bh[QM][NM], bl[QM][NM];
+    v4u x0[QM], x1[QM];
+#pragma unroll
+    for (int u = 0; u < QM; u++) {
+        const uint32_t q = q0 + u;
+        if (q < q1) {
+#pragma unroll
+            for (int m = 0; m < NM; m++) {
+                bh[u][m] = *(const v4i*)(bp[m] + (size_t)q * kMfRecord);
+                bl[u][m] = *(const v4i*)(bp[m] + (size_t)q * kMfRecord + 1024);
+            }
+            x0[u] = x1[u] = v4u{0, 0, 0, 0};
+            if (xrow) {
+                x0[u] = *(const v4u*)(xp + 64 * q);
+                x1[u] = *(const v4u*)(xp + 64 * q + 8);
+            }
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < QM; u++) {
+        if (q0 + u < q1) {
+            mf_chunk<NM, EPI>(a, q0 + u, g, x0[u], x1[u], bh[u], bl[u], cac, cmix, cbd, sc, sd);
+        }
+    }
+#else
 #pragma unroll 4
     for (uint32_t q = q0; q < q1; q++) {
         v4i bh[NM], bl[NM];
@@ -299,18 +380,9 @@ __global__ __launch_bounds__(64 * KS) void proj_mfma_kernel(ProjArgs a, uint32_t
             x0 = *(const v4u*)(xp + 64 * q);
             x1 = *(const v4u*)(xp + 64 * q + 8);
         }
-        v4i ah, al;
-        split16(x0, x1, ah, al);
-        sc = byte_sum(ah, sc);
-        sd = byte_sum(al, sd);
-#pragma unroll
-        for (int m = 0; m < NM; m++) {
-            cac[m] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, bh[m], cac[m], 0, 0, 0);
-            cmix[m] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, bl[m], cmix[m], 0, 0, 0);
-            cmix[m] = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, bh[m], cmix[m], 0, 0, 0);
-            cbd[m] = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, bl[m], cbd[m], 0, 0, 0);
-        }
+        mf_chunk<NM, EPI>(a, q, g, x0, x1, bh, bl, cac, cmix, cbd, sc, sd);
     }
+#endif
     // C lane l holds rows 4 (l / 16) + s, column l % 16.
     __shared__ v4i red[KS][NM][3][64];
     __shared__ int32_t rsum[KS][2][64];
@@ -423,12 +495,13 @@ __global__ __launch_bounds__(256) void copy_kernel(const uint4* __restrict__ src
 template <int RT, int EPI>
 static hipError_t launch_proj_rt(const ProjArgs& a, int L, uint32_t blocks,
                                  hipStream_t st) {
+    constexpr int W = EPI == EPI_SILU ? LLM_PROJ_WPB_SILU : LLM_PROJ_WPB;
     switch (L) {
-    case 0: proj_kernel<RT, 0, EPI><<<blocks, 256, 0, st>>>(a); break;
-    case 1: proj_kernel<RT, 1, EPI><<<blocks, 256, 0, st>>>(a); break;
-    case 4: proj_kernel<RT, 4, EPI><<<blocks, 256, 0, st>>>(a); break;
-    case 8: proj_kernel<RT, 8, EPI><<<blocks, 256, 0, st>>>(a); break;
-    default: proj_kernel<RT, 16, EPI><<<blocks, 256, 0, st>>>(a); break;
+    case 0: proj_kernel<RT, 0, EPI, W><<<blocks, 64 * W, 0, st>>>(a); break;
+    case 1: proj_kernel<RT, 1, EPI, W><<<blocks, 64 * W, 0, st>>>(a); break;
+    case 4: proj_kernel<RT, 4, EPI, W><<<blocks, 64 * W, 0, st>>>(a); break;
+    case 8: proj_kernel<RT, 8, EPI, W><<<blocks, 64 * W, 0, st>>>(a); break;
+    default: proj_kernel<RT, 16, EPI, W><<<blocks, 64 * W, 0, st>>>(a); break;
     }
     return hipGetLastError();
 }
@@ -442,27 +515,48 @@ static hipError_t launch_proj_epi(const ProjArgs& a, int L, uint32_t blocks,
     return launch_proj_rt<8, EPI>(a, L, blocks, st);
 }
 
+// Largest K-chunk count of one wavefront: parts split kq, wavefronts
+// split a part, each by floor division of the boundaries.
+static uint32_t mf_chunks_per_wave(uint32_t kq, uint32_t parts, uint32_t ks) {
+    const uint32_t per_part = (kq + parts - 1) / parts;
+    return (per_part + ks - 1) / ks;
+}
+
 MfSplit mf_split(uint32_t nc, uint32_t kq) {
-    // about 512 workgroups, at least two K chunks per wavefront
+    // about LLM_MF_WG_TARGET workgroups, at least two K chunks per
+    // wavefront, at most 8
     MfSplit s{4, 1};
-    while (nc * s.parts < 512 && kq / (s.parts * 2) >= s.ks * 2) s.parts *= 2;
-    if (kq / s.parts >= 8 * 4) s.ks = 8;
+    while (nc * s.parts < LLM_MF_WG_TARGET && kq / (s.parts * 2) >= s.ks * 2) s.parts *= 2;
+    while (s.ks < LLM_MF_KS_MAX && kq / s.parts >= s.ks * 2 * 4) s.ks *= 2;
+    while (mf_chunks_per_wave(kq, s.parts, s.ks) > 8) s.parts *= 2;
     return s;
+}
+
+template <int NM, int KS, int EPI>
+static hipError_t launch_mfma_q(const ProjArgs& a, uint32_t parts, hipStream_t st) {
+    const uint32_t qm = mf_chunks_per_wave(a.kq, parts, KS);
+    const dim3 grid(a.nc * parts);
+    if (qm <= 2)
+        proj_mfma_kernel<NM, KS, 2, EPI><<<grid, 64 * KS, 0, st>>>(a, parts);
+    else if (qm <= 4)
+        proj_mfma_kernel<NM, KS, 4, EPI><<<grid, 64 * KS, 0, st>>>(a, parts);
+    else if (qm <= 8)
+        proj_mfma_kernel<NM, KS, 8, EPI><<<grid, 64 * KS, 0, st>>>(a, parts);
+    else
+        return hipErrorInvalidConfiguration;  // mf_split keeps qm <= 8
+    return hipGetLastError();
 }
 
 template <int NM, int EPI>
 static hipError_t launch_mfma_epi(const ProjArgs& a, hipStream_t st) {
     const MfSplit sp = mf_split(a.nc, a.kq);
-    if (sp.ks == 8)
-        proj_mfma_kernel<NM, 8, EPI><<<a.nc * sp.parts, 64 * 8, 0, st>>>(a, sp.parts);
-    else
-        proj_mfma_kernel<NM, 4, EPI><<<a.nc * sp.parts, 64 * 4, 0, st>>>(a, sp.parts);
-    return hipGetLastError();
+    if (sp.ks >= 16) return launch_mfma_q<NM, 16, EPI>(a, sp.parts, st);
+    if (sp.ks == 8) return launch_mfma_q<NM, 8, EPI>(a, sp.parts, st);
+    return launch_mfma_q<NM, 4, EPI>(a, sp.parts, st);
 }
 
 bool proj_uses_mfma(const ProjArgs& a, int epi) {
-    return a.rows >= kMfMinRows && a.mf0 && a.mf_part && epi != EPI_STORE_NORM_IN &&
-           a.kq * kMfCols <= 32768;
+    return a.rows >= kMfMinRows && a.mf0 && a.mf_part && a.kq * kMfCols <= 32768;
 }
 
 hipError_t launch_proj(const ProjArgs& a, int epi, int L, uint32_t blocks,
@@ -471,6 +565,7 @@ hipError_t launch_proj(const ProjArgs& a, int epi, int L, uint32_t blocks,
         switch (epi) {
         case EPI_STORE: return launch_mfma_epi<1, EPI_STORE>(a, st);
         case EPI_RESID: return launch_mfma_epi<1, EPI_RESID>(a, st);
+        case EPI_STORE_NORM_IN: return launch_mfma_epi<1, EPI_STORE_NORM_IN>(a, st);
         default: return launch_mfma_epi<2, EPI_SILU>(a, st);
         }
     }

@@ -364,8 +364,8 @@ int enqueue_attention_sublayer(llm_ctx* c, uint32_t layer, uint32_t R,
     const bool cached = c->const_gain > 0 && c->attn_cache.pair == in_pair &&
                         c->attn_cache.layer == layer;
     // With a constant gain the projection normalises the raw rows itself
-    // (for one or two rows; larger blocks amortise a separate pass).
-    const bool norm_in = !cached && c->const_gain > 0 && R <= 2;
+    // as it loads them.
+    const bool norm_in = !cached && c->const_gain > 0;
     if (!cached && !norm_in) {
         TimedScope ts(c, LLM_K_RMSNORM);
         HIP_TRY(llm::launch_rmsnorm(in, c->Hp,
