@@ -213,6 +213,49 @@ int llm_bench_projection(llm_ctx_t* ctx, uint32_t kernel, uint32_t rows,
  * bandwidth); *ms is the average duration of one copy. */
 int llm_bench_copy(llm_ctx_t* ctx, uint64_t bytes, uint32_t iters, float* ms);
 
+/* LM head for the device argmax: [vocab][hidden] raw int16 (the tied
+ * embedding table, or lm_head.fix16.bin; model_data_t::lm_head_argmax,
+ * host/host_qwen_8x64.cpp:937-969).  vocab < 2^18, hidden <= 16384. */
+int llm_load_lm_head(llm_ctx_t* ctx, const int16_t* table, uint32_t vocab);
+/* For rows [row0, row0 + rows) of `pair`: argmax over v of the exact int64
+ * sum_k h[k] * W[v][k], first index on ties (the reference's strict >
+ * scan), into tokens[]; scores[] (optional) receives the winning sums.
+ * Replaces the host-side lm_head_argmax of the reference. */
+int llm_lm_head_argmax(llm_ctx_t* ctx, uint32_t pair, uint32_t row0,
+                       uint32_t rows, uint32_t* tokens, int64_t* scores);
+
+/* Report of llm_generate (the QWEN_8X64_E2E_PROFILE fields of the
+ * reference's generate mode, host/host_qwen_8x64.cpp:9264-9336). */
+typedef struct {
+    uint32_t prompt_tokens;
+    uint32_t generated_tokens;
+    uint32_t prompt_forward_passes;
+    uint32_t generated_forward_passes;
+    uint32_t coarse_task_count;       /* ceil(P/B)*2L + 1 + (G-1)*(2L+1) */
+    uint32_t output_materializations;
+    uint32_t released_prompt_blocks;
+    uint32_t reserved0;
+    double prompt_forward_ms;
+    double time_to_first_token_ms;
+    double generated_forward_ms;
+    double lm_head_ms;
+    double total_ms;
+} llm_generate_stats_t;
+
+/* The reference's generate loop with coarse tasks (host/host_qwen_8x64.cpp
+ * :9016-9136 with run_prompt_block :7840-7884 and run_token :7665-7712):
+ * the prompt in blocks of block_size (<= 8) tokens through layers
+ * [0, layer_count) (Task 18 from pair 1 into pair 0, Task 19 back, per
+ * layer), Task 20 only after the final block; then max_new_tokens sampled
+ * tokens, each the LM-head argmax of the last row, with a one-row forward
+ * (Tasks 18/19 per layer and 20) for every sampled token but the last.
+ * Embedding rows are gathered on the host from `embedding` [vocab][hidden]
+ * and uploaded, as in the reference.  Requires llm_load_lm_head first. */
+int llm_generate(llm_ctx_t* ctx, const int16_t* embedding, uint32_t vocab,
+                 const uint32_t* prompt, uint32_t n_prompt, uint32_t block_size,
+                 uint32_t layer_count, uint32_t max_new_tokens,
+                 uint32_t* out_tokens, llm_generate_stats_t* stats);
+
 /* The two exp tables the kernels use, 2049 entries for x = -8 .. 0 in
  * Q8.8 steps: q8_8 = floor(e^x * 256) (SiLU), q2_14 = floor(e^x * 16384)
  * (attention probabilities). */

@@ -72,6 +72,16 @@ constexpr uint32_t kMfRecord = 2048;
 
 hipError_t launch_copy(const uint4* src, uint4* dst, size_t n16,
                        hipStream_t st);
+
+// LM-head argmax: for each of `rows` activation rows x[r] (stride ldx),
+// argmax over v < n of the exact int64 sum_k x[r][k] * W[v][k] (tile4x128
+// weights w with `steps` k-steps, widening interval L), first index on
+// ties.  keys[r] must be zero on entry; it receives
+// ((score + 2^45) << 18) | (2^18 - 1 - v) of the winner.
+constexpr uint32_t kArgmaxVocabMax = (1u << 18) - 1;
+hipError_t launch_lm_argmax(const int16_t* w, uint32_t steps, uint32_t n,
+                            const int16_t* x, uint32_t ldx, uint32_t rows, int L,
+                            unsigned long long* keys, hipStream_t st);
 // Blocks of at least kMfMinRows rows run on the matrix cores when the
 // byte-plane layout is present; others on the VALU dot2 kernel.
 constexpr uint32_t kMfMinRows = 3;

@@ -479,6 +479,117 @@ __global__ __launch_bounds__(64 * KS) void proj_mfma_kernel(ProjArgs a, uint32_t
 }
 
 // ---------------------------------------------------------------------
+// LM-head argmax (model_data_t::lm_head_argmax, host/host_qwen_8x64.cpp
+// :937-969): exact int64 scores, strict > over increasing v.  Persistent:
+// each wavefront walks 4-row blocks (all k-steps) in a grid-stride loop,
+// keeps its best (score, v) per activation row, then the workgroup's best
+// goes into one 64-bit atomicMax per row.  The key orders by score, then
+// by smaller v, so equal scores resolve to the first index.
+// ---------------------------------------------------------------------
+__device__ __forceinline__ unsigned long long argmax_key(int64_t score, uint32_t v) {
+    return ((unsigned long long)(score + ((int64_t)1 << 45)) << 18) |
+           (unsigned long long)(kArgmaxVocabMax - v);
+}
+
+template <int RT, int L>
+__global__ __launch_bounds__(256) void lm_argmax_kernel(const int16_t* __restrict__ w,
+                                                        uint32_t S, uint32_t n,
+                                                        const int16_t* __restrict__ x,
+                                                        uint32_t ldx, uint32_t rows,
+                                                        unsigned long long* keys) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int i = lane >> 4, j = lane & 15;
+    const uint32_t nblocks = (n + 3) / 4;
+    const uint32_t stride = gridDim.x * 4;
+    unsigned long long best[RT];
+#pragma unroll
+    for (int r = 0; r < RT; r++) best[r] = 0;
+    for (uint32_t b = blockIdx.x * 4 + wave; b < nblocks; b += stride) {
+        const int16_t* wp = w + ((size_t)b * S * 4 + i) * 128 + j * 8;
+        const int16_t* xp = x + j * 8;
+        int64_t acc[RT];
+        int32_t part[RT];
+#pragma unroll
+        for (int r = 0; r < RT; r++) acc[r] = 0, part[r] = 0;
+        for (uint32_t s = 0; s < S;) {
+            const uint32_t lim = (L == 0) ? S : (s + L < S ? s + L : S);
+#pragma unroll 4
+            for (; s < lim; s++) {
+                const uint4 wv = *(const uint4*)(wp + (size_t)s * 512);
+#pragma unroll
+                for (int r = 0; r < RT; r++) {
+                    // rows beyond `rows` read row 0 (in bounds; ignored)
+                    const uint4 xv = *(const uint4*)(xp + (size_t)(r < (int)rows ? r : 0) * ldx +
+                                                     s * 128);
+                    if (L == 0) {
+                        acc[r] += dot2_wide(wv.x, xv.x) + dot2_wide(wv.y, xv.y) +
+                                  dot2_wide(wv.z, xv.z) + dot2_wide(wv.w, xv.w);
+                    } else {
+                        int32_t p = part[r];
+                        p = dot2(wv.x, xv.x, p);
+                        p = dot2(wv.y, xv.y, p);
+                        p = dot2(wv.z, xv.z, p);
+                        p = dot2(wv.w, xv.w, p);
+                        part[r] = p;
+                    }
+                }
+            }
+            if (L != 0) {
+#pragma unroll
+                for (int r = 0; r < RT; r++) acc[r] += part[r], part[r] = 0;
+            }
+        }
+        const uint32_t v = b * 4 + i;
+#pragma unroll
+        for (int r = 0; r < RT; r++) {
+#pragma unroll
+            for (int off = 8; off > 0; off >>= 1) acc[r] += __shfl_xor(acc[r], off, 64);
+            const unsigned long long k = argmax_key(acc[r], v);
+            if (j == 0 && v < n && k > best[r]) best[r] = k;
+        }
+    }
+    __shared__ unsigned long long wbest[4][4][RT];
+    if (j == 0) {
+#pragma unroll
+        for (int r = 0; r < RT; r++) wbest[wave][i][r] = best[r];
+    }
+    __syncthreads();
+    if (threadIdx.x < RT && threadIdx.x < rows) {
+        const int r = threadIdx.x;
+        unsigned long long k = 0;
+        for (int ww = 0; ww < 4; ww++)
+            for (int ii = 0; ii < 4; ii++) k = wbest[ww][ii][r] > k ? wbest[ww][ii][r] : k;
+        atomicMax(&keys[r], k);
+    }
+}
+
+template <int RT>
+static hipError_t launch_lm_rt(const int16_t* w, uint32_t steps, uint32_t n,
+                               const int16_t* x, uint32_t ldx, uint32_t rows, int L,
+                               unsigned long long* keys, hipStream_t st) {
+    const uint32_t nblocks = (n + 3) / 4;
+    uint32_t grid = (nblocks + 3) / 4;
+    if (grid > 2048) grid = 2048;
+    switch (L) {
+    case 0: lm_argmax_kernel<RT, 0><<<grid, 256, 0, st>>>(w, steps, n, x, ldx, rows, keys); break;
+    case 1: lm_argmax_kernel<RT, 1><<<grid, 256, 0, st>>>(w, steps, n, x, ldx, rows, keys); break;
+    case 4: lm_argmax_kernel<RT, 4><<<grid, 256, 0, st>>>(w, steps, n, x, ldx, rows, keys); break;
+    case 8: lm_argmax_kernel<RT, 8><<<grid, 256, 0, st>>>(w, steps, n, x, ldx, rows, keys); break;
+    default: lm_argmax_kernel<RT, 16><<<grid, 256, 0, st>>>(w, steps, n, x, ldx, rows, keys); break;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_lm_argmax(const int16_t* w, uint32_t steps, uint32_t n,
+                            const int16_t* x, uint32_t ldx, uint32_t rows, int L,
+                            unsigned long long* keys, hipStream_t st) {
+    if (rows <= 1) return launch_lm_rt<1>(w, steps, n, x, ldx, rows, L, keys, st);
+    if (rows <= 2) return launch_lm_rt<2>(w, steps, n, x, ldx, rows, L, keys, st);
+    if (rows <= 4) return launch_lm_rt<4>(w, steps, n, x, ldx, rows, L, keys, st);
+    return launch_lm_rt<8>(w, steps, n, x, ldx, rows, L, keys, st);
+}
+
+// ---------------------------------------------------------------------
 // Plain copy (calibration reference for HBM counters).
 // ---------------------------------------------------------------------
 __global__ __launch_bounds__(256) void copy_kernel(const uint4* __restrict__ src,

@@ -15,6 +15,7 @@
 #include <cstdio>
 #include <cstring>
 #include <string>
+#include <chrono>
 #include <vector>
 
 #include "attention.h"
@@ -132,6 +133,11 @@ struct llm_ctx {
     std::vector<Timed> pending;
     double kernel_ms[LLM_K_COUNT] = {};
     uint64_t kernel_n[LLM_K_COUNT] = {};
+
+    // LM head [vocab][hidden] (tile4x128) and the argmax keys of 8 rows
+    Matrix lm;
+    uint32_t lm_vocab = 0;
+    unsigned long long* lm_keys = nullptr;
 
     Matrix& mat(uint32_t layer, int m) { return mats[layer * M_COUNT + m]; }
 };
@@ -1142,6 +1148,165 @@ int llm_exp_tables(int16_t* q8_8, int16_t* q2_14) {
     build_exp_tables(a, b);
     if (q8_8) std::memcpy(q8_8, a, sizeof(a));
     if (q2_14) std::memcpy(q2_14, b, sizeof(b));
+    return 0;
+}
+
+}  // extern "C"
+
+namespace {
+
+int64_t key_score(unsigned long long k) {
+    return (int64_t)(k >> 18) - ((int64_t)1 << 45);
+}
+uint32_t key_token(unsigned long long k) {
+    return llm::kArgmaxVocabMax - (uint32_t)(k & llm::kArgmaxVocabMax);
+}
+
+double ms_since(std::chrono::steady_clock::time_point t) {
+    return std::chrono::duration<double, std::milli>(
+               std::chrono::steady_clock::now() - t).count();
+}
+
+// One materialised forward of `rows` rows at `position` through layers
+// [0, layer_count): embedding rows into pair 1, Task 18 (1 -> 0) and 19
+// (0 -> 1) per layer, Task 20 (1 -> 0) when `final_norm`
+// (run_composed_decoder_stack, host/host_qwen_8x64.cpp:1258-1445).
+int run_stack(llm_ctx_t* c, const int16_t* embedding, const uint32_t* tokens,
+              uint32_t rows, uint32_t position, uint32_t layer_count,
+              bool final_norm, uint32_t* tasks) {
+    std::vector<int16_t> hidden((size_t)rows * c->H);
+    for (uint32_t r = 0; r < rows; r++)
+        std::memcpy(&hidden[(size_t)r * c->H], embedding + (size_t)tokens[r] * c->H,
+                    (size_t)c->H * 2);
+    int rc = llm_hidden_upload(c, 1, hidden.data(), rows);
+    if (rc) return rc;
+    llm_status_t st;
+    auto task = [&](uint32_t op, uint32_t layer, uint32_t in, uint32_t out) {
+        const int r = llm_task(c, op, layer, rows, position, 0, in, out, &st);
+        if (r < 0) return r;
+        if (r != 0 || st.op != op || !st.last_task)
+            return fail(LLM_E_STATE, "controller status failure: op " +
+                                         std::to_string(op) + " code " +
+                                         std::to_string(st.code));
+        (*tasks)++;
+        return 0;
+    };
+    for (uint32_t layer = 0; layer < layer_count; layer++) {
+        if ((rc = task(LLM_OP_ATTENTION_SUBLAYER, layer, 1, 0))) return rc;
+        if ((rc = task(LLM_OP_FFN_SUBLAYER, layer, 0, 1))) return rc;
+    }
+    if (final_norm && (rc = task(LLM_OP_FINAL_NORM, 0, 1, 0))) return rc;
+    return llm_sync(c);
+}
+
+}  // namespace
+
+extern "C" {
+
+int llm_load_lm_head(llm_ctx_t* c, const int16_t* table, uint32_t vocab) {
+    if (!c || !table || vocab == 0 || vocab > llm::kArgmaxVocabMax)
+        return fail(LLM_E_ARG, "bad LM head arguments");
+    if (c->H > 16384) return fail(LLM_E_ARG, "hidden too large for the argmax key");
+    HIP_TRY(hipSetDevice(c->device));
+    Matrix& m = c->lm;
+    const uint32_t n_pad = round_up(vocab, llm::kBlockRows);
+    if (!m.d || m.n != vocab) {
+        int rc;
+        m = Matrix{};
+        m.n = vocab;
+        m.k = c->H;
+        m.n_pad = n_pad;
+        m.k_pad = round_up(c->H, llm::kStepCols);
+        m.steps = m.k_pad / llm::kStepCols;
+        if ((rc = dev_alloc(c, (void**)&m.d, m.elems() * sizeof(int16_t)))) return rc;
+        if (!c->lm_keys &&
+            (rc = dev_alloc(c, (void**)&c->lm_keys, 8 * sizeof(unsigned long long))))
+            return rc;
+    }
+    const int rc = upload_rows(c, m, 0, vocab, table, 0);
+    if (rc) return rc;
+    c->lm_vocab = vocab;
+    return 0;
+}
+
+int llm_lm_head_argmax(llm_ctx_t* c, uint32_t pair, uint32_t row0, uint32_t rows,
+                       uint32_t* tokens, int64_t* scores) {
+    if (!c || !tokens || pair >= c->pairs.size() || rows == 0 || row0 + rows > 8)
+        return fail(LLM_E_ARG, "bad LM head argmax arguments");
+    if (!c->lm_vocab) return fail(LLM_E_STATE, "LM head not loaded");
+    HIP_TRY(hipSetDevice(c->device));
+    HIP_TRY(hipMemsetAsync(c->lm_keys, 0, 8 * sizeof(unsigned long long), c->stream));
+    HIP_TRY(llm::launch_lm_argmax(c->lm.d, c->lm.steps, c->lm_vocab,
+                                  c->pairs[pair] + (size_t)row0 * c->Hp, c->Hp, rows,
+                                  c->lm.L, c->lm_keys, c->stream));
+    unsigned long long keys[8];
+    HIP_TRY(hipMemcpyAsync(keys, c->lm_keys, rows * sizeof(unsigned long long),
+                           hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    for (uint32_t r = 0; r < rows; r++) {
+        tokens[r] = key_token(keys[r]);
+        if (scores) scores[r] = key_score(keys[r]);
+    }
+    return 0;
+}
+
+int llm_generate(llm_ctx_t* c, const int16_t* embedding, uint32_t vocab,
+                 const uint32_t* prompt, uint32_t n_prompt, uint32_t block_size,
+                 uint32_t layer_count, uint32_t max_new_tokens,
+                 uint32_t* out_tokens, llm_generate_stats_t* stats) {
+    if (!c || !embedding || !prompt || n_prompt == 0 || block_size == 0 ||
+        block_size > 8 || layer_count == 0 || layer_count > c->L ||
+        (max_new_tokens && !out_tokens))
+        return fail(LLM_E_ARG, "bad generate arguments");
+    if (!c->lm_vocab && max_new_tokens) return fail(LLM_E_STATE, "LM head not loaded");
+    const uint64_t last_pos = (uint64_t)n_prompt + (max_new_tokens ? max_new_tokens - 1 : 0);
+    if (last_pos > c->max_seq)
+        return fail(LLM_E_ARG, "sequence exceeds max_seq_len");
+    for (uint32_t t = 0; t < n_prompt; t++)
+        if (prompt[t] >= vocab) return fail(LLM_E_ARG, "prompt token outside the vocabulary");
+    llm_generate_stats_t local{};
+    llm_generate_stats_t& S = stats ? *stats : local;
+    S = llm_generate_stats_t{};
+    S.prompt_tokens = n_prompt;
+    S.generated_tokens = max_new_tokens;
+    const auto begin = std::chrono::steady_clock::now();
+    uint32_t last_row = 0;
+    int rc;
+    // prompt blocks (host/host_qwen_8x64.cpp:9016-9060, :7840-7884)
+    for (uint32_t b0 = 0; b0 < n_prompt; b0 += block_size) {
+        const uint32_t rows = std::min(block_size, n_prompt - b0);
+        const bool final_block = b0 + rows == n_prompt;
+        const auto t = std::chrono::steady_clock::now();
+        if ((rc = run_stack(c, embedding, prompt + b0, rows, b0, layer_count,
+                            final_block, &S.coarse_task_count)))
+            return rc;
+        S.prompt_forward_ms += ms_since(t);
+        S.prompt_forward_passes++;
+        if (final_block) S.output_materializations++;
+        else S.released_prompt_blocks++;
+        last_row = rows - 1;
+    }
+    // sampled tokens (host/host_qwen_8x64.cpp:9091-9136)
+    uint32_t token = 0;
+    for (uint32_t step = 0; step < max_new_tokens; step++) {
+        const auto t = std::chrono::steady_clock::now();
+        if ((rc = llm_lm_head_argmax(c, 0, last_row, 1, &token, nullptr))) return rc;
+        S.lm_head_ms += ms_since(t);
+        out_tokens[step] = token;
+        if (step == 0) S.time_to_first_token_ms = ms_since(begin);
+        if (step + 1 < max_new_tokens) {
+            if (token >= vocab) return fail(LLM_E_STATE, "sampled token outside the embedding");
+            const auto f = std::chrono::steady_clock::now();
+            if ((rc = run_stack(c, embedding, &token, 1, n_prompt + step, layer_count,
+                                true, &S.coarse_task_count)))
+                return rc;
+            S.generated_forward_ms += ms_since(f);
+            S.generated_forward_passes++;
+            S.output_materializations++;
+            last_row = 0;
+        }
+    }
+    S.total_ms = ms_since(begin);
     return 0;
 }
 

@@ -32,7 +32,8 @@ EXPORTS = (
     "llm_kv_clear", "llm_pair_device_ptr", "llm_stream", "llm_sync",
     "llm_event_record", "llm_event_elapsed_ms", "llm_exp_tables",
     "llm_kernel_timing", "llm_kernel_stats", "llm_bench_copy",
-    "llm_bench_projection",
+    "llm_bench_projection", "llm_load_lm_head", "llm_lm_head_argmax",
+    "llm_generate",
 )
 KERNELS = ("rmsnorm", "qkv", "rope", "attention", "oproj", "gateup", "down")
 
@@ -62,6 +63,19 @@ class Status(ctypes.Structure):
         return (self.op, self.code, self.token_count, self.output_waves,
                 self.mm_tasks, self.vector_tasks, self.completed_packets,
                 self.last_task)
+
+
+class GenerateStats(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint32) for n in (
+        "prompt_tokens", "generated_tokens", "prompt_forward_passes",
+        "generated_forward_passes", "coarse_task_count",
+        "output_materializations", "released_prompt_blocks", "reserved0")] + [
+            (n, ctypes.c_double) for n in (
+                "prompt_forward_ms", "time_to_first_token_ms",
+                "generated_forward_ms", "lm_head_ms", "total_ms")]
+
+    def as_dict(self):
+        return {n: getattr(self, n) for n, _ in self._fields_ if n != "reserved0"}
 
 
 class AccelError(RuntimeError):
@@ -112,6 +126,15 @@ def load_library(path=LIB_PATH):
                                           ctypes.POINTER(ctypes.c_float)]),
         "llm_bench_projection": (ctypes.c_int, [vp, _u32, _u32, _u32, _u32,
                                                 ctypes.POINTER(ctypes.c_float)]),
+        "llm_load_lm_head": (ctypes.c_int, [vp, _i16p, _u32]),
+        "llm_lm_head_argmax": (ctypes.c_int, [vp, _u32, _u32, _u32,
+                                              ctypes.POINTER(ctypes.c_uint32),
+                                              ctypes.POINTER(ctypes.c_int64)]),
+        "llm_generate": (ctypes.c_int, [vp, _i16p, _u32,
+                                        ctypes.POINTER(ctypes.c_uint32), _u32,
+                                        _u32, _u32, _u32,
+                                        ctypes.POINTER(ctypes.c_uint32),
+                                        ctypes.POINTER(GenerateStats)]),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)
@@ -231,6 +254,30 @@ class Accelerator:
             self._ctx, pair, _p16(port0), _p16(port1), rows, stride_words),
             "download_ports")
         return port0, port1
+
+    # --- LM head and generation ------------------------------------------
+    def load_lm_head(self, table):
+        table = np.ascontiguousarray(table, np.int16)
+        self._check(lib().llm_load_lm_head(self._ctx, _p16(table), table.shape[0]),
+                    "llm_load_lm_head")
+
+    def lm_head_argmax(self, pair, row0, rows):
+        toks = (ctypes.c_uint32 * rows)()
+        scores = (ctypes.c_int64 * rows)()
+        self._check(lib().llm_lm_head_argmax(self._ctx, pair, row0, rows, toks,
+                                             scores), "llm_lm_head_argmax")
+        return list(toks), list(scores)
+
+    def generate(self, embedding, prompt, block_size, layer_count, max_new_tokens):
+        embedding = np.ascontiguousarray(embedding, np.int16)
+        prompt_arr = (ctypes.c_uint32 * len(prompt))(*prompt)
+        out = (ctypes.c_uint32 * max(max_new_tokens, 1))()
+        st = GenerateStats()
+        self._check(lib().llm_generate(self._ctx, _p16(embedding), embedding.shape[0],
+                                       prompt_arr, len(prompt), block_size,
+                                       layer_count, max_new_tokens, out,
+                                       ctypes.byref(st)), "llm_generate")
+        return list(out)[:max_new_tokens], st.as_dict()
 
     # --- tasks ------------------------------------------------------------
     def task(self, op, layer, token_count, position, in_pair, out_pair,
