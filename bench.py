@@ -43,6 +43,8 @@ def parse():
     ap.add_argument("--copies", type=int, default=8)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--sweep", action=argparse.BooleanOptionalAction, default=True,
+                    help="configs[3] decode context sweep (extra field)")
     return ap.parse_args()
 
 
@@ -119,6 +121,37 @@ def cpu_baseline(spec, synth, seconds):
         "p8_block_us": float(np.mean(p8_times)) * 1e6,
         "decode_forward_us": dec * 1e6,
     }
+
+
+def context_sweep(llm_accel, workloads, spec, synth):
+    """one layer, K/V preloaded with seeded Q8.8
+    N(0, 0.3) to n positions, one decode forward (T18/T19/T20) at position
+    n; median of 5, the Infinity Cache flushed by a 512 MiB copy before
+    each forward."""
+    nmax = 16384
+    shape = llm_accel.Shape(spec.vocab, spec.hidden, spec.inter, 1, spec.heads,
+                            spec.kv_heads, nmax + 64, 1e6)
+    out = {}
+    with llm_accel.Accelerator(shape, num_pairs=4) as a:
+        a.load_model(synth)
+        for h in range(spec.kv_heads):
+            k, v = synth.kv_rows(nmax, seed_offset=20 + h)
+            a.kv_write(0, h, 0, k, v)
+        a.upload(3, synth.hidden_rows(1))
+        for n in (128, 1024, 4096, 16384):
+            times = []
+            for rep in range(6):
+                a.bench_copy(512 << 20, 1)
+                a.record(0)
+                a.task(18, 0, 1, n, 3, 0)
+                a.task(19, 0, 1, n, 0, 1)
+                a.task(20, 0, 1, n, 1, 0)
+                a.record(1)
+                a.sync()
+                if rep:
+                    times.append(a.elapsed_ms(0, 1) * 1e3)
+            out[str(n)] = round(float(np.median(times)), 2)
+    return out
 
 
 def main():
@@ -215,6 +248,7 @@ def main():
     copy_ms = acc.bench_copy(copy_bytes, 20)
     copy_gbs = 2 * copy_bytes / copy_ms / 1e6
     acc.close()
+    sweep = context_sweep(llm_accel, workloads, spec, synth) if args.sweep else None
 
     lb = layer_bytes(spec)
     gu_bytes = gateup_bytes(spec, 1)
@@ -251,6 +285,7 @@ def main():
         "kernel_us_decode": {k: round(v[1], 3) for k, v in kdec.items()},
         "kernel_us_p8": {k: round(v[1], 3) for k, v in kp8.items()},
         "copy_kernel_gbs": copy_gbs,
+        "decode_forward_us_by_context": sweep,
         "roofline": {
             "kernel": "proj_kernel<1,*,EPI_SILU> (gate|up + SiLU*up, decode row)",
             "bound": "hbm",

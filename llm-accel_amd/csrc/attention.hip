@@ -754,12 +754,15 @@ __global__ __launch_bounds__(NT) void attention_pv_kernel(AttnArgs a) {
 #pragma unroll
             for (int u = 0; u < SB; u++) {
                 if (j0 + u < ntiles) {
-                    const int32_t mn = tmx[u] > m ? tmx[u] : m;
-                    const int64_t old = (int64_t)prob(sm.e14, m - mn) << 2;
-                    sum = fx_sat32(fx_rnd((int64_t)sum * old + ((int64_t)tsm[u] << 18), 16));
-                    acc = fx_sat32(fx_rnd((int64_t)acc * old, 16));
+                    if (tmx[u] > m) {  // the running max moves: rescale
+                        const int64_t old = (int64_t)prob(sm.e14, m - tmx[u]) << 2;
+                        sum = fx_sat32(fx_rnd((int64_t)sum * old + ((int64_t)tsm[u] << 18), 16));
+                        acc = fx_sat32(fx_rnd((int64_t)acc * old, 16));
+                        m = tmx[u];
+                    } else {  // factor exp(0) = 1.0: rnd(v * 2^16, 16) = v
+                        sum = fx_sat32((int64_t)sum + ((int64_t)tsm[u] << 2));
+                    }
                     acc = fx_sat32((int64_t)acc + ((int64_t)tv[u] << 8));
-                    m = mn;
                 }
             }
         }

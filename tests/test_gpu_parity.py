@@ -188,6 +188,45 @@ def test_kv_preload_then_decode_long_context():
     assert first_mismatch(got, want) is None
 
 
+@pytest.mark.parametrize("n", [1024, 4096, 16384])
+def test_context_sweep_decode_forward(n):
+    """K/V of one Qwen2.5-3B-shaped layer preloaded
+    with seeded Q8.8 N(0, 0.3) to length n, then one decode forward (Task
+    18, 19, 20) at position n; every task's output and the appended K/V row
+    bit-exact."""
+    import llm_accel
+    spec = workloads.CONFIG_B
+    synth = workloads.SyntheticModel(spec, layers=1)
+    oshape = oracle_shape(spec, layers=1, max_seq=n + 64)
+    om = oracle_from_synthetic(synth, oshape)
+    kc, vc = om.new_kv()
+    x = synth.hidden_rows(1)
+    with llm_accel.Accelerator(accel_shape(spec, layers=1, max_seq=n + 64)) as a:
+        a.load_model(synth)
+        for h in range(spec.kv_heads):
+            k, v = synth.kv_rows(n, seed_offset=20 + h)
+            kc[0, h, :n] = k
+            vc[0, h, :n] = v
+            a.kv_write(0, h, 0, k, v)
+        a.upload(2, x)
+        _say(f"case context sweep n={n}")
+        got = []
+        for op, pin, pout in ((18, 2, 0), (19, 0, 1), (20, 1, 0)):
+            rc, st = a.task(op, 0, 1, n, pin, pout)
+            assert rc == 0
+            got.append(a.download(pout, 1))
+        kv_got = [a.kv_read(0, h, n, 1) for h in range(spec.kv_heads)]
+    cur = x
+    for i, op in enumerate((18, 19, 20)):
+        code, cur, _ = om.task((kc, vc), op, 0, cur, n)
+        assert code == 0
+        err = first_mismatch(got[i], cur)
+        assert err is None, f"op {op}: {err}"
+    for h in range(spec.kv_heads):
+        assert first_mismatch(kv_got[h][0], kc[0, h, n:n + 1]) is None
+        assert first_mismatch(kv_got[h][1], vc[0, h, n:n + 1]) is None
+
+
 def test_split_attention_p8_block_late_position():
     # 8 rows at positions 200..207: 4 tiles per row, split over workgroups.
     import llm_accel
