@@ -29,7 +29,18 @@ struct AttnArgs {
     int32_t* s_tsum;      // [8][kv_heads][max_tiles][group]
     int16_t* s_tval;      // [8][kv_heads][max_tiles][group][head_dim]
     uint32_t* counters;   // [8][kv_heads], zero between launches
+    // split path, per chunk of tiles and query head: whether the running
+    // max rises inside the chunk, sum of its tile sums << 2, and per
+    // element the sum of its tile PV values << 8 (the whole chunk's effect
+    // on the recurrence when the max does not rise)
+    uint32_t max_chunks;
+    int32_t* c_flag;      // [8][kv_heads][max_chunks][group]
+    int32_t* c_tsum;      // [8][kv_heads][max_chunks][group]
+    int32_t* c_sum;       // [8][kv_heads][max_chunks][group][head_dim]
 };
+
+// Tiles per split-path workgroup: at most kMaxChunkTiles.
+constexpr uint32_t kMaxChunkTiles = 8;
 
 // chunks = max over active rows of ceil(tiles / chunk_tiles); 1 selects
 // the fused single-workgroup path.

@@ -494,6 +494,47 @@ __device__ __forceinline__ void store_appended(const AttnArgs& a, const Smem<D>&
         a.vcache[page_off<D>(a, h, tile) + tid * TILE + paired(slot)] = sm.app_v[tid];
 }
 
+// Running state of the per-tile recurrence of one (query head, element).
+struct ScanState {
+    int32_t m, sum, acc;
+};
+
+// Tiles [j0, j1) of the recurrence, one by one (a chunk in which the
+// running max rises, or whose sums could saturate).
+template <int D>
+__device__ __noinline__ ScanState scan_tiles(const int16_t* s_tval, const int16_t* s_tmax,
+                                             const int32_t* s_tsum, const int16_t* e14,
+                                             size_t row0, uint32_t G, uint32_t g,
+                                             uint32_t e, uint32_t j0, uint32_t j1,
+                                             ScanState st) {
+    // row0 = (row, head) * max_tiles: tile j of head g at (row0 + j) * G + g
+    int32_t tv[kMaxChunkTiles], tmx[kMaxChunkTiles], tsm[kMaxChunkTiles];
+#pragma unroll
+    for (int v = 0; v < (int)kMaxChunkTiles; v++) {
+        if (j0 + v < j1) {
+            const size_t base = (row0 + j0 + v) * G + g;
+            tv[v] = ld_coherent(&s_tval[base * D + e]);
+            tmx[v] = s_tmax[base];
+            tsm[v] = ld_coherent(&s_tsum[base]);
+        }
+    }
+#pragma unroll
+    for (int v = 0; v < (int)kMaxChunkTiles; v++) {
+        if (j0 + v < j1) {
+            if (tmx[v] > st.m) {  // the running max moves: rescale
+                const int64_t old = (int64_t)prob(e14, st.m - tmx[v]) << 2;
+                st.sum = fx_sat32(fx_rnd((int64_t)st.sum * old + ((int64_t)tsm[v] << 18), 16));
+                st.acc = fx_sat32(fx_rnd((int64_t)st.acc * old, 16));
+                st.m = tmx[v];
+            } else {  // factor exp(0) = 1.0: rnd(v * 2^16, 16) = v
+                st.sum = fx_sat32((int64_t)st.sum + ((int64_t)tsm[v] << 2));
+            }
+            st.acc = fx_sat32((int64_t)st.acc + ((int64_t)tv[v] << 8));
+        }
+    }
+    return st;
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------
@@ -662,6 +703,7 @@ template <int D>
 __global__ __launch_bounds__(NT) void attention_pv_kernel(AttnArgs a) {
     __shared__ Smem<D> sm;
     __shared__ int32_t mrun[MAXG];
+    __shared__ int32_t cflag[MAXG], ctsum[MAXG];
     const uint32_t t = blockIdx.x, h = blockIdx.y, c = blockIdx.z;
     const uint32_t G = a.group;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -679,7 +721,15 @@ __global__ __launch_bounds__(NT) void attention_pv_kernel(AttnArgs a) {
     TileGeo tg = tile_geo(a, n, t0);
     issue_v<D>(a, h, tg, ld);
     commit_prologue<D>(a, sm, false, true, pl);
-    if (threadIdx.x < G) mrun[threadIdx.x] = INT16_MIN;
+    if (threadIdx.x < G) {
+        mrun[threadIdx.x] = INT16_MIN;
+        cflag[threadIdx.x] = 0;
+        ctsum[threadIdx.x] = 0;
+    }
+    constexpr int IT = MAXG * D / NT > 0 ? MAXG * D / NT : 1;  // (g, e) items per thread
+    int32_t csum[IT];
+#pragma unroll
+    for (int u = 0; u < IT; u++) csum[u] = 0;
     __syncthreads();
     // running max before this chunk: parallel over (tile, head)
     for (uint32_t idx = threadIdx.x; idx < t0 * G; idx += blockDim.x)
@@ -714,17 +764,25 @@ __global__ __launch_bounds__(NT) void attention_pv_kernel(AttnArgs a) {
                 const int32_t pr = lane < tl ? prob(sm.e14, sc[gi] - mn) : 0;
                 put_prob<D>(sm, g, lane, pr);
                 const int32_t ts = wave_sum(pr);
-                if (lane == 0) st_coherent(&a.s_tsum[(rh * a.max_tiles + tile) * G + g], ts);
+                if (lane == 0) {
+                    st_coherent(&a.s_tsum[(rh * a.max_tiles + tile) * G + g], ts);
+                    ctsum[g] += ts << 2;               // this wave owns head g
+                    if (tm[gi] > mrun[g]) cflag[g] = 1;  // the running max rises
+                }
             }
         }
         __syncthreads();  // probabilities staged
-        for (uint32_t idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
+#pragma unroll
+        for (int u = 0; u < IT; u++) {
+            const uint32_t idx = threadIdx.x + NT * u;
+            if (idx >= G * D) break;
             const uint32_t g = idx / D, e = idx % D;
             v4u vr[TILE / 8];
             load_v_row<D>(sm, e, vr);
             const size_t base = (rh * a.max_tiles + tile) * G + g;
-            st_coherent(&a.s_tval[base * D + e],
-                        (int16_t)row_pv(sm.p + g * TILE, sm.cp + g * TILE, vr, vcorr));
+            const int32_t tv = row_pv(sm.p + g * TILE, sm.cp + g * TILE, vr, vcorr);
+            st_coherent(&a.s_tval[base * D + e], (int16_t)tv);
+            csum[u] += tv << 8;
         }
         __syncthreads();  // tile consumed
         if (threadIdx.x < G) {
@@ -733,39 +791,62 @@ __global__ __launch_bounds__(NT) void attention_pv_kernel(AttnArgs a) {
         }
     }
     if (own / TILE >= t0 && own / TILE < t1) store_appended<D>(a, sm, h, own, false, true);
+    // The chunk's summary per query head (and element).
+    const size_t rc = rh * a.max_chunks + c;
+#pragma unroll
+    for (int u = 0; u < IT; u++) {
+        const uint32_t idx = threadIdx.x + NT * u;
+        if (idx < G * D) st_coherent(&a.c_sum[rc * G * D + idx], csum[u]);
+    }
+    if (threadIdx.x < G) {
+        st_coherent(&a.c_flag[rc * G + threadIdx.x], cflag[threadIdx.x]);
+        st_coherent(&a.c_tsum[rc * G + threadIdx.x], ctsum[threadIdx.x]);
+    }
     // Publish, then let the last chunk of this (row, head) finish.
     if (!arrive_last(&a.counters[rh], nchunks, &sm.last)) return;
-    constexpr int SB = 16;  // tiles whose values are in flight together
+    // The per-tile recurrence (sum, acc rounded at every tile).  A chunk in
+    // which the running max does not rise only adds: its factors are
+    // exp(0) = 1.0, so rnd(v * 2^16, 16) = v, and while |acc| and sum stay
+    // clear of the int32 bounds by the chunk's largest possible movement
+    // (tile values << 8 < 2^23, tile sums << 2 <= 2^22) no saturation can
+    // occur inside it; such a chunk is applied as one addition.  Other
+    // chunks run tile by tile.
+    constexpr int SB = 16;  // chunks whose summaries are in flight together
+    const uint32_t CT = a.chunk_tiles;
     for (uint32_t idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
         const uint32_t g = idx / D, e = idx % D;
-        int32_t m = INT16_MIN, sum = 0, acc = 0;
-        for (uint32_t j0 = 0; j0 < ntiles; j0 += SB) {
-            int32_t tv[SB], tmx[SB], tsm[SB];
+        ScanState st{INT16_MIN, 0, 0};
+        for (uint32_t c0 = 0; c0 < nchunks; c0 += SB) {
+            int32_t fl[SB], cs[SB], ct[SB];
 #pragma unroll
             for (int u = 0; u < SB; u++) {
-                const uint32_t j = j0 + u;
-                if (j < ntiles) {
-                    const size_t base = (rh * a.max_tiles + j) * G + g;
-                    tv[u] = ld_coherent(&a.s_tval[base * D + e]);
-                    tmx[u] = a.s_tmax[base];
-                    tsm[u] = ld_coherent(&a.s_tsum[base]);
+                fl[u] = 1, cs[u] = 0, ct[u] = 0;
+                if (c0 + u < nchunks) {
+                    const size_t q = rh * a.max_chunks + c0 + u;
+                    fl[u] = ld_coherent(&a.c_flag[q * G + g]);
+                    cs[u] = ld_coherent(&a.c_sum[q * G * D + idx]);
+                    ct[u] = ld_coherent(&a.c_tsum[q * G + g]);
                 }
             }
 #pragma unroll
             for (int u = 0; u < SB; u++) {
-                if (j0 + u < ntiles) {
-                    if (tmx[u] > m) {  // the running max moves: rescale
-                        const int64_t old = (int64_t)prob(sm.e14, m - tmx[u]) << 2;
-                        sum = fx_sat32(fx_rnd((int64_t)sum * old + ((int64_t)tsm[u] << 18), 16));
-                        acc = fx_sat32(fx_rnd((int64_t)acc * old, 16));
-                        m = tmx[u];
-                    } else {  // factor exp(0) = 1.0: rnd(v * 2^16, 16) = v
-                        sum = fx_sat32((int64_t)sum + ((int64_t)tsm[u] << 2));
+                const uint32_t cc = c0 + u;
+                if (cc < nchunks) {
+                    const uint32_t j0 = cc * CT, j1 = j0 + CT < ntiles ? j0 + CT : ntiles;
+                    const int64_t nt = j1 - j0;
+                    const int64_t aa = st.acc < 0 ? -(int64_t)st.acc : st.acc;
+                    if (!fl[u] && aa <= INT32_MAX - (nt << 23) &&
+                        st.sum <= INT32_MAX - (nt << 22)) {
+                        st.acc += cs[u];
+                        st.sum += ct[u];
+                    } else {
+                        st = scan_tiles<D>(a.s_tval, a.s_tmax, a.s_tsum, sm.e14,
+                                           rh * a.max_tiles, G, g, e, j0, j1, st);
                     }
-                    acc = fx_sat32((int64_t)acc + ((int64_t)tv[u] << 8));
                 }
             }
         }
+        const int32_t sum = st.sum, acc = st.acc;
         const int64_t inv = fx_inv_sum(sum);
         a.out[(size_t)t * a.ldo + (size_t)h * G * D + idx] =
             fx_sat16(fx_rnd((int64_t)acc * inv, 16));

@@ -98,7 +98,10 @@ struct llm_ctx {
     int16_t* attn = nullptr;           // [8][Hp]
     int16_t* act = nullptr;            // [8][Ip]
     // attention split-path scratch
-    uint32_t chunk_tiles = 2;
+    uint32_t chunk_tiles = 4;
+    int32_t* c_flag = nullptr;
+    int32_t* c_tsum = nullptr;
+    int32_t* c_sum = nullptr;
     int16_t* s_scores = nullptr;
     int16_t* s_tmax = nullptr;
     int32_t* s_tsum = nullptr;
@@ -423,10 +426,14 @@ int enqueue_attention_sublayer(llm_ctx* c, uint32_t layer, uint32_t R,
     at.s_tsum = c->s_tsum;
     at.s_tval = c->s_tval;
     at.counters = c->counters;
+    at.max_chunks = (uint32_t)cdiv(c->tiles, c->chunk_tiles);
+    at.c_flag = c->c_flag;
+    at.c_tsum = c->c_tsum;
+    at.c_sum = c->c_sum;
     const uint32_t last_tiles = (uint32_t)cdiv(pos + R, llm::kTile);
     static_assert(llm::kTile == 64, "attention tiles are 64 positions");
-    if (c->chunk_tiles == 0 || c->chunk_tiles > 64)  // page-index span in LDS
-        return fail(LLM_E_STATE, "attention chunk must be 1..64 tiles");
+    if (c->chunk_tiles == 0 || c->chunk_tiles > llm::kMaxChunkTiles)
+        return fail(LLM_E_STATE, "attention chunk must be 1..8 tiles");
     const uint32_t chunks = (uint32_t)cdiv(last_tiles, c->chunk_tiles);
     {
         TimedScope ts(c, LLM_K_ATTENTION);
@@ -670,6 +677,13 @@ int llm_ctx_create(const llm_shape_t* shape, int device, uint32_t num_pairs,
         (rc = dev_alloc(c, (void**)&c->s_tval, rht * d * 2)) ||
         (rc = dev_alloc(c, (void**)&c->counters, (size_t)8 * c->Hkv * 4)))
         return cleanup(rc);
+    {
+        const size_t rhc = (size_t)8 * c->Hkv * cdiv(c->tiles, c->chunk_tiles) * c->G;
+        if ((rc = dev_alloc(c, (void**)&c->c_flag, rhc * 4)) ||
+            (rc = dev_alloc(c, (void**)&c->c_tsum, rhc * 4)) ||
+            (rc = dev_alloc(c, (void**)&c->c_sum, rhc * d * 4)))
+            return cleanup(rc);
+    }
     {
         // split matrix-core scratch: the largest (chunks x parts x record)
         size_t words = 0, chunks = 0;

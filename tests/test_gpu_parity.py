@@ -228,14 +228,14 @@ def test_context_sweep_decode_forward(n):
 
 
 def test_split_attention_p8_block_late_position():
-    # 8 rows at positions 200..207: 4 tiles per row, split over workgroups.
+    # 8 rows at positions 500..507: 8-9 tiles per row, split over workgroups.
     import llm_accel
     spec = workloads.CONFIG_A
-    n = 200
+    n = 500
     synth = workloads.SyntheticModel(spec, layers=1)
-    om = oracle_from_synthetic(synth, oracle_shape(spec, layers=1, max_seq=256))
+    om = oracle_from_synthetic(synth, oracle_shape(spec, layers=1, max_seq=576))
     kc, vc = om.new_kv()
-    with llm_accel.Accelerator(accel_shape(spec, layers=1, max_seq=256)) as a:
+    with llm_accel.Accelerator(accel_shape(spec, layers=1, max_seq=576)) as a:
         a.load_model(synth)
         for h in range(spec.kv_heads):
             k, v = synth.kv_rows(n, seed_offset=20 + h)
@@ -243,7 +243,7 @@ def test_split_attention_p8_block_late_position():
             a.kv_write(0, h, 0, k, v)
         x = synth.hidden_rows(8)
         a.upload(2, x)
-        _say("case split P8 at 200")
+        _say("case split P8 at 500")
         a.task(18, 0, 8, n, 2, 0)
         got = a.download(0, 8)
         kg, vg = a.kv_read(0, 1, 0, n + 8)
@@ -253,10 +253,11 @@ def test_split_attention_p8_block_late_position():
     assert first_mismatch(vg, vc[0, 1, :n + 8]) is None
 
 
-@pytest.mark.parametrize("n", [40, 150])
+@pytest.mark.parametrize("n", [40, 150, 700])
 def test_saturating_kv_takes_exact_path(n):
     # K/V values beyond +-8.0 saturate in Q4.12; the kernel must switch to
-    # the per-product path on those tiles (fused for n=40, split for 150).
+    # the per-product path on those tiles (fused for n=40 and 150, split
+    # for 700).
     import llm_accel
     spec = workloads.CONFIG_B
     synth = workloads.SyntheticModel(spec, layers=1)
@@ -276,6 +277,33 @@ def test_saturating_kv_takes_exact_path(n):
         _say(f"case saturating kv n={n}")
         a.task(18, 0, 2, n, 2, 0)
         got = a.download(0, 2)
+    code, want, _ = om.task((kc, vc), 18, 0, x, n)
+    assert first_mismatch(got, want) is None
+
+
+def test_accumulator_saturation_over_long_context():
+    # K = 0 (every score 0, uniform probabilities) and V saturated at +8.0
+    # over 16384 positions: the attention accumulator reaches the Q16.16
+    # bound, so chunks of the split scan must fall back to the per-tile
+    # saturating recurrence.
+    import llm_accel
+    spec = workloads.CONFIG_B
+    n = 16384
+    synth = workloads.SyntheticModel(spec, layers=1)
+    om = oracle_from_synthetic(synth, oracle_shape(spec, layers=1, max_seq=n + 64))
+    kc, vc = om.new_kv()
+    x = synth.hidden_rows(1)
+    with llm_accel.Accelerator(accel_shape(spec, layers=1, max_seq=n + 64)) as a:
+        a.load_model(synth)
+        for h in range(spec.kv_heads):
+            k = np.zeros((n, spec.head_dim), np.int16)
+            v = np.full((n, spec.head_dim), 32767, np.int16)
+            kc[0, h, :n], vc[0, h, :n] = k, v
+            a.kv_write(0, h, 0, k, v)
+        a.upload(2, x)
+        _say("case accumulator saturation n=16384")
+        a.task(18, 0, 1, n, 2, 0)
+        got = a.download(0, 1)
     code, want, _ = om.task((kc, vc), 18, 0, x, n)
     assert first_mismatch(got, want) is None
 
