@@ -117,23 +117,48 @@ __device__ __forceinline__ uint4 norm8(uint4 x, uint4 g, int32_t gain) {
     return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
+// Epilogue operands that do not depend on the sums (residual, norm
+// gammas), fetched when the kernel starts so that the epilogue waits on no
+// memory round trip.
+struct EpiIn {
+    int32_t res, g0, g1;
+};
+template <int EPI>
+__device__ __forceinline__ EpiIn epi_fetch(const ProjArgs& a, uint32_t r, uint32_t n) {
+    EpiIn e{0, 0, 0};
+    if (EPI == EPI_RESID) {
+        e.res = a.res[(size_t)r * a.ldr + n];
+        if (a.norm_out) e.g0 = a.norm_gamma[n];
+        if (a.final_out) e.g1 = a.final_gamma[n];
+    }
+    return e;
+}
+
+// The Q8.8 exp table staged in LDS for the SiLU epilogue (one 16-byte
+// piece per thread; visible after the workgroup's next barrier).
+__device__ __forceinline__ void stage_exp8(const int16_t* exp8, int16_t* e8s) {
+    for (uint32_t c = threadIdx.x; c < 2056 / 8; c += blockDim.x)
+        *(uint4*)(e8s + 8 * c) = *(const uint4*)(exp8 + 8 * c);
+}
+
 // Output (r, n) of a projection from its exact sums (gate and up for
 // EPI_SILU): the reference's narrowing, then the epilogue.
 template <int EPI>
 __device__ __forceinline__ void proj_out(const ProjArgs& a, uint32_t r, uint32_t n,
-                                         int64_t t0, int64_t t1) {
+                                         int64_t t0, int64_t t1, const EpiIn& ei,
+                                         const int16_t* e8) {
     int16_t y = fx_narrow_projection(t0);
     if (EPI == EPI_RESID) {
-        y = fx_sat16((int32_t)y + a.res[(size_t)r * a.ldr + n]);
+        y = fx_sat16((int32_t)y + ei.res);
         if (a.norm_out)
             a.norm_out[(size_t)r * a.ldn + n] = fx_sat16(fx_rnd(
-                (int64_t)y * a.norm_gain * a.norm_gamma[n], 16));
+                (int64_t)y * a.norm_gain * ei.g0, 16));
         if (a.final_out)
             a.final_out[(size_t)r * a.ldn + n] = fx_sat16(fx_rnd(
-                (int64_t)y * a.norm_gain * a.final_gamma[n], 16));
+                (int64_t)y * a.norm_gain * ei.g1, 16));
     } else if (EPI == EPI_SILU) {
         const int16_t up = fx_narrow_projection(t1);
-        const int16_t sg = fx_silu(y, a.exp8);
+        const int16_t sg = fx_silu(y, e8);
         y = fx_sat16(fx_rnd((int64_t)sg * up, 8));
     }
     a.out[(size_t)r * a.ldo + n] = y;
@@ -145,6 +170,19 @@ __global__ __launch_bounds__(64 * WPB) void proj_kernel(ProjArgs a) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int i = lane >> 4, j = lane & 15;
     const uint32_t b = blockIdx.x;
+    // epilogue thread t < 4 RT: output row et % RT of block row et / RT
+    const int et = threadIdx.x;
+    const uint32_t en = b * 4 + et / RT, er = et % RT;
+    const bool eout = et < 4 * RT && er < a.rows && en < a.n;
+    EpiIn ei{0, 0, 0};
+    if (eout) ei = epi_fetch<EPI>(a, er, en);
+    // rows >= rows of the final-norm pair copy the residual rows
+    const uint32_t fn = b * 4 + (et >> 3), fr = et & 7;
+    const bool efill = EPI == EPI_RESID && a.final_out && et < 32 && fr >= a.rows && fn < a.n;
+    int16_t fill = 0;
+    if (efill) fill = a.res[(size_t)fr * a.ldr + fn];
+    __shared__ int16_t e8s[EPI == EPI_SILU ? 2056 : 8];
+    if (EPI == EPI_SILU) stage_exp8(a.exp8, e8s);
     const uint32_t S = a.steps;
     const uint32_t s0 = wave * S / WPB, s1 = (wave + 1) * S / WPB;
 
@@ -230,27 +268,18 @@ __global__ __launch_bounds__(64 * WPB) void proj_kernel(ProjArgs a) {
             for (int r = 0; r < RT; r++) red[wave][m][i][r] = acc[m][r];
     }
     __syncthreads();
-    const int t = threadIdx.x;
-    if (t < 4 * RT) {
-        const int ii = t / RT, r = t % RT;
-        const uint32_t n = b * 4 + ii;
-        if ((uint32_t)r < a.rows && n < a.n) {
-            int64_t tot[NM];
+    if (eout) {
+        const int ii = et / RT;
+        int64_t tot[NM];
 #pragma unroll
-            for (int m = 0; m < NM; m++) {
-                tot[m] = 0;
+        for (int m = 0; m < NM; m++) {
+            tot[m] = 0;
 #pragma unroll
-                for (int w = 0; w < WPB; w++) tot[m] += red[w][m][ii][r];
-            }
-            proj_out<EPI>(a, r, n, tot[0], tot[NM - 1]);
+            for (int w = 0; w < WPB; w++) tot[m] += red[w][m][ii][er];
         }
+        proj_out<EPI>(a, er, en, tot[0], tot[NM - 1], ei, e8s);
     }
-    if (EPI == EPI_RESID && a.final_out && t < 32) {
-        const int ii = t >> 3, r = t & 7;
-        const uint32_t n = b * 4 + ii;
-        if ((uint32_t)r >= a.rows && n < a.n)
-            a.final_out[(size_t)r * a.ldn + n] = a.res[(size_t)r * a.ldr + n];
-    }
+    if (efill) a.final_out[(size_t)fr * a.ldn + fn] = fill;
 }
 
 // ---------------------------------------------------------------------
@@ -332,6 +361,24 @@ __global__ __launch_bounds__(64 * KS) void proj_mfma_kernel(ProjArgs a, uint32_t
     const uint32_t i = lane & 15, g = lane >> 4;
     const bool xrow = i < a.rows;
     const int16_t* xp = a.x + (size_t)(xrow ? i : 0) * a.ldx + 16 * g;
+    // epilogue operands of this thread's first output t = threadIdx.x
+    const uint32_t et = threadIdx.x, er = et >> 4, en = c * kMfRows + (et & 15);
+    EpiIn ei{0, 0, 0};
+    int32_t ems[NM][2] = {};
+    int16_t fill = 0;
+    if (et < 256 && en < a.n) {
+        if (er < a.rows) {
+            ei = epi_fetch<EPI>(a, er, en);
+#pragma unroll
+            for (int m = 0; m < NM; m++) {
+                const int32_t* ms = m == 0 ? a.ms0 : a.ms1;
+                ems[m][0] = ms[2 * en];
+                ems[m][1] = ms[2 * en + 1];
+            }
+        } else if (EPI == EPI_RESID && a.final_out && er < 8) {
+            fill = a.res[(size_t)er * a.ldr + en];
+        }
+    }
     const int8_t* bp[NM];
     bp[0] = a.mf0 + (size_t)c * KQ * kMfRecord + lane * 16;
     if (NM == 2) bp[NM - 1] = a.mf1 + (size_t)c * KQ * kMfRecord + lane * 16;
@@ -463,17 +510,24 @@ __global__ __launch_bounds__(64 * KS) void proj_mfma_kernel(ProjArgs a, uint32_t
                         rd += rsum[w][1][r + 16 * gg];
                     }
             }
+            // later outputs of this thread (fewer than 4 wavefronts) fetch
+            // their operands here
+            const bool first = t == et;
+            EpiIn e = first ? ei : epi_fetch<EPI>(a, r, n);
             int64_t tot[NM];
 #pragma unroll
             for (int m = 0; m < NM; m++) {
                 const int32_t* ms = m == 0 ? a.ms0 : a.ms1;
+                const int32_t m0 = first ? ems[m][0] : ms[2 * n];
+                const int32_t m1 = first ? ems[m][1] : ms[2 * n + 1];
                 tot[m] = 65536 * sums[m][0] + 256 * sums[m][1] + sums[m][2] +
-                         32768 * (int64_t)ms[2 * n] + 128 * (int64_t)ms[2 * n + 1] +
-                         32768 * rc + 128 * rd + 16384 * k64;
+                         32768 * (int64_t)m0 + 128 * (int64_t)m1 + 32768 * rc + 128 * rd +
+                         16384 * k64;
             }
-            proj_out<EPI>(a, r, n, tot[0], tot[NM - 1]);
+            proj_out<EPI>(a, r, n, tot[0], tot[NM - 1], e, a.exp8);
         } else if (EPI == EPI_RESID && a.final_out && r < 8) {
-            a.final_out[(size_t)r * a.ldn + n] = a.res[(size_t)r * a.ldr + n];
+            a.final_out[(size_t)r * a.ldn + n] =
+                t == et ? fill : a.res[(size_t)r * a.ldr + n];
         }
     }
 }
