@@ -49,6 +49,7 @@
 // waiting).
 #include "attention.h"
 
+#include "attn_common.h"
 #include "coherent.h"
 #include "fixed_point.h"
 
@@ -56,89 +57,11 @@ namespace llm {
 
 namespace {
 
-constexpr int TILE = 64;
 constexpr int MAXG = 16;
+constexpr uint32_t kHeadPathRows = 2;  // rows per block taking the head path
 constexpr int NT = 512;          // threads per workgroup
 constexpr int NW = NT / 64;      // wavefronts per workgroup
 constexpr int VROW = TILE + 8;   // padded LDS row of the V^T tile (int16)
-
-typedef short s16x2 __attribute__((ext_vector_type(2)));
-// Register staging types: native vectors (plain loads and stores, no
-// aggregate copies).
-typedef uint32_t v4u __attribute__((ext_vector_type(4)));
-typedef uint32_t v2u __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ int32_t dot2(uint32_t a, uint32_t b, int32_t c) {
-    return __builtin_amdgcn_sdot2(__builtin_bit_cast(s16x2, a),
-                                  __builtin_bit_cast(s16x2, b), c, false);
-}
-
-// Slot of element u (0..7) of a group in the bank-paired order, and back.
-__device__ __forceinline__ uint32_t paired(uint32_t e) {
-    const uint32_t u = e & 7u;
-    return (e & ~7u) | (u < 4 ? 2 * u : 2 * (u - 4) + 1);
-}
-__device__ __forceinline__ uint32_t slot_pos(uint32_t j) {
-    return (j >> 1) + 4 * (j & 1);
-}
-
-__device__ __forceinline__ int32_t clamp_k(int32_t v) {
-    return v < -2048 ? -2048 : (v > 2048 ? 2048 : v);
-}
-// c(x) = floor((8 - x) / 16): correction of a product with 32767.
-__device__ __forceinline__ int32_t sat_corr(int32_t x) { return (8 - x) >> 4; }
-
-// Both int16 halves clamped to [-2048, 2048] (v_pk_max_i16 / v_pk_min_i16).
-__device__ __forceinline__ uint32_t clamp_word(uint32_t w) {
-    const s16x2 lo = {-2048, -2048}, hi = {2048, 2048};
-    const s16x2 v = __builtin_bit_cast(s16x2, w);
-    return __builtin_bit_cast(uint32_t,
-                              __builtin_elementwise_min(__builtin_elementwise_max(v, lo), hi));
-}
-// 1 in each half of a clamped word that holds 2048 (a saturating value):
-// in [-2048, 2048] that is the one value with bit 11 set and bit 15 clear.
-__device__ __forceinline__ uint32_t sat_mask(uint32_t w) {
-    return (w >> 11) & ~(w >> 15) & 0x00010001u;
-}
-__device__ __forceinline__ v4u clamp4(v4u v, uint32_t& any) {
-    v4u r;
-    r.x = clamp_word(v.x);
-    r.y = clamp_word(v.y);
-    r.z = clamp_word(v.z);
-    r.w = clamp_word(v.w);
-    any |= sat_mask(r.x) | sat_mask(r.y) | sat_mask(r.z) | sat_mask(r.w);
-    return r;
-}
-
-__device__ __forceinline__ int16_t prob(const int16_t* exp14, int32_t x) {
-    x = fx_sat16(x);
-    x = x < -2048 ? -2048 : x;
-    return exp14[x + 2048];
-}
-
-// Wavefront reductions over DPP row operations; the result is uniform.
-template <int CTRL, int ROWS>
-__device__ __forceinline__ int32_t dpp(int32_t old, int32_t v) {
-    return __builtin_amdgcn_update_dpp(old, v, CTRL, ROWS, 0xf, false);
-}
-__device__ __forceinline__ int32_t wave_max(int32_t v) {
-    v = max(v, dpp<0xb1, 0xf>(v, v));   // quad_perm [1 0 3 2]
-    v = max(v, dpp<0x4e, 0xf>(v, v));   // quad_perm [2 3 0 1]
-    v = max(v, dpp<0x141, 0xf>(v, v));  // row_half_mirror
-    v = max(v, dpp<0x140, 0xf>(v, v));  // row_mirror
-    v = max(v, dpp<0x142, 0xa>(v, v));  // row_bcast:15 -> rows 1, 3
-    v = max(v, dpp<0x143, 0xc>(v, v));  // row_bcast:31 -> rows 2, 3
-    return __builtin_amdgcn_readlane(v, 63);
-}
-__device__ __forceinline__ int32_t wave_sum(int32_t v) {
-    v += dpp<0xb1, 0xf>(0, v);
-    v += dpp<0x4e, 0xf>(0, v);
-    v += dpp<0x141, 0xf>(0, v);
-    v += dpp<0x140, 0xf>(0, v);
-    v += dpp<0x142, 0xa>(0, v);
-    v += dpp<0x143, 0xc>(0, v);
-    return __builtin_amdgcn_readlane(v, 63);
-}
 
 template <int D>
 struct __attribute__((aligned(16))) Smem {
@@ -172,23 +95,6 @@ __device__ __forceinline__ int32_t read_flags(const Smem<D>& sm) {
 #pragma unroll
     for (int w = 0; w < NW; w++) f |= sm.wflags[w];
     return f;
-}
-
-// (x0, x1) rotated by the Q8.8 table entry (c, s) (host:4765-4788).  The
-// table holds quantised cos / sin, |c|, |s| <= 256, so the sums fit int32.
-__device__ __forceinline__ void rope_pair(int32_t x0, int32_t x1, int32_t c,
-                                          int32_t s, int32_t& y0, int32_t& y1) {
-    y0 = fx_sat16((x0 * c - x1 * s + 128) >> 8);
-    y1 = fx_sat16((x1 * c + x0 * s + 128) >> 8);
-}
-
-__device__ __forceinline__ int32_t half16(const v2u& v, uint32_t j) {
-    const uint32_t w = j < 2 ? v.x : v.y;
-    return (int16_t)((j & 1) ? (w >> 16) : (w & 0xffff));
-}
-__device__ __forceinline__ int32_t half16(const v4u& v, uint32_t j) {
-    const uint32_t w = j < 2 ? v.x : (j < 4 ? v.y : (j < 6 ? v.z : v.w));
-    return (int16_t)((j & 1) ? (w >> 16) : (w & 0xffff));
 }
 
 // Four RoPE pairs (elements c..c+3 and c+d/2..c+d/2+3) of one vector.
@@ -397,70 +303,6 @@ __device__ __forceinline__ void commit_prologue(const AttnArgs& a, Smem<D>& sm, 
     }
 }
 
-// Score (Q8.8) of query head g against the K row held in kr (bank-paired,
-// clamped).
-template <int D>
-__device__ __forceinline__ int16_t row_score(const Smem<D>& sm, const v4u* kr,
-                                             uint32_t g, bool corr, int64_t scale) {
-    const int16_t* qg = sm.q + g * D;
-    int32_t b0 = 0, b1 = 0, b2 = 0, b3 = 0;
-#pragma unroll
-    for (int c = 0; c < D / 8; c++) {
-        const v4u qv = *(const v4u*)(qg + 8 * c);
-        b0 = dot2(kr[c].x, qv.x, b0);
-        b1 = dot2(kr[c].y, qv.y, b1);
-        b2 = dot2(kr[c].z, qv.z, b2);
-        b3 = dot2(kr[c].w, qv.w, b3);
-    }
-    if (corr) {
-        const int16_t* cg = sm.cq + g * D;
-#pragma unroll
-        for (int c = 0; c < D / 8; c++) {
-            const v4u cv = *(const v4u*)(cg + 8 * c);
-            b0 = dot2(sat_mask(kr[c].x), cv.x, b0);
-            b1 = dot2(sat_mask(kr[c].y), cv.y, b1);
-            b2 = dot2(sat_mask(kr[c].z), cv.z, b2);
-            b3 = dot2(sat_mask(kr[c].w), cv.w, b3);
-        }
-    }
-    // +2^31 (one saturating bank) wraps to INT32_MIN
-    const int64_t t64 = (int64_t)(b0 == INT32_MIN ? INT32_MAX : b0) +
-                        (b1 == INT32_MIN ? INT32_MAX : b1) +
-                        (b2 == INT32_MIN ? INT32_MAX : b2) +
-                        (b3 == INT32_MIN ? INT32_MAX : b3);
-    int32_t t = fx_sat32(t64);
-    t = fx_sat32(fx_rnd((int64_t)t * scale, 16));
-    return fx_sat16(fx_rnd(t, 8));
-}
-
-// Q8.8 PV tile value of one query head (probabilities pg, c(p) cg) against
-// the V^T row held in vr: banks, x fm(1/64).
-__device__ __forceinline__ int32_t row_pv(const int16_t* pg, const int16_t* cg,
-                                          const v4u* vr, bool corr) {
-    int32_t b0 = 0, b1 = 0, b2 = 0, b3 = 0;
-#pragma unroll
-    for (int c = 0; c < TILE / 8; c++) {
-        const v4u pv = *(const v4u*)(pg + 8 * c);
-        b0 = dot2(vr[c].x, pv.x, b0);
-        b1 = dot2(vr[c].y, pv.y, b1);
-        b2 = dot2(vr[c].z, pv.z, b2);
-        b3 = dot2(vr[c].w, pv.w, b3);
-    }
-    if (corr) {
-#pragma unroll
-        for (int c = 0; c < TILE / 8; c++) {
-            const v4u cv = *(const v4u*)(cg + 8 * c);
-            b0 = dot2(sat_mask(vr[c].x), cv.x, b0);
-            b1 = dot2(sat_mask(vr[c].y), cv.y, b1);
-            b2 = dot2(sat_mask(vr[c].z), cv.z, b2);
-            b3 = dot2(sat_mask(vr[c].w), cv.w, b3);
-        }
-    }
-    int32_t t = fx_sat32((int64_t)b0 + b1 + b2 + b3);
-    t = fx_sat32(fx_rnd((int64_t)t * 1024, 16));
-    return fx_sat16(fx_rnd(t, 8));
-}
-
 template <int D>
 __device__ __forceinline__ void load_k_row(const Smem<D>& sm, uint32_t p, v4u* kr) {
 #pragma unroll
@@ -593,7 +435,8 @@ __global__ __launch_bounds__(NT) void attention_fused_kernel(AttnArgs a) {
                 const uint32_t g = wave + NW * gi;
                 if (g >= G) break;
                 const bool valid = lane < tl;
-                const int32_t s = valid ? row_score<D>(sm, kr, g, kcorr, scale)
+                const int32_t s = valid ? row_score<D>(sm.q + g * D, sm.cq + g * D, kr,
+                                                           kcorr, scale)
                                         : INT16_MIN;
                 const int32_t wm = wave_max(s);
                 const int32_t mn = wm > m[gi] ? wm : m[gi];
@@ -646,6 +489,223 @@ __global__ __launch_bounds__(NT) void attention_fused_kernel(AttnArgs a) {
 }
 
 // ---------------------------------------------------------------------
+// Head path: one wavefront per (row, query head) walks every tile, for the
+// contexts of the fused path.  Every load of the first tile is issued at
+// once: the cache rows go to registers (lane p holds the K row of position
+// p, lanes e and e + 64 the V^T rows of those elements), the current
+// block's rows are rotated into LDS, the exp table is staged, and the
+// wavefront then computes without a workgroup barrier.  The serial chain
+// of one head is short, and the grid covers every (row, head), so this is
+// the latency path for decode and for 8-row blocks at short contexts.
+// ---------------------------------------------------------------------
+template <int D>
+struct __attribute__((aligned(16))) HeadSmem {
+    int16_t q[D], cq[D];        // rotated query, c(q), bank-paired
+    int16_t kc[8][D];           // the block's K rows after RoPE, bank-paired
+    int16_t vc[8][D];           // the block's V rows
+    int16_t p[TILE], cp[TILE];  // a tile's probabilities and c(p), paired
+    int16_t e14[2056];          // Q2.14 exp table
+};
+
+template <int D>
+struct HeadRows {
+    static constexpr int EW = (D + 63) / 64;  // elements per lane in PV
+    v4u k[D / 8];
+    v4u v[EW][TILE / 8];
+};
+
+// This lane's cache rows of `tile`: the K row of its position (cached
+// positions only) and the V^T chunks that hold cached positions.
+template <int D>
+__device__ __forceinline__ void head_load(const AttnArgs& a, uint32_t h, uint32_t tile,
+                                          HeadRows<D>& R) {
+    const uint32_t lane = threadIdx.x, p = tile * TILE + lane;
+    const int16_t* kp = a.kcache + page_off<D>(a, h, tile);
+    const int16_t* vp = a.vcache + page_off<D>(a, h, tile);
+#pragma unroll
+    for (int c = 0; c < D / 8; c++)
+        R.k[c] = p < a.pos0 ? *(const v4u*)(kp + (size_t)lane * D + 8 * c) : v4u{0, 0, 0, 0};
+#pragma unroll
+    for (int ei = 0; ei < HeadRows<D>::EW; ei++) {
+        const uint32_t e = lane + 64 * ei;
+#pragma unroll
+        for (int c = 0; c < TILE / 8; c++)
+            R.v[ei][c] = e < D && tile * TILE + 8 * c < a.pos0
+                             ? *(const v4u*)(vp + (size_t)e * TILE + 8 * c)
+                             : v4u{0, 0, 0, 0};
+    }
+}
+
+// Half-word j (0..7) of a 16-byte chunk replaced by v.
+__device__ __forceinline__ v4u put_half(v4u w, uint32_t j, int32_t v) {
+    const uint32_t sh = 16 * (j & 1), msk = 0xffffu << sh, val = (uint32_t)(uint16_t)v << sh;
+    if (j / 2 == 0) w.x = (w.x & ~msk) | val;
+    else if (j / 2 == 1) w.y = (w.y & ~msk) | val;
+    else if (j / 2 == 2) w.z = (w.z & ~msk) | val;
+    else w.w = (w.w & ~msk) | val;
+    return w;
+}
+
+template <int D>
+__global__ __launch_bounds__(64) void attention_head_kernel(AttnArgs a) {
+    __shared__ HeadSmem<D> sm;
+    constexpr int EW = HeadRows<D>::EW;
+    const uint32_t t = blockIdx.x, g = blockIdx.y, lane = threadIdx.x;
+    const uint32_t h = g / a.group;
+    const uint32_t n = a.pos0 + t + 1, own = n - 1;
+    const uint32_t ntiles = (n + TILE - 1) / TILE;
+    const int64_t scale = (int64_t)a.qk_scale << 8;
+
+    // ---- every load of the first tile ----
+    HeadRows<D> rows;
+    head_load<D>(a, h, 0, rows);
+    v4u ex[5];
+#pragma unroll
+    for (int u = 0; u < 5; u++) {
+        const uint32_t c = lane + 64 * u < 257 ? lane + 64 * u : 256;
+        ex[u] = *(const v4u*)(a.exp14 + 8 * c);
+    }
+    const uint32_t c = lane < D / 2 ? lane : 0;  // RoPE pair (c, c + D/2)
+    const int16_t* qrow = a.qkv + (size_t)t * a.ldqkv + (size_t)g * D;
+    const int16_t* qrope = a.rope + (size_t)own * D;
+    const int32_t qx0 = qrow[c], qx1 = qrow[D / 2 + c], qc = qrope[c], qs = qrope[D / 2 + c];
+    int32_t kx0[8], kx1[8], kc[8], ks[8], vv[8][EW];
+#pragma unroll
+    for (int r = 0; r < 8; r++) {
+        if (r <= (int)t) {
+            const int16_t* row = a.qkv + (size_t)r * a.ldqkv;
+            const int16_t* krow = row + (size_t)a.num_heads * D + (size_t)h * D;
+            const int16_t* vrow = row + (size_t)(a.num_heads + a.num_kv_heads) * D + (size_t)h * D;
+            const int16_t* kr = a.rope + (size_t)(a.pos0 + r) * D;
+            kx0[r] = krow[c];
+            kx1[r] = krow[D / 2 + c];
+            kc[r] = kr[c];
+            ks[r] = kr[D / 2 + c];
+#pragma unroll
+            for (int ei = 0; ei < EW; ei++) {
+                const uint32_t e = lane + 64 * ei;
+                vv[r][ei] = e < D ? vrow[e] : 0;
+            }
+        }
+    }
+    // ---- staging (one wavefront: LDS operations stay in order) ----
+#pragma unroll
+    for (int u = 0; u < 5; u++) {
+        const uint32_t cc = lane + 64 * u < 257 ? lane + 64 * u : 256;
+        *(v4u*)(sm.e14 + 8 * cc) = ex[u];
+    }
+    if (lane < D / 2) {
+        int32_t y0, y1;
+        rope_pair(qx0, qx1, qc, qs, y0, y1);
+        sm.q[paired(c)] = (int16_t)y0;
+        sm.q[paired(D / 2 + c)] = (int16_t)y1;
+        sm.cq[paired(c)] = (int16_t)sat_corr(y0);
+        sm.cq[paired(D / 2 + c)] = (int16_t)sat_corr(y1);
+    }
+#pragma unroll
+    for (int r = 0; r < 8; r++) {
+        if (r <= (int)t) {
+            if (lane < D / 2) {
+                int32_t y0, y1;
+                rope_pair(kx0[r], kx1[r], kc[r], ks[r], y0, y1);
+                sm.kc[r][paired(c)] = (int16_t)y0;
+                sm.kc[r][paired(D / 2 + c)] = (int16_t)y1;
+            }
+#pragma unroll
+            for (int ei = 0; ei < EW; ei++) {
+                const uint32_t e = lane + 64 * ei;
+                if (e < D) sm.vc[r][e] = (int16_t)vv[r][ei];
+            }
+        }
+    }
+
+    int32_t m = INT16_MIN, sum = 0, acc[EW];
+#pragma unroll
+    for (int ei = 0; ei < EW; ei++) acc[ei] = 0;
+    for (uint32_t tile = 0; tile < ntiles; tile++) {
+        if (tile > 0) head_load<D>(a, h, tile, rows);
+        const uint32_t p = tile * TILE + lane;
+        const bool valid = p < n;
+        // K row of this lane's position: cached, or a row of this block
+        const bool blk = p >= a.pos0 && p <= own;
+        const int16_t* kb = sm.kc[blk ? p - a.pos0 : 0];
+        v4u kr[D / 8];
+        s16x2 mk = {-32768, -32768};
+#pragma unroll
+        for (int cc = 0; cc < D / 8; cc++)
+            kr[cc] = clamp4m(blk ? *(const v4u*)(kb + 8 * cc) : rows.k[cc], mk);
+        const bool kcorr = __any(sat_any(mk));
+        // q and c(q) are read inside the loop (hoisted, they would hold
+        // 2 D/8 vector registers across it)
+        uint32_t qoff = 0;
+        asm volatile("" : "+v"(qoff));
+        const int32_t s = valid ? row_score<D>(sm.q + qoff, sm.cq + qoff, kr, kcorr, scale)
+                                : INT16_MIN;
+        const int32_t wm = wave_max(s);
+        const int32_t mn = wm > m ? wm : m;
+        const int32_t old = prob(sm.e14, m - mn);
+        const int32_t pr = valid ? prob(sm.e14, s - mn) : 0;
+        sm.p[paired(lane)] = (int16_t)pr;
+        sm.cp[paired(lane)] = (int16_t)sat_corr(pr);
+        const int32_t ts = wave_sum(pr);  // <= 64 * 16384
+        sum = fx_sat32(fx_rnd((int64_t)sum * ((int64_t)old << 2) + ((int64_t)ts << 18), 16));
+        m = mn;
+        if (old != 16384) {
+#pragma unroll
+            for (int ei = 0; ei < EW; ei++)
+                acc[ei] = fx_sat32(fx_rnd((int64_t)acc[ei] * ((int64_t)old << 2), 16));
+        }
+        // V^T rows: the block's rows in this tile go to their own slots
+        // (slots beyond the context meet probability 0)
+        for (uint32_t r = 0; r <= t; r++) {
+            const uint32_t pp = a.pos0 + r;
+            if (pp / TILE != tile) continue;
+            const uint32_t slot = paired(pp % TILE);
+#pragma unroll
+            for (int ei = 0; ei < EW; ei++) {
+                const uint32_t e = lane + 64 * ei < D ? lane + 64 * ei : 0;
+#pragma unroll
+                for (int cc = 0; cc < TILE / 8; cc++)
+                    if (slot / 8 == (uint32_t)cc)
+                        rows.v[ei][cc] = put_half(rows.v[ei][cc], slot % 8, sm.vc[r][e]);
+            }
+        }
+        v4u vr[EW][TILE / 8];
+        s16x2 mv = {-32768, -32768};
+#pragma unroll
+        for (int ei = 0; ei < EW; ei++)
+#pragma unroll
+            for (int cc = 0; cc < TILE / 8; cc++) vr[ei][cc] = clamp4m(rows.v[ei][cc], mv);
+        const bool vcorr = __any(sat_any(mv));
+#pragma unroll
+        for (int ei = 0; ei < EW; ei++) {
+            if (lane + 64 * ei >= D) break;
+            const int32_t tv = row_pv(sm.p, sm.cp, vr[ei], vcorr);
+            acc[ei] = fx_sat32((int64_t)acc[ei] + ((int64_t)tv << 8));
+        }
+    }
+    const int64_t inv = fx_inv_sum(sum);
+#pragma unroll
+    for (int ei = 0; ei < EW; ei++) {
+        const uint32_t e = lane + 64 * ei;
+        if (e < D)
+            a.out[(size_t)t * a.ldo + (size_t)g * D + e] =
+                fx_sat16(fx_rnd((int64_t)acc[ei] * inv, 16));
+    }
+    if (g % a.group == 0) {  // this row's K (rotated, paired) and V into the cache
+        const uint32_t tile = own / TILE, slot = own % TILE;
+        if (lane < D / 8)
+            *(v4u*)(a.kcache + page_off<D>(a, h, tile) + slot * D + 8 * lane) =
+                *(const v4u*)(sm.kc[t] + 8 * lane);
+#pragma unroll
+        for (int ei = 0; ei < EW; ei++) {
+            const uint32_t e = lane + 64 * ei;
+            if (e < D) a.vcache[page_off<D>(a, h, tile) + e * TILE + paired(slot)] = sm.vc[t][e];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------
 // Split path, phase A: scores and tile maxima for a chunk of tiles; the
 // row's own K is appended by the chunk that holds its position.
 // grid (rows, kv_heads, chunks).
@@ -683,7 +743,8 @@ __global__ __launch_bounds__(NT) void attention_scores_kernel(AttnArgs a) {
         load_k_row<D>(sm, lane, kr);
         for (uint32_t g = wave; g < G; g += NW) {
             const bool valid = lane < tl;
-            const int32_t s = valid ? row_score<D>(sm, kr, g, kcorr, scale) : INT16_MIN;
+            const int32_t s = valid ? row_score<D>(sm.q + g * D, sm.cq + g * D, kr, kcorr, scale)
+                                    : INT16_MIN;
             const size_t base = (rh * a.max_tiles + tile) * G + g;
             a.s_scores[base * TILE + lane] = (int16_t)s;
             const int32_t mx = wave_max(s);
@@ -857,7 +918,12 @@ template <int D>
 static hipError_t launch_d(const AttnArgs& a, uint32_t rows, uint32_t kv_heads,
                            uint32_t chunks, hipStream_t st) {
     if (chunks <= 1) {
-        attention_fused_kernel<D><<<dim3(rows, kv_heads), NT, 0, st>>>(a);
+        // a wavefront per (row, query head) for single rows and pairs; a
+        // workgroup per (row, KV head) beyond (measured at configs[1])
+        if (rows <= kHeadPathRows)
+            attention_head_kernel<D><<<dim3(rows, a.num_heads), 64, 0, st>>>(a);
+        else
+            attention_fused_kernel<D><<<dim3(rows, kv_heads), NT, 0, st>>>(a);
         return hipGetLastError();
     }
     attention_scores_kernel<D><<<dim3(rows, kv_heads, chunks), NT, 0, st>>>(a);

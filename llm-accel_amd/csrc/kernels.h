@@ -42,7 +42,8 @@ struct ProjArgs {
     int16_t* final_out;
     const int16_t* final_gamma;
     // EPI_STORE_NORM_IN: x[r][k] is replaced by rnd(x * in_gain * in_gamma[k],
-    // 16) for k < in_cols and by 0 beyond.
+    // 16); in_gamma is read in whole k-steps (the table is padded), and past
+    // in_cols the rows themselves are 0.
     const int16_t* in_gamma;
     int32_t in_gain;
     uint32_t in_cols;
@@ -84,7 +85,10 @@ hipError_t launch_lm_argmax(const int16_t* w, uint32_t steps, uint32_t n,
                             unsigned long long* keys, hipStream_t st);
 // Blocks of at least kMfMinRows rows run on the matrix cores when the
 // byte-plane layout is present; others on the VALU dot2 kernel.
-constexpr uint32_t kMfMinRows = 3;
+#ifndef LLM_MF_MIN_ROWS
+#define LLM_MF_MIN_ROWS 3
+#endif
+constexpr uint32_t kMfMinRows = LLM_MF_MIN_ROWS;
 // Workgroup shape of the matrix-core kernel for a matrix: KS wavefronts
 // per workgroup, P workgroups per 16-output chunk.
 struct MfSplit {

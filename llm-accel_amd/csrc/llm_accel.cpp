@@ -624,8 +624,10 @@ int llm_ctx_create(const llm_shape_t* shape, int device, uint32_t num_pairs,
             return cleanup(fail(LLM_E_HIP, "hipMemset failed"));
     }
     // tables
+    // norm table + one k-step of padding: the fused-norm projections read
+    // gammas in whole k-steps
     if ((rc = dev_alloc(c, (void**)&c->norms,
-                        (size_t)(2 * c->L + 1) * c->H * sizeof(int16_t))) ||
+                        ((size_t)(2 * c->L + 1) * c->H + c->Hp) * sizeof(int16_t))) ||
         (rc = dev_alloc(c, (void**)&c->rope,
                         (size_t)c->max_seq * d * sizeof(int16_t))) ||
         (rc = dev_alloc(c, (void**)&c->exp8, 2056 * sizeof(int16_t))) ||
