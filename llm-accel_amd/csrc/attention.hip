@@ -59,6 +59,11 @@ namespace {
 
 constexpr int MAXG = 16;
 constexpr uint32_t kHeadPathRows = 2;  // rows per block taking the head path
+#ifndef LLM_SPLIT_HEAD_ROWS
+#define LLM_SPLIT_HEAD_ROWS 2
+#endif
+// rows per block taking the split-head path (head_dim a multiple of 32)
+constexpr uint32_t kSplitHeadRows = LLM_SPLIT_HEAD_ROWS;
 constexpr int NT = 512;          // threads per workgroup
 constexpr int NW = NT / 64;      // wavefronts per workgroup
 constexpr int VROW = TILE + 8;   // padded LDS row of the V^T tile (int16)
@@ -706,6 +711,220 @@ __global__ __launch_bounds__(64) void attention_head_kernel(AttnArgs a) {
 }
 
 // ---------------------------------------------------------------------
+// Split-head path: D / 32 wavefronts per (row, query head), for the
+// contexts of the fused path.  Wavefront w owns head elements
+// [32 w, 32 w + 32).  QK: lane p forms the four bank partial sums of its
+// position over the wavefront's 32 elements (8 products per bank, far from
+// wrapping), the partials of all wavefronts meet in LDS (one barrier per
+// tile; the buffer alternates with the tile's parity) and every wavefront
+// completes the same bank sums, scores, softmax state and probabilities,
+// which it keeps in its own LDS slice.  PV: lane (e, half) sums the 32
+// positions of one half of the tile for element 32 w + e; the halves meet
+// across lanes e and e + 32.  A bank sum taken in pieces is the same
+// integer mod 2^32 as the sequential chain, so the +2^31 case reads the
+// same.  Cache rows of the next tile are loaded while a tile is computed.
+// ---------------------------------------------------------------------
+template <int D>
+struct __attribute__((aligned(16))) SplitSmem {
+    static constexpr int NWH = D / 32;
+    int16_t q[D], cq[D];                  // rotated query, c(q), bank-paired
+    int16_t kc[8][D];                     // the block's K rows after RoPE, bank-paired
+    int16_t vc[8][D];                     // the block's V rows
+    int16_t p[NWH][TILE], cp[NWH][TILE];  // per wavefront: probabilities, c(p)
+    v4u part[2][NWH][TILE];               // QK bank partials (int32), by tile parity
+    int16_t e14[2056];                    // Q2.14 exp table
+};
+
+// This lane's cache operands of `tile`: the K chunks of its position
+// (cached positions only) over the wavefront's elements, and the V^T
+// chunks of element 32 w + lane % 32 over half lane / 32 of the tile.
+struct SplitRegs {
+    v4u k[4], v[4];
+};
+template <int D>
+__device__ __forceinline__ void split_load(const AttnArgs& a, uint32_t h, uint32_t tile,
+                                           uint32_t w, uint32_t lane, SplitRegs& R) {
+    const uint32_t p = tile * TILE + lane;
+    const int16_t* kp = a.kcache + page_off<D>(a, h, tile) + (size_t)lane * D + 32 * w;
+    const uint32_t e = 32 * w + (lane & 31), hh = lane >> 5;
+    const int16_t* vp = a.vcache + page_off<D>(a, h, tile) + (size_t)e * TILE + 32 * hh;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        R.k[c] = p < a.pos0 ? *(const v4u*)(kp + 8 * c) : v4u{0, 0, 0, 0};
+        R.v[c] = tile * TILE + 32 * hh + 8 * c < a.pos0 ? *(const v4u*)(vp + 8 * c)
+                                                         : v4u{0, 0, 0, 0};
+    }
+}
+
+template <int D>
+__global__ __launch_bounds__(D * 2) void attention_split_head_kernel(AttnArgs a) {
+    static_assert(D % 32 == 0, "split-head path: head_dim a multiple of 32");
+    constexpr uint32_t NTH = D * 2;  // D / 32 wavefronts
+    __shared__ SplitSmem<D> sm;
+    const uint32_t t = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
+    const uint32_t lane = tid & 63, w = tid >> 6;
+    const uint32_t h = g / a.group;
+    const uint32_t n = a.pos0 + t + 1, own = n - 1;
+    const uint32_t ntiles = (n + TILE - 1) / TILE;
+    const int64_t scale = (int64_t)a.qk_scale << 8;
+
+    // ---- the first tile's cache rows, the exp table, query and block rows ----
+    SplitRegs regs;
+    split_load<D>(a, h, 0, w, lane, regs);
+    for (uint32_t c = tid; c < 257; c += NTH)
+        *(v4u*)(sm.e14 + 8 * c) = *(const v4u*)(a.exp14 + 8 * c);
+    if (tid < D / 2) {
+        const int16_t* qrow = a.qkv + (size_t)t * a.ldqkv + (size_t)g * D;
+        const int16_t* qrope = a.rope + (size_t)own * D;
+        int32_t y0, y1;
+        rope_pair(qrow[tid], qrow[D / 2 + tid], qrope[tid], qrope[D / 2 + tid], y0, y1);
+        sm.q[paired(tid)] = (int16_t)y0;
+        sm.q[paired(D / 2 + tid)] = (int16_t)y1;
+        sm.cq[paired(tid)] = (int16_t)sat_corr(y0);
+        sm.cq[paired(D / 2 + tid)] = (int16_t)sat_corr(y1);
+    }
+    for (uint32_t i = tid; i < (t + 1) * (D / 2); i += NTH) {
+        const uint32_t r = i / (D / 2), c = i % (D / 2);
+        const int16_t* krow = a.qkv + (size_t)r * a.ldqkv + (size_t)a.num_heads * D +
+                              (size_t)h * D;
+        const int16_t* kr = a.rope + (size_t)(a.pos0 + r) * D;
+        int32_t y0, y1;
+        rope_pair(krow[c], krow[D / 2 + c], kr[c], kr[D / 2 + c], y0, y1);
+        sm.kc[r][paired(c)] = (int16_t)y0;
+        sm.kc[r][paired(D / 2 + c)] = (int16_t)y1;
+    }
+    for (uint32_t i = tid; i < (t + 1) * D; i += NTH) {
+        const uint32_t r = i / D, e = i % D;
+        sm.vc[r][e] = a.qkv[(size_t)r * a.ldqkv +
+                            (size_t)(a.num_heads + a.num_kv_heads) * D + (size_t)h * D + e];
+    }
+    __syncthreads();
+
+    const uint32_t el = lane & 31, hh = lane >> 5, e = 32 * w + el;
+    int32_t m = INT16_MIN, sum = 0, acc = 0;
+    for (uint32_t tile = 0; tile < ntiles; tile++) {
+        const SplitRegs cur = regs;
+        if (tile + 1 < ntiles) split_load<D>(a, h, tile + 1, w, lane, regs);
+        // ---- QK partials over this wavefront's elements ----
+        const uint32_t p = tile * TILE + lane;
+        const bool valid = p < n;
+        const bool blk = p >= a.pos0 && p <= own;  // K row of this block
+        const int16_t* kb = sm.kc[blk ? p - a.pos0 : 0] + 32 * w;
+        v4u kr[4];
+        s16x2 mk = {-32768, -32768};
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+            kr[c] = clamp4m(blk ? *(const v4u*)(kb + 8 * c) : cur.k[c], mk);
+        const bool kcorr = __any(sat_any(mk));
+        int32_t b0 = 0, b1 = 0, b2 = 0, b3 = 0;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const v4u qv = *(const v4u*)(sm.q + 32 * w + 8 * c);
+            b0 = dot2(kr[c].x, qv.x, b0);
+            b1 = dot2(kr[c].y, qv.y, b1);
+            b2 = dot2(kr[c].z, qv.z, b2);
+            b3 = dot2(kr[c].w, qv.w, b3);
+        }
+        if (kcorr) {
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const v4u cv = *(const v4u*)(sm.cq + 32 * w + 8 * c);
+                b0 = dot2(sat_mask(kr[c].x), cv.x, b0);
+                b1 = dot2(sat_mask(kr[c].y), cv.y, b1);
+                b2 = dot2(sat_mask(kr[c].z), cv.z, b2);
+                b3 = dot2(sat_mask(kr[c].w), cv.w, b3);
+            }
+        }
+        sm.part[tile & 1][w][lane] = v4u{(uint32_t)b0, (uint32_t)b1, (uint32_t)b2, (uint32_t)b3};
+        __syncthreads();  // every wavefront's partials
+        uint32_t s0 = 0, s1 = 0, s2 = 0, s3 = 0;  // bank sums mod 2^32
+#pragma unroll
+        for (int ww = 0; ww < SplitSmem<D>::NWH; ww++) {
+            const v4u pv = sm.part[tile & 1][ww][lane];
+            s0 += pv.x;
+            s1 += pv.y;
+            s2 += pv.z;
+            s3 += pv.w;
+        }
+        // +2^31 (one saturating bank) wraps to INT32_MIN
+        const int64_t t64 = (int64_t)((int32_t)s0 == INT32_MIN ? INT32_MAX : (int32_t)s0) +
+                            ((int32_t)s1 == INT32_MIN ? INT32_MAX : (int32_t)s1) +
+                            ((int32_t)s2 == INT32_MIN ? INT32_MAX : (int32_t)s2) +
+                            ((int32_t)s3 == INT32_MIN ? INT32_MAX : (int32_t)s3);
+        int32_t ts32 = fx_sat32(t64);
+        ts32 = fx_sat32(fx_rnd((int64_t)ts32 * scale, 16));
+        const int32_t s = valid ? fx_sat16(fx_rnd(ts32, 8)) : INT16_MIN;
+        // ---- softmax state (the same in every wavefront) ----
+        const int32_t wm = wave_max(s);
+        const int32_t mn = wm > m ? wm : m;
+        const int32_t old = prob(sm.e14, m - mn);
+        const int32_t pr = valid ? prob(sm.e14, s - mn) : 0;
+        sm.p[w][paired(lane)] = (int16_t)pr;
+        sm.cp[w][paired(lane)] = (int16_t)sat_corr(pr);
+        const int32_t tsum = wave_sum(pr);  // <= 64 * 16384
+        sum = fx_sat32(fx_rnd((int64_t)sum * ((int64_t)old << 2) + ((int64_t)tsum << 18), 16));
+        m = mn;
+        if (old != 16384) acc = fx_sat32(fx_rnd((int64_t)acc * ((int64_t)old << 2), 16));
+        // ---- PV over half hh of the tile for element e ----
+        v4u vr[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) vr[c] = cur.v[c];
+        // the block's V rows in this tile go to their own slots (slots
+        // beyond the context meet probability 0)
+        for (uint32_t r = 0; r <= t; r++) {
+            const uint32_t pp = a.pos0 + r;
+            if (pp / TILE != tile) continue;
+            const uint32_t slot = paired(pp % TILE);
+            if (slot / 32 != hh) continue;
+#pragma unroll
+            for (int c = 0; c < 4; c++)
+                if ((slot % 32) / 8 == (uint32_t)c) vr[c] = put_half(vr[c], slot % 8, sm.vc[r][e]);
+        }
+        s16x2 mv = {-32768, -32768};
+#pragma unroll
+        for (int c = 0; c < 4; c++) vr[c] = clamp4m(vr[c], mv);
+        const bool vcorr = __any(sat_any(mv));
+        b0 = b1 = b2 = b3 = 0;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const v4u pv = *(const v4u*)(sm.p[w] + 32 * hh + 8 * c);
+            b0 = dot2(vr[c].x, pv.x, b0);
+            b1 = dot2(vr[c].y, pv.y, b1);
+            b2 = dot2(vr[c].z, pv.z, b2);
+            b3 = dot2(vr[c].w, pv.w, b3);
+        }
+        if (vcorr) {
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const v4u cv = *(const v4u*)(sm.cp[w] + 32 * hh + 8 * c);
+                b0 = dot2(sat_mask(vr[c].x), cv.x, b0);
+                b1 = dot2(sat_mask(vr[c].y), cv.y, b1);
+                b2 = dot2(sat_mask(vr[c].z), cv.z, b2);
+                b3 = dot2(sat_mask(vr[c].w), cv.w, b3);
+            }
+        }
+        // the two halves of each bank (PV banks never leave the range)
+        b0 += __shfl_xor(b0, 32, 64);
+        b1 += __shfl_xor(b1, 32, 64);
+        b2 += __shfl_xor(b2, 32, 64);
+        b3 += __shfl_xor(b3, 32, 64);
+        int32_t tv = fx_sat32((int64_t)b0 + b1 + b2 + b3);
+        tv = fx_sat32(fx_rnd((int64_t)tv * 1024, 16));
+        tv = fx_sat16(fx_rnd(tv, 8));
+        acc = fx_sat32((int64_t)acc + ((int64_t)tv << 8));
+    }
+    const int64_t inv = fx_inv_sum(sum);
+    if (hh == 0)
+        a.out[(size_t)t * a.ldo + (size_t)g * D + e] = fx_sat16(fx_rnd((int64_t)acc * inv, 16));
+    if (g % a.group == 0) {  // this row's K (rotated, paired) and V into the cache
+        const uint32_t tile = own / TILE, slot = own % TILE;
+        if (tid < D / 8)
+            *(v4u*)(a.kcache + page_off<D>(a, h, tile) + slot * D + 8 * tid) =
+                *(const v4u*)(sm.kc[t] + 8 * tid);
+        if (tid < D) a.vcache[page_off<D>(a, h, tile) + tid * TILE + paired(slot)] = sm.vc[t][tid];
+    }
+}
+// ---------------------------------------------------------------------
 // Split path, phase A: scores and tile maxima for a chunk of tiles; the
 // row's own K is appended by the chunk that holds its position.
 // grid (rows, kv_heads, chunks).
@@ -920,7 +1139,10 @@ static hipError_t launch_d(const AttnArgs& a, uint32_t rows, uint32_t kv_heads,
     if (chunks <= 1) {
         // a wavefront per (row, query head) for single rows and pairs; a
         // workgroup per (row, KV head) beyond (measured at configs[1])
-        if (rows <= kHeadPathRows)
+        if (D % 32 == 0 && rows <= kSplitHeadRows)
+            attention_split_head_kernel<D % 32 == 0 ? D : 32>
+                <<<dim3(rows, a.num_heads), 2 * D, 0, st>>>(a);
+        else if (rows <= kHeadPathRows)
             attention_head_kernel<D><<<dim3(rows, a.num_heads), 64, 0, st>>>(a);
         else
             attention_fused_kernel<D><<<dim3(rows, kv_heads), NT, 0, st>>>(a);

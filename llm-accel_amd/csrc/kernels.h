@@ -96,7 +96,7 @@ struct MfSplit {
 };
 MfSplit mf_split(uint32_t nc, uint32_t kq);
 // int32 words of partial sums per (chunk, part) record.
-constexpr uint32_t mf_part_words(uint32_t nm) { return nm * 3 * 256 + 32; }
+constexpr uint32_t mf_part_words(uint32_t nm) { return nm * 2 * 256 + 32; }
 bool proj_uses_mfma(const ProjArgs& a, int epi);
 hipError_t launch_proj(const ProjArgs& a, int epi, int L, uint32_t blocks,
                        hipStream_t st);

@@ -23,17 +23,26 @@
 #ifndef LLM_PROJ_UNROLL
 #define LLM_PROJ_UNROLL 2   // k-steps whose loads are issued together
 #endif
+#ifndef LLM_PROJ_UNROLL_LONG
+#define LLM_PROJ_UNROLL_LONG 2  // the same for 16-wavefront blocks
+#endif
 #ifndef LLM_PROJ_LONG_STEPS
 #define LLM_PROJ_LONG_STEPS 48  // k-steps from which 1-2 row blocks use 16 waves
 #endif
-#ifndef LLM_MF_LOADFIRST
-#define LLM_MF_LOADFIRST 0  // matrix-core kernel: all loads before products
+#ifndef LLM_MF_KS
+#define LLM_MF_KS 8         // matrix-core kernel: wavefronts per workgroup
 #endif
 #ifndef LLM_MF_WG_TARGET
-#define LLM_MF_WG_TARGET 256  // matrix-core kernel: workgroups to aim for
+#define LLM_MF_WG_TARGET 128  // matrix-core kernel: split K below this many workgroups
 #endif
-#ifndef LLM_MF_KS_MAX
-#define LLM_MF_KS_MAX 16    // matrix-core kernel: wavefronts per workgroup
+#ifndef LLM_MF_QMAX
+#define LLM_MF_QMAX 12      // matrix-core kernel: K chunks per wavefront (<= 12)
+#endif
+#ifndef LLM_MF_PD1
+#define LLM_MF_PD1 4        // K chunks of loads in flight per wavefront, one matrix
+#endif
+#ifndef LLM_MF_PD2
+#define LLM_MF_PD2 2        // the same for gate|up (two matrices)
 #endif
 
 namespace llm {
@@ -51,6 +60,19 @@ __device__ __forceinline__ int64_t dot2_wide(uint32_t a, uint32_t b) {
     int32_t a0 = (int16_t)(a & 0xffff), a1 = (int16_t)(a >> 16);
     int32_t b0 = (int16_t)(b & 0xffff), b1 = (int16_t)(b >> 16);
     return (int64_t)(a0 * b0) + (int64_t)(a1 * b1);
+}
+
+// All-ones when `keep`, else zero, as a per-lane value the compiler cannot
+// turn back into a branch: a wave-uniform select would let it sink the
+// loads that feed the masked value into a conditional block, one memory
+// round trip after another.
+__device__ __forceinline__ uint32_t lane_mask(bool keep) {
+    uint32_t m = keep ? 0xffffffffu : 0u;
+    asm volatile("" : "+v"(m));
+    return m;
+}
+__device__ __forceinline__ uint4 and4(uint4 v, uint32_t m) {
+    return make_uint4(v.x & m, v.y & m, v.z & m, v.w & m);
 }
 
 // ---------------------------------------------------------------------
@@ -167,7 +189,11 @@ __device__ __forceinline__ void proj_out(const ProjArgs& a, uint32_t r, uint32_t
     a.out[(size_t)r * a.ldo + n] = y;
 }
 
-template <int RT, int L, int EPI, int WPB>
+// SPW > 0: every wavefront has at most SPW k-steps and issues all of their
+// loads (weights, activations, gammas) before the first product; loads past
+// its last step repeat that step (in bounds, products of zero).  SPW = 0:
+// a loop over the steps, LLM_PROJ_UNROLL steps of loads at a time.
+template <int RT, int L, int EPI, int WPB, int SPW>
 __global__ __launch_bounds__(64 * WPB) void proj_kernel(ProjArgs a) {
     constexpr int NM = EPI == EPI_SILU ? 2 : 1;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -201,9 +227,59 @@ __global__ __launch_bounds__(64 * WPB) void proj_kernel(ProjArgs a) {
         ? a.w1 + ((size_t)(b * S + s0) * 4 + i) * 128 + j * 8 : nullptr;
     const int16_t* xp = a.x + (size_t)s0 * 128 + j * 8;
 
-    for (uint32_t s = s0; s < s1;) {
+    if constexpr (SPW > 0) {
+        const uint32_t cnt = s1 - s0;  // <= SPW (the launcher's choice)
+        uint4 wv[SPW][NM], xv[SPW][RT], gv[SPW];
+#pragma unroll
+        for (int u = 0; u < SPW; u++) {
+            const uint32_t du = cnt == 0 ? 0 : ((uint32_t)u < cnt ? u : cnt - 1);
+            wv[u][0] = *(const uint4*)(wp0 + (size_t)du * 512);
+            if (NM == 2) wv[u][NM - 1] = *(const uint4*)(wp1 + (size_t)du * 512);
+#pragma unroll
+            for (int r = 0; r < RT; r++)
+                xv[u][r] = *(const uint4*)(xp + (size_t)r * a.ldx + du * 128);
+            if (EPI == EPI_STORE_NORM_IN)
+                gv[u] = *(const uint4*)(a.in_gamma + (s0 + du) * 128 + j * 8);
+        }
+        // every step is computed: no branch may separate a load from its
+        // use, or the compiler sinks the load into the branch; steps past
+        // the wavefront's last contribute zero weights
+#pragma unroll
+        for (int u = 0; u < SPW; u++) {
+            const uint32_t keep = lane_mask((uint32_t)u < cnt);
+#pragma unroll
+            for (int m = 0; m < NM; m++) wv[u][m] = and4(wv[u][m], keep);
+            if (EPI == EPI_STORE_NORM_IN) {
+#pragma unroll
+                for (int r = 0; r < RT; r++) xv[u][r] = norm8(xv[u][r], gv[u], a.in_gain);
+            }
+#pragma unroll
+            for (int m = 0; m < NM; m++)
+#pragma unroll
+                for (int r = 0; r < RT; r++) {
+                    int32_t p = part[m][r];
+                    p = dot2(wv[u][m].x, xv[u][r].x, p);
+                    p = dot2(wv[u][m].y, xv[u][r].y, p);
+                    p = dot2(wv[u][m].z, xv[u][r].z, p);
+                    p = dot2(wv[u][m].w, xv[u][r].w, p);
+                    part[m][r] = p;
+                }
+            if (L < SPW && (u + 1) % L == 0) {
+#pragma unroll
+                for (int m = 0; m < NM; m++)
+#pragma unroll
+                    for (int r = 0; r < RT; r++) acc[m][r] += part[m][r], part[m][r] = 0;
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < NM; m++)
+#pragma unroll
+            for (int r = 0; r < RT; r++) acc[m][r] += part[m][r];
+    }
+    constexpr int UNR = WPB >= 16 ? LLM_PROJ_UNROLL_LONG : LLM_PROJ_UNROLL;
+    for (uint32_t s = s0; SPW == 0 && s < s1;) {
         const uint32_t lim = (L == 0) ? s1 : (s + L < s1 ? s + L : s1);
-#pragma unroll LLM_PROJ_UNROLL
+#pragma unroll UNR
         for (; s < lim; s++) {
             uint4 wv[NM];
             wv[0] = *(const uint4*)(wp0);
@@ -294,27 +370,34 @@ __global__ __launch_bounds__(64 * WPB) void proj_kernel(ProjArgs a) {
 //   sum w x = 65536 sum ac + 256 (sum ad + sum bc) + sum bd
 //           + 32768 sum a + 128 sum b + 32768 sum c + 128 sum d + 16384 K
 // over the padded K (zero weights pad; whatever the activations hold there
-// enters both sides alike).  The three sums of products run on
-// v_mfma_i32_16x16x64_i8 (A = 16 activation rows, rows >= `rows` zero;
-// B = 16 outputs), each bounded by 2^15 K < 2^31 for K <= 32768; the
-// weight sums come with the layout, the activation sums from v_dot4.
+// enters both sides alike).  The 16 rows of the A operand of
+// v_mfma_i32_16x16x64_i8 hold both byte planes of the (at most 8)
+// activation rows: row r < 8 the high bytes c of activation row r, row
+// 8 + r its low bytes d.  One product with the weights' high plane then
+// gives sum ac (rows 0-7) and sum ad (rows 8-15), one with the low plane
+// sum bc and sum bd: two matrix products per matrix and K chunk.  Each sum
+// is bounded by 2^14 K < 2^31 for K <= 32768; the weight sums come with the
+// layout, the activation sums from v_dot4.  Rows of the A operand whose
+// activation row is not active carry whatever the buffer holds and only
+// reach outputs that are not read.
 // Workgroup = KS wavefronts on one 16-output chunk, splitting the K
-// chunks; LDS reduction, then the shared epilogue.
+// chunks; every wavefront keeps PD chunks of loads in flight.  LDS
+// reduction over the wavefronts, then the shared epilogue.
 // ---------------------------------------------------------------------
 typedef int32_t v4i __attribute__((ext_vector_type(4)));
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 
-// 16 int16 activations (two 16-byte loads) -> high bytes and biased low
-// bytes, element e in byte e.
-__device__ __forceinline__ void split16(const v4u& x0, const v4u& x1, v4i& hi, v4i& lo) {
-    hi.x = (int32_t)__builtin_amdgcn_perm(x0.y, x0.x, 0x07050301u);
-    hi.y = (int32_t)__builtin_amdgcn_perm(x0.w, x0.z, 0x07050301u);
-    hi.z = (int32_t)__builtin_amdgcn_perm(x1.y, x1.x, 0x07050301u);
-    hi.w = (int32_t)__builtin_amdgcn_perm(x1.w, x1.z, 0x07050301u);
-    lo.x = (int32_t)(__builtin_amdgcn_perm(x0.y, x0.x, 0x06040200u) ^ 0x80808080u);
-    lo.y = (int32_t)(__builtin_amdgcn_perm(x0.w, x0.z, 0x06040200u) ^ 0x80808080u);
-    lo.z = (int32_t)(__builtin_amdgcn_perm(x1.y, x1.x, 0x06040200u) ^ 0x80808080u);
-    lo.w = (int32_t)(__builtin_amdgcn_perm(x1.w, x1.z, 0x06040200u) ^ 0x80808080u);
+// 16 int16 activations (two 16-byte loads) -> high bytes (hi_plane) or
+// biased low bytes, element e in byte e.
+__device__ __forceinline__ v4i split16(const v4u& x0, const v4u& x1, bool hi_plane) {
+    const uint32_t sel = hi_plane ? 0x07050301u : 0x06040200u;
+    const uint32_t bias = hi_plane ? 0u : 0x80808080u;
+    v4i r;
+    r.x = (int32_t)(__builtin_amdgcn_perm(x0.y, x0.x, sel) ^ bias);
+    r.y = (int32_t)(__builtin_amdgcn_perm(x0.w, x0.z, sel) ^ bias);
+    r.z = (int32_t)(__builtin_amdgcn_perm(x1.y, x1.x, sel) ^ bias);
+    r.w = (int32_t)(__builtin_amdgcn_perm(x1.w, x1.z, sel) ^ bias);
+    return r;
 }
 __device__ __forceinline__ int32_t byte_sum(const v4i& v, int32_t acc) {
     acc = __builtin_amdgcn_sdot4(v.x, 0x01010101, acc, false);
@@ -323,47 +406,84 @@ __device__ __forceinline__ int32_t byte_sum(const v4i& v, int32_t acc) {
     return __builtin_amdgcn_sdot4(v.w, 0x01010101, acc, false);
 }
 
-// One K chunk: activations (normalised first for EPI_STORE_NORM_IN) split
-// into bytes, their sums, and the four products per matrix.
+// Operands of one K chunk as loaded: both weight planes per matrix, the
+// lane's 16 activations and, for EPI_STORE_NORM_IN, their 16 gammas.
 template <int NM, int EPI>
-__device__ __forceinline__ void mf_chunk(const ProjArgs& a, uint32_t q, uint32_t g,
-                                         v4u x0, v4u x1, const v4i* bh, const v4i* bl,
-                                         v4i* cac, v4i* cmix, v4i* cbd,
-                                         int32_t& sc, int32_t& sd) {
-    if (EPI == EPI_STORE_NORM_IN) {
-        const uint32_t k0 = 64 * q + 16 * g;
-        const uint4 ga = k0 < a.in_cols ? *(const uint4*)(a.in_gamma + k0)
-                                        : make_uint4(0, 0, 0, 0);
-        const uint4 gb = k0 + 8 < a.in_cols ? *(const uint4*)(a.in_gamma + k0 + 8)
-                                            : make_uint4(0, 0, 0, 0);
-        const uint4 n0 = norm8(make_uint4(x0.x, x0.y, x0.z, x0.w), ga, a.in_gain);
-        const uint4 n1 = norm8(make_uint4(x1.x, x1.y, x1.z, x1.w), gb, a.in_gain);
-        x0 = v4u{n0.x, n0.y, n0.z, n0.w};
-        x1 = v4u{n1.x, n1.y, n1.z, n1.w};
-    }
-    v4i ah, al;
-    split16(x0, x1, ah, al);
-    sc = byte_sum(ah, sc);
-    sd = byte_sum(al, sd);
+struct MfChunk {
+    v4i bh[NM], bl[NM];
+    v4u x0, x1;
+    v4u g0, g1;
+};
+
+template <int NM, int EPI>
+__device__ __forceinline__ void mf_load(const ProjArgs& a, const int8_t* const* bp,
+                                        const int16_t* xp, const int16_t* gp, uint32_t q,
+                                        MfChunk<NM, EPI>& ch) {
 #pragma unroll
     for (int m = 0; m < NM; m++) {
-        cac[m] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, bh[m], cac[m], 0, 0, 0);
-        cmix[m] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, bl[m], cmix[m], 0, 0, 0);
-        cmix[m] = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, bh[m], cmix[m], 0, 0, 0);
-        cbd[m] = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, bl[m], cbd[m], 0, 0, 0);
+        ch.bh[m] = *(const v4i*)(bp[m] + (size_t)q * kMfRecord);
+        ch.bl[m] = *(const v4i*)(bp[m] + (size_t)q * kMfRecord + 1024);
+    }
+    ch.x0 = *(const v4u*)(xp + 64 * q);
+    ch.x1 = *(const v4u*)(xp + 64 * q + 8);
+    if (EPI == EPI_STORE_NORM_IN) {
+        // unconditional: the norm table is padded by a whole k-step, and
+        // past in_cols the activations are 0 and so is the normalised value
+        ch.g0 = *(const v4u*)(gp + 64 * q);
+        ch.g1 = *(const v4u*)(gp + 64 * q + 8);
     }
 }
 
-template <int NM, int KS, int QM, int EPI>
+// One K chunk: activations (normalised first for EPI_STORE_NORM_IN) to the
+// lane's byte plane, its byte sum, two products per matrix.
+template <int NM, int EPI>
+__device__ __forceinline__ void mf_compute(const ProjArgs& a, const MfChunk<NM, EPI>& ch,
+                                           bool hi_plane, bool ok, v4i* c1, v4i* c2,
+                                           int32_t& rs) {
+    v4u x0 = ch.x0, x1 = ch.x1;
+    if (EPI == EPI_STORE_NORM_IN) {
+        const uint4 n0 = norm8(make_uint4(x0.x, x0.y, x0.z, x0.w),
+                               make_uint4(ch.g0.x, ch.g0.y, ch.g0.z, ch.g0.w), a.in_gain);
+        const uint4 n1 = norm8(make_uint4(x1.x, x1.y, x1.z, x1.w),
+                               make_uint4(ch.g1.x, ch.g1.y, ch.g1.z, ch.g1.w), a.in_gain);
+        x0 = v4u{n0.x, n0.y, n0.z, n0.w};
+        x1 = v4u{n1.x, n1.y, n1.z, n1.w};
+    }
+    // chunks past the wavefront's last (ok false) contribute zero
+    // activations; the caller computes them anyway, so that no branch
+    // separates a load from its use
+    const int32_t keep = (int32_t)lane_mask(ok);
+    const v4i av = split16(x0, x1, hi_plane) & v4i{keep, keep, keep, keep};
+    rs = byte_sum(av, rs);
+#pragma unroll
+    for (int m = 0; m < NM; m++) {
+        c1[m] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, ch.bh[m], c1[m], 0, 0, 0);
+        c2[m] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, ch.bl[m], c2[m], 0, 0, 0);
+    }
+}
+
+// Exact sum (int64) of output (r, n) from its four product sums, the weight
+// sums (m0 = sum a, m1 = sum b), the activation sums and K.
+__device__ __forceinline__ int64_t mf_total(int64_t ac, int64_t ad, int64_t bc, int64_t bd,
+                                            int32_t m0, int32_t m1, int64_t sc, int64_t sd,
+                                            int64_t k64) {
+    return 65536 * ac + 256 * (ad + bc) + bd + 32768 * (int64_t)m0 + 128 * (int64_t)m1 +
+           32768 * sc + 128 * sd + 16384 * k64;
+}
+
+template <int NM, int KS, int QM, int PD, int EPI>
 __global__ __launch_bounds__(64 * KS) void proj_mfma_kernel(ProjArgs a, uint32_t parts) {
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t c = blockIdx.x / parts, p = blockIdx.x % parts, KQ = a.kq;
     const uint32_t pq0 = p * KQ / parts, pq1 = (p + 1) * KQ / parts;
     const uint32_t q0 = pq0 + wave * (pq1 - pq0) / KS;
     const uint32_t q1 = pq0 + (wave + 1) * (pq1 - pq0) / KS;
+    const uint32_t n = q1 - q0;  // <= QM (the launcher's choice)
     const uint32_t i = lane & 15, g = lane >> 4;
-    const bool xrow = i < a.rows;
-    const int16_t* xp = a.x + (size_t)(xrow ? i : 0) * a.ldx + 16 * g;
+    const bool hi_plane = i < 8;
+    // every activation buffer holds 8 rows: row i & 7 is always in bounds
+    const int16_t* xp = a.x + (size_t)(i & 7) * a.ldx + 16 * g;
+    const int16_t* gp = EPI == EPI_STORE_NORM_IN ? a.in_gamma + 16 * g : nullptr;
     // epilogue operands of this thread's first output t = threadIdx.x
     const uint32_t et = threadIdx.x, er = et >> 4, en = c * kMfRows + (et & 15);
     EpiIn ei{0, 0, 0};
@@ -385,152 +505,115 @@ __global__ __launch_bounds__(64 * KS) void proj_mfma_kernel(ProjArgs a, uint32_t
     const int8_t* bp[NM];
     bp[0] = a.mf0 + (size_t)c * KQ * kMfRecord + lane * 16;
     if (NM == 2) bp[NM - 1] = a.mf1 + (size_t)c * KQ * kMfRecord + lane * 16;
-    v4i cac[NM], cmix[NM], cbd[NM];
+    v4i c1[NM], c2[NM];
 #pragma unroll
-    for (int m = 0; m < NM; m++) cac[m] = cmix[m] = cbd[m] = v4i{0, 0, 0, 0};
-    int32_t sc = 0, sd = 0;
-#if LLM_MF_LOADFIRST
-    // every load of this wavefront's K chunks is issued before the first
-    // product (q1 - q0 <= QM)
-    v4i bh[QM][NM], bl[QM][NM];
-    v4u x0[QM], x1[QM];
+    for (int m = 0; m < NM; m++) c1[m] = c2[m] = v4i{0, 0, 0, 0};
+    int32_t rs = 0;
+    // Chunk u of this wavefront is q0 + u; loads past the last chunk
+    // repeat it (in bounds, its products add zero).  A wavefront with no
+    // chunk reads chunk pq0 and uses none.
+    auto chunk_q = [&](uint32_t u) -> uint32_t {
+        return n == 0 ? pq0 : q0 + (u < n ? u : n - 1);
+    };
+    MfChunk<NM, EPI> ring[PD];
 #pragma unroll
-    for (int u = 0; u < QM; u++) {
-        const uint32_t q = q0 + u;
-        if (q < q1) {
-#pragma unroll
-            for (int m = 0; m < NM; m++) {
-                bh[u][m] = *(const v4i*)(bp[m] + (size_t)q * kMfRecord);
-                bl[u][m] = *(const v4i*)(bp[m] + (size_t)q * kMfRecord + 1024);
-            }
-            x0[u] = x1[u] = v4u{0, 0, 0, 0};
-            if (xrow) {
-                x0[u] = *(const v4u*)(xp + 64 * q);
-                x1[u] = *(const v4u*)(xp + 64 * q + 8);
-            }
-        }
-    }
+    for (int u = 0; u < PD; u++) mf_load<NM, EPI>(a, bp, xp, gp, chunk_q(u), ring[u]);
 #pragma unroll
     for (int u = 0; u < QM; u++) {
-        if (q0 + u < q1) {
-            mf_chunk<NM, EPI>(a, q0 + u, g, x0[u], x1[u], bh[u], bl[u], cac, cmix, cbd, sc, sd);
-        }
+        const MfChunk<NM, EPI> cur = ring[u % PD];
+        if (u + PD < QM) mf_load<NM, EPI>(a, bp, xp, gp, chunk_q(u + PD), ring[u % PD]);
+        mf_compute<NM, EPI>(a, cur, hi_plane, (uint32_t)u < n, c1, c2, rs);
     }
-#else
-#pragma unroll 4
-    for (uint32_t q = q0; q < q1; q++) {
-        v4i bh[NM], bl[NM];
-#pragma unroll
-        for (int m = 0; m < NM; m++) {
-            bh[m] = *(const v4i*)(bp[m] + (size_t)q * kMfRecord);
-            bl[m] = *(const v4i*)(bp[m] + (size_t)q * kMfRecord + 1024);
-        }
-        v4u x0 = v4u{0, 0, 0, 0}, x1 = x0;
-        if (xrow) {
-            x0 = *(const v4u*)(xp + 64 * q);
-            x1 = *(const v4u*)(xp + 64 * q + 8);
-        }
-        mf_chunk<NM, EPI>(a, q, g, x0, x1, bh, bl, cac, cmix, cbd, sc, sd);
-    }
-#endif
     // C lane l holds rows 4 (l / 16) + s, column l % 16.
-    __shared__ v4i red[KS][NM][3][64];
-    __shared__ int32_t rsum[KS][2][64];
+    __shared__ v4i red[KS][NM][2][64];
+    __shared__ int32_t rsum[KS][64];
     __shared__ uint32_t last;
 #pragma unroll
     for (int m = 0; m < NM; m++) {
-        red[wave][m][0][lane] = cac[m];
-        red[wave][m][1][lane] = cmix[m];
-        red[wave][m][2][lane] = cbd[m];
+        red[wave][m][0][lane] = c1[m];
+        red[wave][m][1][lane] = c2[m];
     }
-    rsum[wave][0][lane] = sc;
-    rsum[wave][1][lane] = sd;
+    rsum[wave][lane] = rs;
     __syncthreads();
-    // This workgroup's sums of element t = 16 r + j: [m][type] and the
-    // activation row sums, in int32 (each below 2^15 * K).
+    // element (row, col) of product ty of matrix m, summed over wavefronts
+    auto wsum = [&](int m, int ty, uint32_t row, uint32_t col) -> int32_t {
+        int32_t v = 0;
+#pragma unroll
+        for (int w = 0; w < KS; w++) v += red[w][m][ty][16 * (row >> 2) + col][row & 3];
+        return v;
+    };
+    // byte sum of A row `row` (activation row row & 7, plane row >> 3)
+    auto rsum_row = [&](uint32_t row) -> int32_t {
+        int32_t v = 0;
+#pragma unroll
+        for (int w = 0; w < KS; w++)
+#pragma unroll
+            for (int gg = 0; gg < 4; gg++) v += rsum[w][row + 16 * gg];
+        return v;
+    };
     constexpr uint32_t W = mf_part_words(NM);
-    int32_t* part = a.mf_part + (size_t)(c * parts + p) * W;
     if (parts > 1) {
+        // this workgroup's sums: element t = 16 row + col of each product,
+        // then the 16 A-row byte sums
+        int32_t* part = a.mf_part + (size_t)(c * parts + p) * W;
         for (uint32_t t = threadIdx.x; t < 256; t += 64 * KS) {
-            const uint32_t r = t >> 4, j = t & 15, cl = 16 * (r >> 2) + j, s = r & 3;
 #pragma unroll
             for (int m = 0; m < NM; m++)
 #pragma unroll
-                for (int ty = 0; ty < 3; ty++) {
-                    int32_t v = 0;
-#pragma unroll
-                    for (int w = 0; w < KS; w++) v += red[w][m][ty][cl][s];
-                    st_coherent(&part[(m * 3 + ty) * 256 + t], v);
-                }
-            if (j < 2) {
-                int32_t v = 0;
-#pragma unroll
-                for (int w = 0; w < KS; w++)
-#pragma unroll
-                    for (int gg = 0; gg < 4; gg++) v += rsum[w][j][r + 16 * gg];
-                st_coherent(&part[NM * 3 * 256 + 2 * r + j], v);
-            }
+                for (int ty = 0; ty < 2; ty++)
+                    st_coherent(&part[(m * 2 + ty) * 256 + t], wsum(m, ty, t >> 4, t & 15));
+            if (t < 16) st_coherent(&part[NM * 2 * 256 + t], rsum_row(t));
         }
         if (!arrive_last(&a.mf_count[c], parts, &last)) return;
     }
     const int64_t k64 = (int64_t)KQ * kMfCols;
     for (uint32_t t = threadIdx.x; t < 256; t += 64 * KS) {
-        const uint32_t r = t >> 4, j = t & 15, n = c * kMfRows + j;
-        if (n >= a.n) continue;
+        const uint32_t r = t >> 4, j = t & 15, nn = c * kMfRows + j;
+        if (nn >= a.n) continue;
         if (r < a.rows) {
-            const uint32_t cl = 16 * (r >> 2) + j, s = r & 3;
-            int64_t sums[NM][3], rc = 0, rd = 0;
+            int64_t s[NM][4], sc = 0, sd = 0;
             if (parts > 1) {
 #pragma unroll
-                for (int m = 0; m < NM; m++)
-#pragma unroll
-                    for (int ty = 0; ty < 3; ty++) sums[m][ty] = 0;
+                for (int m = 0; m < NM; m++) s[m][0] = s[m][1] = s[m][2] = s[m][3] = 0;
                 for (uint32_t pp = 0; pp < parts; pp++) {
                     const int32_t* q = a.mf_part + (size_t)(c * parts + pp) * W;
 #pragma unroll
-                    for (int m = 0; m < NM; m++)
-#pragma unroll
-                        for (int ty = 0; ty < 3; ty++)
-                            sums[m][ty] += ld_coherent(&q[(m * 3 + ty) * 256 + t]);
-                    rc += ld_coherent(&q[NM * 3 * 256 + 2 * r]);
-                    rd += ld_coherent(&q[NM * 3 * 256 + 2 * r + 1]);
+                    for (int m = 0; m < NM; m++) {
+                        s[m][0] += ld_coherent(&q[(m * 2) * 256 + 16 * r + j]);
+                        s[m][1] += ld_coherent(&q[(m * 2) * 256 + 16 * (8 + r) + j]);
+                        s[m][2] += ld_coherent(&q[(m * 2 + 1) * 256 + 16 * r + j]);
+                        s[m][3] += ld_coherent(&q[(m * 2 + 1) * 256 + 16 * (8 + r) + j]);
+                    }
+                    sc += ld_coherent(&q[NM * 2 * 256 + r]);
+                    sd += ld_coherent(&q[NM * 2 * 256 + 8 + r]);
                 }
             } else {
 #pragma unroll
-                for (int m = 0; m < NM; m++)
-#pragma unroll
-                    for (int ty = 0; ty < 3; ty++) {
-                        int64_t v = 0;
-#pragma unroll
-                        for (int w = 0; w < KS; w++) v += red[w][m][ty][cl][s];
-                        sums[m][ty] = v;
-                    }
-#pragma unroll
-                for (int w = 0; w < KS; w++)
-#pragma unroll
-                    for (int gg = 0; gg < 4; gg++) {
-                        rc += rsum[w][0][r + 16 * gg];
-                        rd += rsum[w][1][r + 16 * gg];
-                    }
+                for (int m = 0; m < NM; m++) {
+                    s[m][0] = wsum(m, 0, r, j);
+                    s[m][1] = wsum(m, 0, 8 + r, j);
+                    s[m][2] = wsum(m, 1, r, j);
+                    s[m][3] = wsum(m, 1, 8 + r, j);
+                }
+                sc = rsum_row(r);
+                sd = rsum_row(8 + r);
             }
             // later outputs of this thread (fewer than 4 wavefronts) fetch
             // their operands here
             const bool first = t == et;
-            EpiIn e = first ? ei : epi_fetch<EPI>(a, r, n);
+            EpiIn e = first ? ei : epi_fetch<EPI>(a, r, nn);
             int64_t tot[NM];
 #pragma unroll
             for (int m = 0; m < NM; m++) {
                 const int32_t* ms = m == 0 ? a.ms0 : a.ms1;
-                const int32_t m0 = first ? ems[m][0] : ms[2 * n];
-                const int32_t m1 = first ? ems[m][1] : ms[2 * n + 1];
-                tot[m] = 65536 * sums[m][0] + 256 * sums[m][1] + sums[m][2] +
-                         32768 * (int64_t)m0 + 128 * (int64_t)m1 + 32768 * rc + 128 * rd +
-                         16384 * k64;
+                const int32_t m0 = first ? ems[m][0] : ms[2 * nn];
+                const int32_t m1 = first ? ems[m][1] : ms[2 * nn + 1];
+                tot[m] = mf_total(s[m][0], s[m][1], s[m][2], s[m][3], m0, m1, sc, sd, k64);
             }
-            proj_out<EPI>(a, r, n, tot[0], tot[NM - 1], e, a.exp8);
+            proj_out<EPI>(a, r, nn, tot[0], tot[NM - 1], e, a.exp8);
         } else if (EPI == EPI_RESID && a.final_out && r < 8) {
-            a.final_out[(size_t)r * a.ldn + n] =
-                t == et ? fill : a.res[(size_t)r * a.ldr + n];
+            a.final_out[(size_t)r * a.ldn + nn] =
+                t == et ? fill : a.res[(size_t)r * a.ldr + nn];
         }
     }
 }
@@ -660,15 +743,31 @@ __global__ __launch_bounds__(256) void copy_kernel(const uint4* __restrict__ src
 // ---------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------
+template <int RT, int EPI, int W, int SPW>
+static void launch_proj_s(const ProjArgs& a, int L, uint32_t blocks, hipStream_t st) {
+    // SPW <= 4: the int32 sums of a wavefront's steps widen once at the
+    // end (L >= 4)
+    proj_kernel<RT, 4, EPI, W, SPW><<<blocks, 64 * W, 0, st>>>(a);
+}
+
 template <int RT, int EPI, int W>
 static hipError_t launch_proj_w(const ProjArgs& a, int L, uint32_t blocks,
                                 hipStream_t st) {
+    // all loads at once pays for up to 4 steps per wavefront; longer
+    // reductions (the down projection: 6) measured faster with the loop,
+    // two steps of loads at a time, at lower register use
+    const uint32_t spw = (a.steps + W - 1) / W;
+    if (RT <= 2 && L >= 4 && spw <= 4) {
+        if (spw <= 2) launch_proj_s<RT, EPI, W, 2>(a, L, blocks, st);
+        else launch_proj_s<RT, EPI, W, 4>(a, L, blocks, st);
+        return hipGetLastError();
+    }
     switch (L) {
-    case 0: proj_kernel<RT, 0, EPI, W><<<blocks, 64 * W, 0, st>>>(a); break;
-    case 1: proj_kernel<RT, 1, EPI, W><<<blocks, 64 * W, 0, st>>>(a); break;
-    case 4: proj_kernel<RT, 4, EPI, W><<<blocks, 64 * W, 0, st>>>(a); break;
-    case 8: proj_kernel<RT, 8, EPI, W><<<blocks, 64 * W, 0, st>>>(a); break;
-    default: proj_kernel<RT, 16, EPI, W><<<blocks, 64 * W, 0, st>>>(a); break;
+    case 0: proj_kernel<RT, 0, EPI, W, 0><<<blocks, 64 * W, 0, st>>>(a); break;
+    case 1: proj_kernel<RT, 1, EPI, W, 0><<<blocks, 64 * W, 0, st>>>(a); break;
+    case 4: proj_kernel<RT, 4, EPI, W, 0><<<blocks, 64 * W, 0, st>>>(a); break;
+    case 8: proj_kernel<RT, 8, EPI, W, 0><<<blocks, 64 * W, 0, st>>>(a); break;
+    default: proj_kernel<RT, 16, EPI, W, 0><<<blocks, 64 * W, 0, st>>>(a); break;
     }
     return hipGetLastError();
 }
@@ -701,27 +800,37 @@ static uint32_t mf_chunks_per_wave(uint32_t kq, uint32_t parts, uint32_t ks) {
 }
 
 MfSplit mf_split(uint32_t nc, uint32_t kq) {
-    // about LLM_MF_WG_TARGET workgroups, at least two K chunks per
-    // wavefront, at most 8
-    MfSplit s{4, 1};
+    // LLM_MF_KS wavefronts per workgroup (fewer when K is short), the K
+    // range split over workgroups only while the chunks alone give fewer
+    // than LLM_MF_WG_TARGET workgroups and each wavefront keeps two K
+    // chunks, or when a wavefront would get more than LLM_MF_QMAX
+    MfSplit s{LLM_MF_KS, 1};
+    while (s.ks > 4 && kq < 2 * s.ks) s.ks /= 2;
     while (nc * s.parts < LLM_MF_WG_TARGET && kq / (s.parts * 2) >= s.ks * 2) s.parts *= 2;
-    while (s.ks < LLM_MF_KS_MAX && kq / s.parts >= s.ks * 2 * 4) s.ks *= 2;
-    while (mf_chunks_per_wave(kq, s.parts, s.ks) > 8) s.parts *= 2;
+    while (mf_chunks_per_wave(kq, s.parts, s.ks) > LLM_MF_QMAX) s.parts *= 2;
     return s;
+}
+
+template <int NM, int KS, int QM, int EPI>
+static void launch_mfma_k(const ProjArgs& a, uint32_t parts, hipStream_t st) {
+    constexpr int PD0 = NM == 2 ? LLM_MF_PD2 : LLM_MF_PD1;
+    constexpr int PD = PD0 < QM ? PD0 : QM;
+    proj_mfma_kernel<NM, KS, QM, PD, EPI><<<a.nc * parts, 64 * KS, 0, st>>>(a, parts);
 }
 
 template <int NM, int KS, int EPI>
 static hipError_t launch_mfma_q(const ProjArgs& a, uint32_t parts, hipStream_t st) {
     const uint32_t qm = mf_chunks_per_wave(a.kq, parts, KS);
-    const dim3 grid(a.nc * parts);
     if (qm <= 2)
-        proj_mfma_kernel<NM, KS, 2, EPI><<<grid, 64 * KS, 0, st>>>(a, parts);
+        launch_mfma_k<NM, KS, 2, EPI>(a, parts, st);
     else if (qm <= 4)
-        proj_mfma_kernel<NM, KS, 4, EPI><<<grid, 64 * KS, 0, st>>>(a, parts);
+        launch_mfma_k<NM, KS, 4, EPI>(a, parts, st);
     else if (qm <= 8)
-        proj_mfma_kernel<NM, KS, 8, EPI><<<grid, 64 * KS, 0, st>>>(a, parts);
+        launch_mfma_k<NM, KS, 8, EPI>(a, parts, st);
+    else if (qm <= 12)
+        launch_mfma_k<NM, KS, 12, EPI>(a, parts, st);
     else
-        return hipErrorInvalidConfiguration;  // mf_split keeps qm <= 8
+        return hipErrorInvalidConfiguration;  // mf_split keeps qm <= LLM_MF_QMAX <= 12
     return hipGetLastError();
 }
 
