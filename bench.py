@@ -45,6 +45,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--sweep", action=argparse.BooleanOptionalAction, default=True,
                     help="configs[3] decode context sweep (extra field)")
+    ap.add_argument("--full", action=argparse.BooleanOptionalAction, default=True,
+                    help="configs[2] and configs[4] request loops (extra fields)")
     return ap.parse_args()
 
 
@@ -154,6 +156,52 @@ def context_sweep(llm_accel, workloads, spec, synth):
     return out
 
 
+def request_loop(llm_accel, workloads, spec, layers, prompt_len, gen, emb, lm_head):
+    """`layers` Qwen2.5-3B-shaped layers
+    (seeded synthetic weights, embedding and LM head), the reference's
+    generate loop through llm_generate: the prompt in 8-row blocks through
+    every layer (Task 18 / 19 per layer, Task 20 after the last block), then
+    `gen` sampled tokens, each the device LM-head argmax of the last row
+    with a one-row forward for every token but the last; hidden state and
+    KV cache stay in HBM throughout.  decode tok/s = generated forwards /
+    their time, LM head excluded (decode_token_s, host/host_qwen_8x64.cpp
+    :9265-9273); times are host clocks around each forward, as the
+    reference reports them."""
+    t0 = time.perf_counter()
+    s = workloads.with_layers(spec, layers, max_seq=prompt_len + gen)
+    synth = workloads.SyntheticModel(s)
+    shape = llm_accel.Shape(spec.vocab, spec.hidden, spec.inter, layers,
+                            spec.heads, spec.kv_heads, prompt_len + gen, 1e6)
+    with llm_accel.Accelerator(shape, num_pairs=4) as a:
+        a.load_model(synth)
+        prompt = [int(t) for t in synth.tokens(prompt_len)]
+        del synth
+        a.load_lm_head(lm_head)
+        setup_s = time.perf_counter() - t0
+        # one short warm-up request (kernels, page tables), then the run
+        a.generate(emb, prompt[:8], 8, layers, 2)
+        toks, st = a.generate(emb, prompt, 8, layers, gen)
+    dec_ms = st["generated_forward_ms"] / max(st["generated_forward_passes"], 1)
+    blocks = st["prompt_forward_passes"]
+    kv_bytes = 4 * spec.kv_heads * spec.head_dim * (prompt_len + gen / 2)
+    return {
+        "workload": f"{layers} layers, P{prompt_len}/G{gen}, 8-row prompt blocks, "
+                    "device LM-head argmax",
+        "decode_tok_s": 1e3 / dec_ms,
+        "decode_forward_ms": dec_ms,
+        "decode_hbm_frac": layers * (layer_bytes(spec) + kv_bytes) / (dec_ms * 1e-3)
+                           / 1e9 / HBM_PEAK_GBS,
+        "prompt_ms": st["prompt_forward_ms"],
+        "p8_block_us_per_layer": st["prompt_forward_ms"] * 1e3 / (blocks * layers),
+        "time_to_first_token_ms": st["time_to_first_token_ms"],
+        "lm_head_ms_per_token": st["lm_head_ms"] / max(st["generated_tokens"], 1),
+        "total_ms": st["total_ms"],
+        "coarse_tasks": st["coarse_task_count"],
+        "first_tokens": toks[:4],
+        "setup_s": round(setup_s, 1),
+    }
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -249,6 +297,17 @@ def main():
     copy_gbs = 2 * copy_bytes / copy_ms / 1e6
     acc.close()
     sweep = context_sweep(llm_accel, workloads, spec, synth) if args.sweep else None
+    full = None
+    if args.full:
+        # seeded embedding table and LM head [151936][2048], shared by both
+        tables = workloads.SyntheticModel(workloads.with_layers(spec, 0))
+        emb, lm_head = tables.embedding(), tables.lm_head()
+        full = {
+            "configs[2]": request_loop(llm_accel, workloads, spec, 2, 16, 8, emb, lm_head),
+            "configs[4]": request_loop(llm_accel, workloads, spec, 36, 1024, 128,
+                                       emb, lm_head),
+        }
+        del emb, lm_head
 
     lb = layer_bytes(spec)
     gu_bytes = gateup_bytes(spec, 1)
@@ -286,6 +345,7 @@ def main():
         "kernel_us_p8": {k: round(v[1], 3) for k, v in kp8.items()},
         "copy_kernel_gbs": copy_gbs,
         "decode_forward_us_by_context": sweep,
+        "request_loops": full,
         "roofline": {
             "kernel": "proj_kernel<1,*,EPI_SILU> (gate|up + SiLU*up, decode row)",
             "bound": "hbm",

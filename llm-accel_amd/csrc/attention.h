@@ -28,7 +28,7 @@ struct AttnArgs {
     int16_t* s_tmax;      // [8][kv_heads][max_tiles][group]
     int32_t* s_tsum;      // [8][kv_heads][max_tiles][group]
     int16_t* s_tval;      // [8][kv_heads][max_tiles][group][head_dim]
-    uint32_t* counters;   // [8][kv_heads], zero between launches
+    uint32_t* counters;   // [8][num_heads], zero between launches
     // split path, per chunk of tiles and query head: whether the running
     // max rises inside the chunk, sum of its tile sums << 2, and per
     // element the sum of its tile PV values << 8 (the whole chunk's effect

@@ -60,7 +60,7 @@ namespace {
 constexpr int MAXG = 16;
 constexpr uint32_t kHeadPathRows = 2;  // rows per block taking the head path
 #ifndef LLM_SPLIT_HEAD_ROWS
-#define LLM_SPLIT_HEAD_ROWS 2
+#define LLM_SPLIT_HEAD_ROWS 8
 #endif
 // rows per block taking the split-head path (head_dim a multiple of 32)
 constexpr uint32_t kSplitHeadRows = LLM_SPLIT_HEAD_ROWS;
@@ -1133,6 +1133,284 @@ __global__ __launch_bounds__(NT) void attention_pv_kernel(AttnArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------
+// Tile path (long contexts, head_dim a multiple of 32): one workgroup of
+// D / 32 wavefronts per (row, query head, tile), in two launches.
+//   (1) attention_tile_scores_kernel: the tile's scores (split-head QK)
+//       and their maximum; the K row of each row's own position is
+//       appended by the workgroup that holds it.
+//   (2) attention_tile_pv_kernel: the running max before and after the
+//       tile (a prefix max of the tile maxima), the tile's probabilities,
+//       their sum and the rounded PV value of every element (split-head
+//       PV); the V append; the last workgroup of a (row, query head) to
+//       arrive runs the per-tile rounding recurrence over all tiles, 64
+//       tiles of operands staged in LDS at a time.
+// Scratch indices as in the chunked path: (row, KV head, tile, head in
+// group).
+// ---------------------------------------------------------------------
+template <int D>
+struct __attribute__((aligned(16))) TileSmem {
+    static constexpr int NWH = D / 32;
+    int16_t q[D], cq[D];                  // rotated query, c(q)
+    int16_t kv[8][D];                     // the block's K (after RoPE) or V rows
+    int16_t p[NWH][TILE], cp[NWH][TILE];  // per wavefront: probabilities, c(p)
+    v4u part[NWH][TILE];                  // QK bank partials (int32)
+    int16_t e14[2056];                    // Q2.14 exp table
+    // recurrence operands of up to 64 tiles: PV values [tile][element],
+    // tile maxima and tile sums
+    int16_t tv[64][D];
+    int32_t tmax[64], tsum[64];
+    uint32_t last;
+};
+
+// The tile's K chunks of this lane's position over the wavefront's
+// elements (cached positions only).
+template <int D>
+__device__ __forceinline__ void tile_load_k(const AttnArgs& a, uint32_t h, uint32_t tile,
+                                            uint32_t w, uint32_t lane, v4u* k) {
+    const uint32_t p = tile * TILE + lane;
+    const int16_t* kp = a.kcache + page_off<D>(a, h, tile) + (size_t)lane * D + 32 * w;
+#pragma unroll
+    for (int c = 0; c < 4; c++) k[c] = p < a.pos0 ? *(const v4u*)(kp + 8 * c) : v4u{0, 0, 0, 0};
+}
+// The tile's V^T chunks of element 32 w + lane % 32 over half lane / 32.
+template <int D>
+__device__ __forceinline__ void tile_load_v(const AttnArgs& a, uint32_t h, uint32_t tile,
+                                            uint32_t w, uint32_t lane, v4u* v) {
+    const uint32_t e = 32 * w + (lane & 31), hh = lane >> 5;
+    const int16_t* vp = a.vcache + page_off<D>(a, h, tile) + (size_t)e * TILE + 32 * hh;
+#pragma unroll
+    for (int c = 0; c < 4; c++)
+        v[c] = tile * TILE + 32 * hh + 8 * c < a.pos0 ? *(const v4u*)(vp + 8 * c)
+                                                     : v4u{0, 0, 0, 0};
+}
+
+template <int D>
+__global__ __launch_bounds__(D * 2) void attention_tile_scores_kernel(AttnArgs a) {
+    static_assert(D % 32 == 0, "tile path: head_dim a multiple of 32");
+    constexpr uint32_t NTH = D * 2;
+    __shared__ TileSmem<D> sm;
+    const uint32_t t = blockIdx.x, g = blockIdx.y, tile = blockIdx.z, tid = threadIdx.x;
+    const uint32_t n = a.pos0 + t + 1, own = n - 1;
+    if (tile * TILE >= n) return;  // beyond this row's context
+    const uint32_t lane = tid & 63, w = tid >> 6;
+    const uint32_t G = a.group, h = g / G, gi = g % G;
+    const int64_t scale = (int64_t)a.qk_scale << 8;
+
+    v4u kc[4];
+    tile_load_k<D>(a, h, tile, w, lane, kc);
+    if (tid < D / 2) {
+        const int16_t* qrow = a.qkv + (size_t)t * a.ldqkv + (size_t)g * D;
+        const int16_t* qrope = a.rope + (size_t)own * D;
+        int32_t y0, y1;
+        rope_pair(qrow[tid], qrow[D / 2 + tid], qrope[tid], qrope[D / 2 + tid], y0, y1);
+        sm.q[paired(tid)] = (int16_t)y0;
+        sm.q[paired(D / 2 + tid)] = (int16_t)y1;
+        sm.cq[paired(tid)] = (int16_t)sat_corr(y0);
+        sm.cq[paired(D / 2 + tid)] = (int16_t)sat_corr(y1);
+    }
+    // the block's K rows that fall in this tile, rotated
+    const uint32_t r0 = tile * TILE > a.pos0 ? tile * TILE - a.pos0 : 0;
+    const uint32_t r1 = own < tile * TILE + TILE - 1 ? own - a.pos0 : tile * TILE + TILE - 1 - a.pos0;
+    if (tile * TILE + TILE > a.pos0) {
+        for (uint32_t i = tid; i < (r1 + 1 - r0) * (D / 2); i += NTH) {
+            const uint32_t r = r0 + i / (D / 2), c = i % (D / 2);
+            const int16_t* krow = a.qkv + (size_t)r * a.ldqkv + (size_t)a.num_heads * D +
+                                  (size_t)h * D;
+            const int16_t* kr = a.rope + (size_t)(a.pos0 + r) * D;
+            int32_t y0, y1;
+            rope_pair(krow[c], krow[D / 2 + c], kr[c], kr[D / 2 + c], y0, y1);
+            sm.kv[r][paired(c)] = (int16_t)y0;
+            sm.kv[r][paired(D / 2 + c)] = (int16_t)y1;
+        }
+    }
+    __syncthreads();
+    const uint32_t p = tile * TILE + lane;
+    const bool valid = p < n;
+    const bool blk = p >= a.pos0 && p <= own;
+    const int16_t* kb = sm.kv[blk ? p - a.pos0 : 0] + 32 * w;
+    v4u kr[4];
+    s16x2 mk = {-32768, -32768};
+#pragma unroll
+    for (int c = 0; c < 4; c++) kr[c] = clamp4m(blk ? *(const v4u*)(kb + 8 * c) : kc[c], mk);
+    const bool kcorr = __any(sat_any(mk));
+    int32_t b0 = 0, b1 = 0, b2 = 0, b3 = 0;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const v4u qv = *(const v4u*)(sm.q + 32 * w + 8 * c);
+        b0 = dot2(kr[c].x, qv.x, b0);
+        b1 = dot2(kr[c].y, qv.y, b1);
+        b2 = dot2(kr[c].z, qv.z, b2);
+        b3 = dot2(kr[c].w, qv.w, b3);
+    }
+    if (kcorr) {
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const v4u cv = *(const v4u*)(sm.cq + 32 * w + 8 * c);
+            b0 = dot2(sat_mask(kr[c].x), cv.x, b0);
+            b1 = dot2(sat_mask(kr[c].y), cv.y, b1);
+            b2 = dot2(sat_mask(kr[c].z), cv.z, b2);
+            b3 = dot2(sat_mask(kr[c].w), cv.w, b3);
+        }
+    }
+    sm.part[w][lane] = v4u{(uint32_t)b0, (uint32_t)b1, (uint32_t)b2, (uint32_t)b3};
+    __syncthreads();
+    if (w == 0) {
+        uint32_t s0 = 0, s1 = 0, s2 = 0, s3 = 0;  // bank sums mod 2^32
+#pragma unroll
+        for (int ww = 0; ww < TileSmem<D>::NWH; ww++) {
+            const v4u pv = sm.part[ww][lane];
+            s0 += pv.x;
+            s1 += pv.y;
+            s2 += pv.z;
+            s3 += pv.w;
+        }
+        // +2^31 (one saturating bank) wraps to INT32_MIN
+        const int64_t t64 = (int64_t)((int32_t)s0 == INT32_MIN ? INT32_MAX : (int32_t)s0) +
+                            ((int32_t)s1 == INT32_MIN ? INT32_MAX : (int32_t)s1) +
+                            ((int32_t)s2 == INT32_MIN ? INT32_MAX : (int32_t)s2) +
+                            ((int32_t)s3 == INT32_MIN ? INT32_MAX : (int32_t)s3);
+        int32_t ts = fx_sat32(t64);
+        ts = fx_sat32(fx_rnd((int64_t)ts * scale, 16));
+        const int32_t s = valid ? fx_sat16(fx_rnd(ts, 8)) : INT16_MIN;
+        const size_t base = (((size_t)t * a.num_kv_heads + h) * a.max_tiles + tile) * G + gi;
+        a.s_scores[base * TILE + lane] = (int16_t)s;
+        const int32_t mx = wave_max(s);
+        if (lane == 0) a.s_tmax[base] = (int16_t)mx;
+    }
+    if (gi == 0 && own / TILE == tile && tid < D / 8)  // this row's K into the cache
+        *(v4u*)(a.kcache + page_off<D>(a, h, tile) + (own % TILE) * D + 8 * tid) =
+            *(const v4u*)(sm.kv[t] + 8 * tid);
+}
+
+template <int D>
+__global__ __launch_bounds__(D * 2) void attention_tile_pv_kernel(AttnArgs a) {
+    static_assert(D % 32 == 0, "tile path: head_dim a multiple of 32");
+    constexpr uint32_t NTH = D * 2;
+    __shared__ TileSmem<D> sm;
+    const uint32_t t = blockIdx.x, g = blockIdx.y, tile = blockIdx.z, tid = threadIdx.x;
+    const uint32_t n = a.pos0 + t + 1, own = n - 1;
+    if (tile * TILE >= n) return;  // beyond this row's context
+    const uint32_t ntiles = (n + TILE - 1) / TILE;
+    const uint32_t lane = tid & 63, w = tid >> 6;
+    const uint32_t G = a.group, h = g / G, gi = g % G;
+    const size_t rh = (size_t)t * a.num_kv_heads + h;
+    const size_t base = (rh * a.max_tiles + tile) * G + gi;
+
+    v4u vc[4];
+    tile_load_v<D>(a, h, tile, w, lane, vc);
+    const int32_t sc = a.s_scores[base * TILE + lane];
+    // maxima of the tiles before this one (this lane's share), and this
+    // tile's
+    int32_t mprev = INT16_MIN;
+    for (uint32_t j = lane; j < tile; j += 64) {
+        const int32_t v = a.s_tmax[(rh * a.max_tiles + j) * G + gi];
+        mprev = v > mprev ? v : mprev;
+    }
+    const int32_t mt = a.s_tmax[base];
+    for (uint32_t c = tid; c < 257; c += NTH)
+        *(v4u*)(sm.e14 + 8 * c) = *(const v4u*)(a.exp14 + 8 * c);
+    // the block's V rows that fall in this tile
+    const uint32_t r0 = tile * TILE > a.pos0 ? tile * TILE - a.pos0 : 0;
+    const uint32_t r1 = own < tile * TILE + TILE - 1 ? own - a.pos0 : tile * TILE + TILE - 1 - a.pos0;
+    if (tile * TILE + TILE > a.pos0) {
+        for (uint32_t i = tid; i < (r1 + 1 - r0) * D; i += NTH) {
+            const uint32_t r = r0 + i / D, e = i % D;
+            sm.kv[r][e] = a.qkv[(size_t)r * a.ldqkv +
+                                (size_t)(a.num_heads + a.num_kv_heads) * D + (size_t)h * D + e];
+        }
+    }
+    __syncthreads();
+    // ---- probabilities under the running max after this tile ----
+    const int32_t m0 = wave_max(mprev);        // running max before the tile
+    const int32_t mn = mt > m0 ? mt : m0;      // and after it
+    const bool valid = tile * TILE + lane < n;
+    const int32_t pr = valid ? prob(sm.e14, sc - mn) : 0;
+    sm.p[w][paired(lane)] = (int16_t)pr;
+    sm.cp[w][paired(lane)] = (int16_t)sat_corr(pr);
+    const int32_t tsum = wave_sum(pr);  // <= 64 * 16384
+    // ---- PV over half hh of the tile for element e ----
+    const uint32_t el = lane & 31, hh = lane >> 5, e = 32 * w + el;
+    v4u vr[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) vr[c] = vc[c];
+    for (uint32_t r = r0; tile * TILE + TILE > a.pos0 && r <= r1; r++) {
+        const uint32_t slot = paired((a.pos0 + r) % TILE);
+        if (slot / 32 != hh) continue;
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+            if ((slot % 32) / 8 == (uint32_t)c) vr[c] = put_half(vr[c], slot % 8, sm.kv[r][e]);
+    }
+    s16x2 mv = {-32768, -32768};
+#pragma unroll
+    for (int c = 0; c < 4; c++) vr[c] = clamp4m(vr[c], mv);
+    const bool vcorr = __any(sat_any(mv));
+    int32_t b0 = 0, b1 = 0, b2 = 0, b3 = 0;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const v4u pv = *(const v4u*)(sm.p[w] + 32 * hh + 8 * c);
+        b0 = dot2(vr[c].x, pv.x, b0);
+        b1 = dot2(vr[c].y, pv.y, b1);
+        b2 = dot2(vr[c].z, pv.z, b2);
+        b3 = dot2(vr[c].w, pv.w, b3);
+    }
+    if (vcorr) {
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const v4u cv = *(const v4u*)(sm.cp[w] + 32 * hh + 8 * c);
+            b0 = dot2(sat_mask(vr[c].x), cv.x, b0);
+            b1 = dot2(sat_mask(vr[c].y), cv.y, b1);
+            b2 = dot2(sat_mask(vr[c].z), cv.z, b2);
+            b3 = dot2(sat_mask(vr[c].w), cv.w, b3);
+        }
+    }
+    b0 += __shfl_xor(b0, 32, 64);
+    b1 += __shfl_xor(b1, 32, 64);
+    b2 += __shfl_xor(b2, 32, 64);
+    b3 += __shfl_xor(b3, 32, 64);
+    int32_t tv = fx_sat32((int64_t)b0 + b1 + b2 + b3);
+    tv = fx_sat32(fx_rnd((int64_t)tv * 1024, 16));
+    tv = fx_sat16(fx_rnd(tv, 8));
+    if (hh == 0) st_coherent(&a.s_tval[base * D + e], (int16_t)tv);
+    if (tid == 0) st_coherent(&a.s_tsum[base], tsum);
+    if (gi == 0 && own / TILE == tile && tid < D)  // this row's V into the cache
+        a.vcache[page_off<D>(a, h, tile) + tid * TILE + paired(own % TILE)] = sm.kv[t][tid];
+    // ---- the last tile of this (row, query head) runs the recurrence ----
+    if (!arrive_last(&a.counters[t * a.num_heads + g], ntiles, &sm.last)) return;
+    int32_t m = INT16_MIN, sum = 0, acc = 0;
+    for (uint32_t j0 = 0; j0 < ntiles; j0 += 64) {
+        const uint32_t nj = ntiles - j0 < 64 ? ntiles - j0 : 64;
+        __syncthreads();  // the previous piece consumed
+        for (uint32_t i = tid; i < nj * D; i += NTH) {
+            const uint32_t j = i / D, ee = i % D;
+            sm.tv[j][ee] = ld_coherent(&a.s_tval[((rh * a.max_tiles + j0 + j) * G + gi) * D + ee]);
+        }
+        for (uint32_t j = tid; j < nj; j += NTH) {
+            const size_t b = (rh * a.max_tiles + j0 + j) * G + gi;
+            sm.tmax[j] = a.s_tmax[b];
+            sm.tsum[j] = ld_coherent(&a.s_tsum[b]);
+        }
+        __syncthreads();
+        if (tid < D) {
+            for (uint32_t j = 0; j < nj; j++) {
+                const int32_t tm = sm.tmax[j];
+                if (tm > m) {  // the running max moves: rescale
+                    const int64_t old = (int64_t)prob(sm.e14, m - tm) << 2;
+                    sum = fx_sat32(fx_rnd((int64_t)sum * old + ((int64_t)sm.tsum[j] << 18), 16));
+                    acc = fx_sat32(fx_rnd((int64_t)acc * old, 16));
+                    m = tm;
+                } else {  // factor exp(0) = 1.0: rnd(v * 2^16, 16) = v
+                    sum = fx_sat32((int64_t)sum + ((int64_t)sm.tsum[j] << 2));
+                }
+                acc = fx_sat32((int64_t)acc + ((int64_t)sm.tv[j][tid] << 8));
+            }
+        }
+    }
+    if (tid < D)
+        a.out[(size_t)t * a.ldo + (size_t)g * D + tid] =
+            fx_sat16(fx_rnd((int64_t)acc * fx_inv_sum(sum), 16));
+}
+
 template <int D>
 static hipError_t launch_d(const AttnArgs& a, uint32_t rows, uint32_t kv_heads,
                            uint32_t chunks, hipStream_t st) {
@@ -1146,6 +1424,15 @@ static hipError_t launch_d(const AttnArgs& a, uint32_t rows, uint32_t kv_heads,
             attention_head_kernel<D><<<dim3(rows, a.num_heads), 64, 0, st>>>(a);
         else
             attention_fused_kernel<D><<<dim3(rows, kv_heads), NT, 0, st>>>(a);
+        return hipGetLastError();
+    }
+    if (D % 32 == 0) {
+        constexpr int DT = D % 32 == 0 ? D : 32;
+        const uint32_t tiles = (a.pos0 + rows + TILE - 1) / TILE;
+        attention_tile_scores_kernel<DT><<<dim3(rows, a.num_heads, tiles), 2 * D, 0, st>>>(a);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        attention_tile_pv_kernel<DT><<<dim3(rows, a.num_heads, tiles), 2 * D, 0, st>>>(a);
         return hipGetLastError();
     }
     attention_scores_kernel<D><<<dim3(rows, kv_heads, chunks), NT, 0, st>>>(a);

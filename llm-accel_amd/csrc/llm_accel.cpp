@@ -16,6 +16,7 @@
 #include <cstring>
 #include <string>
 #include <chrono>
+#include <thread>
 #include <vector>
 
 #include "attention.h"
@@ -217,6 +218,22 @@ int16_t quantize_fix16(double v) {  // host/host_qwen_8x64.cpp:496-505
 }
 
 // Rows [row0, row0 + rows) of matrix m get row-major weights w[rows][k].
+// Runs fn(i) for i in [0, n) on up to 16 host threads (weight repacking).
+template <typename F>
+void parallel_for(uint32_t n, F fn) {
+    const uint32_t T = std::max(1u, std::min({16u, std::thread::hardware_concurrency(), n}));
+    if (T <= 1) {
+        for (uint32_t i = 0; i < n; i++) fn(i);
+        return;
+    }
+    std::vector<std::thread> th;
+    for (uint32_t t = 0; t < T; t++)
+        th.emplace_back([&, t] {
+            for (uint32_t i = t; i < n; i += T) fn(i);
+        });
+    for (auto& x : th) x.join();
+}
+
 int upload_rows(llm_ctx* c, Matrix& m, uint32_t row0, uint32_t rows,
                 const int16_t* w, int which) {
     if (row0 % llm::kBlockRows != 0)
@@ -224,17 +241,21 @@ int upload_rows(llm_ctx* c, Matrix& m, uint32_t row0, uint32_t rows,
     const uint32_t rows_pad = round_up(rows, llm::kBlockRows);
     const uint32_t S = m.steps;
     std::vector<int16_t> buf((size_t)rows_pad * m.k_pad, 0);
-    int maxw = 0;
-    for (uint32_t n = 0; n < rows; n++) {
+    std::vector<int> row_max(rows, 0);
+    parallel_for(rows, [&](uint32_t n) {
         const uint32_t b = n / 4, i = n % 4;
         const int16_t* src = w + (size_t)n * m.k;
+        int mx = 0;
         for (uint32_t k = 0; k < m.k; k++) {
             const uint32_t s = k / 128, j = (k % 128) / 8, e = k % 8;
             const int16_t v = src[k];
             buf[(((size_t)b * S + s) * 4 + i) * 128 + j * 8 + e] = v;
-            maxw = std::max(maxw, std::abs((int)v));
+            mx = std::max(mx, std::abs((int)v));
         }
-    }
+        row_max[n] = mx;
+    });
+    int maxw = 0;
+    for (int v : row_max) maxw = std::max(maxw, v);
     const size_t off = (size_t)(row0 / 4) * S * 512;
     HIP_TRY(hipMemcpy(m.d + off, buf.data(), buf.size() * sizeof(int16_t),
                       hipMemcpyHostToDevice));
@@ -247,11 +268,12 @@ int upload_rows(llm_ctx* c, Matrix& m, uint32_t row0, uint32_t rows,
         const uint32_t KQ = m.kq;
         std::vector<int8_t> rec((size_t)(c1 - c0) * KQ * llm::kMfRecord);
         std::vector<int32_t> sums((size_t)(c1 - c0) * llm::kMfRows * 2, 0);
-        for (uint32_t cc = c0; cc < c1; cc++)
+        parallel_for(c1 - c0, [&](uint32_t ci) {
+            const uint32_t cc = c0 + ci;
             for (uint32_t jj = 0; jj < llm::kMfRows; jj++) {
                 const uint32_t local = cc * llm::kMfRows + jj - row0;
                 const bool valid = local < rows;
-                int32_t* sm = &sums[((size_t)(cc - c0) * llm::kMfRows + jj) * 2];
+                int32_t* sm = &sums[((size_t)ci * llm::kMfRows + jj) * 2];
                 for (uint32_t q = 0; q < KQ; q++)
                     for (uint32_t g = 0; g < 4; g++)
                         for (uint32_t b = 0; b < 16; b++) {
@@ -259,7 +281,7 @@ int upload_rows(llm_ctx* c, Matrix& m, uint32_t row0, uint32_t rows,
                             const int32_t v = valid && k < m.k ? w[(size_t)local * m.k + k] : 0;
                             const int8_t hi = (int8_t)(v >> 8);
                             const int8_t lo = (int8_t)((v & 255) ^ 0x80);
-                            const size_t o = ((size_t)(cc - c0) * KQ + q) * llm::kMfRecord +
+                            const size_t o = ((size_t)ci * KQ + q) * llm::kMfRecord +
                                              (16 * g + jj) * 16 + b;
                             rec[o] = hi;
                             rec[o + 1024] = lo;
@@ -267,6 +289,7 @@ int upload_rows(llm_ctx* c, Matrix& m, uint32_t row0, uint32_t rows,
                             sm[1] += lo;
                         }
             }
+        });
         HIP_TRY(hipMemcpy(m.mf + (size_t)c0 * KQ * llm::kMfRecord, rec.data(),
                           rec.size(), hipMemcpyHostToDevice));
         HIP_TRY(hipMemcpy(m.ms + (size_t)c0 * llm::kMfRows * 2, sums.data(),
@@ -677,7 +700,7 @@ int llm_ctx_create(const llm_shape_t* shape, int device, uint32_t num_pairs,
         (rc = dev_alloc(c, (void**)&c->s_tmax, rht * 2)) ||
         (rc = dev_alloc(c, (void**)&c->s_tsum, rht * 4)) ||
         (rc = dev_alloc(c, (void**)&c->s_tval, rht * d * 2)) ||
-        (rc = dev_alloc(c, (void**)&c->counters, (size_t)8 * c->Hkv * 4)))
+        (rc = dev_alloc(c, (void**)&c->counters, (size_t)8 * c->Hq * 4)))
         return cleanup(rc);
     {
         const size_t rhc = (size_t)8 * c->Hkv * cdiv(c->tiles, c->chunk_tiles) * c->G;
