@@ -64,6 +64,14 @@ constexpr uint32_t kHeadPathRows = 2;  // rows per block taking the head path
 #endif
 // rows per block taking the split-head path (head_dim a multiple of 32)
 constexpr uint32_t kSplitHeadRows = LLM_SPLIT_HEAD_ROWS;
+#ifndef LLM_SPLIT_HEAD_MAX_TILES
+#define LLM_SPLIT_HEAD_MAX_TILES 4
+#endif
+// head_dim a multiple of 32: contexts of up to this many tiles take the
+// split-head path (one launch, tiles in sequence), longer ones the tile
+// path (two launches, tiles in parallel)
+constexpr uint32_t kSplitHeadMaxTiles = LLM_SPLIT_HEAD_MAX_TILES;
+
 constexpr int NT = 512;          // threads per workgroup
 constexpr int NW = NT / 64;      // wavefronts per workgroup
 constexpr int VROW = TILE + 8;   // padded LDS row of the V^T tile (int16)
@@ -724,6 +732,10 @@ __global__ __launch_bounds__(64) void attention_head_kernel(AttnArgs a) {
 // integer mod 2^32 as the sequential chain, so the +2^31 case reads the
 // same.  Cache rows of the next tile are loaded while a tile is computed.
 // ---------------------------------------------------------------------
+// Per-wavefront LDS scratch of the slice transposes: K [64][40], V^T
+// [32][72] (int16; rows padded against bank conflicts).
+constexpr int KSROW = 40, VSROW = 72, SLICE_SCRATCH = 64 * KSROW;
+
 template <int D>
 struct __attribute__((aligned(16))) SplitSmem {
     static constexpr int NWH = D / 32;
@@ -733,27 +745,55 @@ struct __attribute__((aligned(16))) SplitSmem {
     int16_t p[NWH][TILE], cp[NWH][TILE];  // per wavefront: probabilities, c(p)
     v4u part[2][NWH][TILE];               // QK bank partials (int32), by tile parity
     int16_t e14[2056];                    // Q2.14 exp table
+    int16_t scr[NWH][SLICE_SCRATCH];      // per wavefront: slice transposes
 };
 
-// This lane's cache operands of `tile`: the K chunks of its position
-// (cached positions only) over the wavefront's elements, and the V^T
-// chunks of element 32 w + lane % 32 over half lane / 32 of the tile.
+// A wavefront's share of one tile as loaded: four K chunks and four V^T
+// chunks per lane (see slice_load).
 struct SplitRegs {
     v4u k[4], v[4];
 };
+
+// A wavefront's slices of one tile: its 32 head elements of the K rows
+// of all 64 positions, and its 32 V^T rows (all 64 positions), read with
+// coalesced 16-byte loads (the page clamped to one in bounds), loaded
+// unconditionally: a load under a branch makes the compiler wait for every
+// outstanding load where the branch joins, which would stall on the next
+// step's prefetch.  Positions that are not cached are masked where the
+// rows are used.
+//   K: load c, lane l = position 16 c + l / 4, elements 8 (l % 4) ..
+//   V: load c, lane l = V^T row 8 c + l / 8, positions 8 (l % 8) ..
 template <int D>
-__device__ __forceinline__ void split_load(const AttnArgs& a, uint32_t h, uint32_t tile,
+__device__ __forceinline__ void slice_load(const AttnArgs& a, uint32_t h, uint32_t tile,
                                            uint32_t w, uint32_t lane, SplitRegs& R) {
-    const uint32_t p = tile * TILE + lane;
-    const int16_t* kp = a.kcache + page_off<D>(a, h, tile) + (size_t)lane * D + 32 * w;
-    const uint32_t e = 32 * w + (lane & 31), hh = lane >> 5;
-    const int16_t* vp = a.vcache + page_off<D>(a, h, tile) + (size_t)e * TILE + 32 * hh;
+    const uint32_t tp = tile < a.tiles ? tile : a.tiles - 1;
+    const int16_t* kp = a.kcache + page_off<D>(a, h, tp) + 32 * w + 8 * (lane & 3);
+    const int16_t* vp = a.vcache + page_off<D>(a, h, tp) + (size_t)32 * w * TILE + 8 * lane;
 #pragma unroll
     for (int c = 0; c < 4; c++) {
-        R.k[c] = p < a.pos0 ? *(const v4u*)(kp + 8 * c) : v4u{0, 0, 0, 0};
-        R.v[c] = tile * TILE + 32 * hh + 8 * c < a.pos0 ? *(const v4u*)(vp + 8 * c)
-                                                         : v4u{0, 0, 0, 0};
+        R.k[c] = *(const v4u*)(kp + (size_t)(16 * c + (lane >> 2)) * D);
+        R.v[c] = *(const v4u*)(vp + 512 * c);
     }
+}
+// The K row (this wavefront's 32 elements) of position `lane`.  LDS
+// operations of one wavefront complete in order, so no barrier.
+__device__ __forceinline__ void slice_k_rows(int16_t* scr, const SplitRegs& R, uint32_t lane,
+                                             v4u* kr) {
+#pragma unroll
+    for (int c = 0; c < 4; c++)
+        *(v4u*)(scr + (16 * c + (lane >> 2)) * KSROW + 8 * (lane & 3)) = R.k[c];
+#pragma unroll
+    for (int c = 0; c < 4; c++) kr[c] = *(const v4u*)(scr + lane * KSROW + 8 * c);
+}
+// V^T row 32 w + lane % 32 (this wavefront's), positions of half lane / 32.
+__device__ __forceinline__ void slice_v_rows(int16_t* scr, const SplitRegs& R, uint32_t lane,
+                                             v4u* vr) {
+#pragma unroll
+    for (int c = 0; c < 4; c++)
+        *(v4u*)(scr + (8 * c + (lane >> 3)) * VSROW + 8 * (lane & 7)) = R.v[c];
+#pragma unroll
+    for (int c = 0; c < 4; c++)
+        vr[c] = *(const v4u*)(scr + (lane & 31) * VSROW + 32 * (lane >> 5) + 8 * c);
 }
 
 template <int D>
@@ -768,53 +808,95 @@ __global__ __launch_bounds__(D * 2) void attention_split_head_kernel(AttnArgs a)
     const uint32_t ntiles = (n + TILE - 1) / TILE;
     const int64_t scale = (int64_t)a.qk_scale << 8;
 
-    // ---- the first tile's cache rows, the exp table, query and block rows ----
+    // ---- staging loads (indices clamped: every load is issued), then the
+    // first tile's slices, then the staging writes ----
+    constexpr int NE = (257 + NTH - 1) / NTH;          // exp table pieces per thread
+    constexpr int NK = (8 * (D / 2) + NTH - 1) / NTH;  // block K items per thread
+    constexpr int NV = (8 * D + NTH - 1) / NTH;        // block V elements per thread
+    v4u ex[NE];
+#pragma unroll
+    for (int u = 0; u < NE; u++) {
+        const uint32_t c = tid + NTH * u;
+        ex[u] = *(const v4u*)(a.exp14 + 8 * (c < 257 ? c : 256));
+    }
+    const uint32_t qc = tid < D / 2 ? tid : 0;
+    const int16_t* qrow = a.qkv + (size_t)t * a.ldqkv + (size_t)g * D;
+    const int16_t* qrope = a.rope + (size_t)own * D;
+    const int32_t qx0 = qrow[qc], qx1 = qrow[D / 2 + qc], qcs = qrope[qc], qsn = qrope[D / 2 + qc];
+    const uint32_t nk = (t + 1) * (D / 2), nv = (t + 1) * D;
+    int32_t kx[NK][4];
+#pragma unroll
+    for (int u = 0; u < NK; u++) {
+        const uint32_t i = tid + NTH * u < nk ? tid + NTH * u : 0;
+        const uint32_t r = i / (D / 2), c = i % (D / 2);
+        const int16_t* krow = a.qkv + (size_t)r * a.ldqkv + (size_t)a.num_heads * D +
+                              (size_t)h * D;
+        const int16_t* kr = a.rope + (size_t)(a.pos0 + r) * D;
+        kx[u][0] = krow[c];
+        kx[u][1] = krow[D / 2 + c];
+        kx[u][2] = kr[c];
+        kx[u][3] = kr[D / 2 + c];
+    }
+    int16_t vx[NV];
+#pragma unroll
+    for (int u = 0; u < NV; u++) {
+        const uint32_t i = tid + NTH * u < nv ? tid + NTH * u : 0;
+        vx[u] = a.qkv[(size_t)(i / D) * a.ldqkv + (size_t)(a.num_heads + a.num_kv_heads) * D +
+                      (size_t)h * D + i % D];
+    }
     SplitRegs regs;
-    split_load<D>(a, h, 0, w, lane, regs);
-    for (uint32_t c = tid; c < 257; c += NTH)
-        *(v4u*)(sm.e14 + 8 * c) = *(const v4u*)(a.exp14 + 8 * c);
+    slice_load<D>(a, h, 0, w, lane, regs);
+#pragma unroll
+    for (int u = 0; u < NE; u++) {
+        const uint32_t c = tid + NTH * u;
+        if (c < 257) *(v4u*)(sm.e14 + 8 * c) = ex[u];
+    }
     if (tid < D / 2) {
-        const int16_t* qrow = a.qkv + (size_t)t * a.ldqkv + (size_t)g * D;
-        const int16_t* qrope = a.rope + (size_t)own * D;
         int32_t y0, y1;
-        rope_pair(qrow[tid], qrow[D / 2 + tid], qrope[tid], qrope[D / 2 + tid], y0, y1);
+        rope_pair(qx0, qx1, qcs, qsn, y0, y1);
         sm.q[paired(tid)] = (int16_t)y0;
         sm.q[paired(D / 2 + tid)] = (int16_t)y1;
         sm.cq[paired(tid)] = (int16_t)sat_corr(y0);
         sm.cq[paired(D / 2 + tid)] = (int16_t)sat_corr(y1);
     }
-    for (uint32_t i = tid; i < (t + 1) * (D / 2); i += NTH) {
-        const uint32_t r = i / (D / 2), c = i % (D / 2);
-        const int16_t* krow = a.qkv + (size_t)r * a.ldqkv + (size_t)a.num_heads * D +
-                              (size_t)h * D;
-        const int16_t* kr = a.rope + (size_t)(a.pos0 + r) * D;
-        int32_t y0, y1;
-        rope_pair(krow[c], krow[D / 2 + c], kr[c], kr[D / 2 + c], y0, y1);
-        sm.kc[r][paired(c)] = (int16_t)y0;
-        sm.kc[r][paired(D / 2 + c)] = (int16_t)y1;
+#pragma unroll
+    for (int u = 0; u < NK; u++) {
+        const uint32_t i = tid + NTH * u;
+        if (i < nk) {
+            const uint32_t r = i / (D / 2), c = i % (D / 2);
+            int32_t y0, y1;
+            rope_pair(kx[u][0], kx[u][1], kx[u][2], kx[u][3], y0, y1);
+            sm.kc[r][paired(c)] = (int16_t)y0;
+            sm.kc[r][paired(D / 2 + c)] = (int16_t)y1;
+        }
     }
-    for (uint32_t i = tid; i < (t + 1) * D; i += NTH) {
-        const uint32_t r = i / D, e = i % D;
-        sm.vc[r][e] = a.qkv[(size_t)r * a.ldqkv +
-                            (size_t)(a.num_heads + a.num_kv_heads) * D + (size_t)h * D + e];
+#pragma unroll
+    for (int u = 0; u < NV; u++) {
+        const uint32_t i = tid + NTH * u;
+        if (i < nv) sm.vc[i / D][i % D] = vx[u];
     }
-    __syncthreads();
+    lds_barrier();
 
     const uint32_t el = lane & 31, hh = lane >> 5, e = 32 * w + el;
     int32_t m = INT16_MIN, sum = 0, acc = 0;
     for (uint32_t tile = 0; tile < ntiles; tile++) {
         const SplitRegs cur = regs;
-        if (tile + 1 < ntiles) split_load<D>(a, h, tile + 1, w, lane, regs);
+        // the next tile's slices (a repeat of this tile's on the last one)
+        slice_load<D>(a, h, tile + 1 < ntiles ? tile + 1 : tile, w, lane, regs);
         // ---- QK partials over this wavefront's elements ----
         const uint32_t p = tile * TILE + lane;
         const bool valid = p < n;
         const bool blk = p >= a.pos0 && p <= own;  // K row of this block
+        const bool cached = p < a.pos0;
         const int16_t* kb = sm.kc[blk ? p - a.pos0 : 0] + 32 * w;
         v4u kr[4];
+        slice_k_rows(sm.scr[w], cur, lane, kr);
         s16x2 mk = {-32768, -32768};
 #pragma unroll
-        for (int c = 0; c < 4; c++)
-            kr[c] = clamp4m(blk ? *(const v4u*)(kb + 8 * c) : cur.k[c], mk);
+        for (int c = 0; c < 4; c++) {
+            const v4u kv = blk ? *(const v4u*)(kb + 8 * c) : kr[c];
+            kr[c] = clamp4m(blk || cached ? kv : v4u{0, 0, 0, 0}, mk);
+        }
         const bool kcorr = __any(sat_any(mk));
         int32_t b0 = 0, b1 = 0, b2 = 0, b3 = 0;
 #pragma unroll
@@ -836,7 +918,7 @@ __global__ __launch_bounds__(D * 2) void attention_split_head_kernel(AttnArgs a)
             }
         }
         sm.part[tile & 1][w][lane] = v4u{(uint32_t)b0, (uint32_t)b1, (uint32_t)b2, (uint32_t)b3};
-        __syncthreads();  // every wavefront's partials
+        lds_barrier();  // every wavefront's partials
         uint32_t s0 = 0, s1 = 0, s2 = 0, s3 = 0;  // bank sums mod 2^32
 #pragma unroll
         for (int ww = 0; ww < SplitSmem<D>::NWH; ww++) {
@@ -867,8 +949,10 @@ __global__ __launch_bounds__(D * 2) void attention_split_head_kernel(AttnArgs a)
         if (old != 16384) acc = fx_sat32(fx_rnd((int64_t)acc * ((int64_t)old << 2), 16));
         // ---- PV over half hh of the tile for element e ----
         v4u vr[4];
+        slice_v_rows(sm.scr[w], cur, lane, vr);
 #pragma unroll
-        for (int c = 0; c < 4; c++) vr[c] = cur.v[c];
+        for (int c = 0; c < 4; c++)  // chunks holding no cached position: zero
+            vr[c] = tile * TILE + 32 * hh + 8 * c < a.pos0 ? vr[c] : v4u{0, 0, 0, 0};
         // the block's V rows in this tile go to their own slots (slots
         // beyond the context meet probability 0)
         for (uint32_t r = 0; r <= t; r++) {
@@ -924,6 +1008,7 @@ __global__ __launch_bounds__(D * 2) void attention_split_head_kernel(AttnArgs a)
         if (tid < D) a.vcache[page_off<D>(a, h, tile) + tid * TILE + paired(slot)] = sm.vc[t][tid];
     }
 }
+
 // ---------------------------------------------------------------------
 // Split path, phase A: scores and tile maxima for a chunk of tiles; the
 // row's own K is appended by the chunk that holds its position.
@@ -1149,47 +1234,48 @@ __global__ __launch_bounds__(NT) void attention_pv_kernel(AttnArgs a) {
 // group).
 // ---------------------------------------------------------------------
 template <int D>
-struct __attribute__((aligned(16))) TileSmem {
+struct __attribute__((aligned(16))) TileScoresSmem {
     static constexpr int NWH = D / 32;
     int16_t q[D], cq[D];                  // rotated query, c(q)
-    int16_t kv[8][D];                     // the block's K (after RoPE) or V rows
-    int16_t p[NWH][TILE], cp[NWH][TILE];  // per wavefront: probabilities, c(p)
+    int16_t kv[8][D];                     // the block's K rows after RoPE
     v4u part[NWH][TILE];                  // QK bank partials (int32)
+    int16_t scr[NWH][SLICE_SCRATCH];      // per wavefront: slice transposes
+};
+template <int D>
+struct __attribute__((aligned(16))) TilePvSmem {
+    static constexpr int NWH = D / 32;
+    int16_t kv[8][D];                     // the block's V rows
+    int16_t p[NWH][TILE], cp[NWH][TILE];  // per wavefront: probabilities, c(p)
     int16_t e14[2056];                    // Q2.14 exp table
-    // recurrence operands of up to 64 tiles: PV values [tile][element],
-    // tile maxima and tile sums
-    int16_t tv[64][D];
-    int32_t tmax[64], tsum[64];
     uint32_t last;
+    union {
+        int16_t scr[NWH][SLICE_SCRATCH];  // per wavefront: slice transposes
+        struct {                          // then the recurrence operands of up
+            int16_t tv[64][D];            // to 64 tiles: PV values
+            int32_t tmax[64], tsum[64];   // [tile][element], maxima, sums
+        };
+    };
 };
 
-// The tile's K chunks of this lane's position over the wavefront's
-// elements (cached positions only).
-template <int D>
-__device__ __forceinline__ void tile_load_k(const AttnArgs& a, uint32_t h, uint32_t tile,
-                                            uint32_t w, uint32_t lane, v4u* k) {
-    const uint32_t p = tile * TILE + lane;
-    const int16_t* kp = a.kcache + page_off<D>(a, h, tile) + (size_t)lane * D + 32 * w;
-#pragma unroll
-    for (int c = 0; c < 4; c++) k[c] = p < a.pos0 ? *(const v4u*)(kp + 8 * c) : v4u{0, 0, 0, 0};
-}
-// The tile's V^T chunks of element 32 w + lane % 32 over half lane / 32.
-template <int D>
-__device__ __forceinline__ void tile_load_v(const AttnArgs& a, uint32_t h, uint32_t tile,
-                                            uint32_t w, uint32_t lane, v4u* v) {
-    const uint32_t e = 32 * w + (lane & 31), hh = lane >> 5;
-    const int16_t* vp = a.vcache + page_off<D>(a, h, tile) + (size_t)e * TILE + 32 * hh;
-#pragma unroll
-    for (int c = 0; c < 4; c++)
-        v[c] = tile * TILE + 32 * hh + 8 * c < a.pos0 ? *(const v4u*)(vp + 8 * c)
-                                                     : v4u{0, 0, 0, 0};
+// Block rows [r0, r1] of a row's block that fall in `tile` (nrow = 0 when
+// none does); r0 is a row of the block in any case.
+struct TileRows {
+    uint32_t r0, nrow;
+};
+__device__ __forceinline__ TileRows tile_rows(const AttnArgs& a, uint32_t tile, uint32_t own) {
+    TileRows r;
+    const uint32_t lo = tile * TILE, hi = tile * TILE + TILE - 1;
+    r.r0 = lo > a.pos0 ? lo - a.pos0 : 0;
+    r.nrow = hi >= a.pos0 ? (own < hi ? own : hi) - a.pos0 + 1 - r.r0 : 0;
+    return r;
 }
 
 template <int D>
 __global__ __launch_bounds__(D * 2) void attention_tile_scores_kernel(AttnArgs a) {
     static_assert(D % 32 == 0, "tile path: head_dim a multiple of 32");
     constexpr uint32_t NTH = D * 2;
-    __shared__ TileSmem<D> sm;
+    constexpr int NK = (8 * (D / 2) + NTH - 1) / NTH;  // block K items per thread
+    __shared__ TileScoresSmem<D> sm;
     const uint32_t t = blockIdx.x, g = blockIdx.y, tile = blockIdx.z, tid = threadIdx.x;
     const uint32_t n = a.pos0 + t + 1, own = n - 1;
     if (tile * TILE >= n) return;  // beyond this row's context
@@ -1197,42 +1283,62 @@ __global__ __launch_bounds__(D * 2) void attention_tile_scores_kernel(AttnArgs a
     const uint32_t G = a.group, h = g / G, gi = g % G;
     const int64_t scale = (int64_t)a.qk_scale << 8;
 
-    v4u kc[4];
-    tile_load_k<D>(a, h, tile, w, lane, kc);
+    // ---- staging loads (indices clamped: every load is issued), this
+    // tile's slices, then the staging writes ----
+    const uint32_t qc = tid < D / 2 ? tid : 0;
+    const int16_t* qrow = a.qkv + (size_t)t * a.ldqkv + (size_t)g * D;
+    const int16_t* qrope = a.rope + (size_t)own * D;
+    const int32_t qx0 = qrow[qc], qx1 = qrow[D / 2 + qc], qcs = qrope[qc], qsn = qrope[D / 2 + qc];
+    const TileRows tr = tile_rows(a, tile, own);
+    const uint32_t nk = tr.nrow * (D / 2);
+    int32_t kx[NK][4];
+#pragma unroll
+    for (int u = 0; u < NK; u++) {
+        const uint32_t i = tid + NTH * u < nk ? tid + NTH * u : 0;
+        const uint32_t r = tr.r0 + i / (D / 2), c = i % (D / 2);
+        const int16_t* krow = a.qkv + (size_t)r * a.ldqkv + (size_t)a.num_heads * D +
+                              (size_t)h * D;
+        const int16_t* kr = a.rope + (size_t)(a.pos0 + r) * D;
+        kx[u][0] = krow[c];
+        kx[u][1] = krow[D / 2 + c];
+        kx[u][2] = kr[c];
+        kx[u][3] = kr[D / 2 + c];
+    }
+    SplitRegs regs;
+    slice_load<D>(a, h, tile, w, lane, regs);
     if (tid < D / 2) {
-        const int16_t* qrow = a.qkv + (size_t)t * a.ldqkv + (size_t)g * D;
-        const int16_t* qrope = a.rope + (size_t)own * D;
         int32_t y0, y1;
-        rope_pair(qrow[tid], qrow[D / 2 + tid], qrope[tid], qrope[D / 2 + tid], y0, y1);
+        rope_pair(qx0, qx1, qcs, qsn, y0, y1);
         sm.q[paired(tid)] = (int16_t)y0;
         sm.q[paired(D / 2 + tid)] = (int16_t)y1;
         sm.cq[paired(tid)] = (int16_t)sat_corr(y0);
         sm.cq[paired(D / 2 + tid)] = (int16_t)sat_corr(y1);
     }
-    // the block's K rows that fall in this tile, rotated
-    const uint32_t r0 = tile * TILE > a.pos0 ? tile * TILE - a.pos0 : 0;
-    const uint32_t r1 = own < tile * TILE + TILE - 1 ? own - a.pos0 : tile * TILE + TILE - 1 - a.pos0;
-    if (tile * TILE + TILE > a.pos0) {
-        for (uint32_t i = tid; i < (r1 + 1 - r0) * (D / 2); i += NTH) {
-            const uint32_t r = r0 + i / (D / 2), c = i % (D / 2);
-            const int16_t* krow = a.qkv + (size_t)r * a.ldqkv + (size_t)a.num_heads * D +
-                                  (size_t)h * D;
-            const int16_t* kr = a.rope + (size_t)(a.pos0 + r) * D;
+#pragma unroll
+    for (int u = 0; u < NK; u++) {
+        const uint32_t i = tid + NTH * u;
+        if (i < nk) {
+            const uint32_t r = tr.r0 + i / (D / 2), c = i % (D / 2);
             int32_t y0, y1;
-            rope_pair(krow[c], krow[D / 2 + c], kr[c], kr[D / 2 + c], y0, y1);
+            rope_pair(kx[u][0], kx[u][1], kx[u][2], kx[u][3], y0, y1);
             sm.kv[r][paired(c)] = (int16_t)y0;
             sm.kv[r][paired(D / 2 + c)] = (int16_t)y1;
         }
     }
-    __syncthreads();
+    lds_barrier();
     const uint32_t p = tile * TILE + lane;
     const bool valid = p < n;
     const bool blk = p >= a.pos0 && p <= own;
+    const bool cached = p < a.pos0;
     const int16_t* kb = sm.kv[blk ? p - a.pos0 : 0] + 32 * w;
     v4u kr[4];
+    slice_k_rows(sm.scr[w], regs, lane, kr);
     s16x2 mk = {-32768, -32768};
 #pragma unroll
-    for (int c = 0; c < 4; c++) kr[c] = clamp4m(blk ? *(const v4u*)(kb + 8 * c) : kc[c], mk);
+    for (int c = 0; c < 4; c++) {
+        const v4u kv = blk ? *(const v4u*)(kb + 8 * c) : kr[c];
+        kr[c] = clamp4m(blk || cached ? kv : v4u{0, 0, 0, 0}, mk);
+    }
     const bool kcorr = __any(sat_any(mk));
     int32_t b0 = 0, b1 = 0, b2 = 0, b3 = 0;
 #pragma unroll
@@ -1254,11 +1360,11 @@ __global__ __launch_bounds__(D * 2) void attention_tile_scores_kernel(AttnArgs a
         }
     }
     sm.part[w][lane] = v4u{(uint32_t)b0, (uint32_t)b1, (uint32_t)b2, (uint32_t)b3};
-    __syncthreads();
+    lds_barrier();
     if (w == 0) {
         uint32_t s0 = 0, s1 = 0, s2 = 0, s3 = 0;  // bank sums mod 2^32
 #pragma unroll
-        for (int ww = 0; ww < TileSmem<D>::NWH; ww++) {
+        for (int ww = 0; ww < TileScoresSmem<D>::NWH; ww++) {
             const v4u pv = sm.part[ww][lane];
             s0 += pv.x;
             s1 += pv.y;
@@ -1283,11 +1389,24 @@ __global__ __launch_bounds__(D * 2) void attention_tile_scores_kernel(AttnArgs a
             *(const v4u*)(sm.kv[t] + 8 * tid);
 }
 
+// The wavefront's V^T slice of `tile` alone (see slice_load).
+template <int D>
+__device__ __forceinline__ void slice_load_v(const AttnArgs& a, uint32_t h, uint32_t tile,
+                                             uint32_t w, uint32_t lane, SplitRegs& R) {
+    const uint32_t tp = tile < a.tiles ? tile : a.tiles - 1;
+    const int16_t* vp = a.vcache + page_off<D>(a, h, tp) + (size_t)32 * w * TILE + 8 * lane;
+#pragma unroll
+    for (int c = 0; c < 4; c++) R.v[c] = *(const v4u*)(vp + 512 * c);
+}
+
 template <int D>
 __global__ __launch_bounds__(D * 2) void attention_tile_pv_kernel(AttnArgs a) {
     static_assert(D % 32 == 0, "tile path: head_dim a multiple of 32");
     constexpr uint32_t NTH = D * 2;
-    __shared__ TileSmem<D> sm;
+    constexpr int NE = (257 + NTH - 1) / NTH;    // exp table pieces per thread
+    constexpr int NV = (8 * D + NTH - 1) / NTH;  // block V elements per thread
+    constexpr int NM = 4;                        // tile maxima per lane (tiles < 256)
+    __shared__ TilePvSmem<D> sm;
     const uint32_t t = blockIdx.x, g = blockIdx.y, tile = blockIdx.z, tid = threadIdx.x;
     const uint32_t n = a.pos0 + t + 1, own = n - 1;
     if (tile * TILE >= n) return;  // beyond this row's context
@@ -1297,30 +1416,50 @@ __global__ __launch_bounds__(D * 2) void attention_tile_pv_kernel(AttnArgs a) {
     const size_t rh = (size_t)t * a.num_kv_heads + h;
     const size_t base = (rh * a.max_tiles + tile) * G + gi;
 
-    v4u vc[4];
-    tile_load_v<D>(a, h, tile, w, lane, vc);
+    // ---- staging loads (indices clamped: every load is issued), this
+    // tile's V slice, then the staging writes ----
+    v4u ex[NE];
+#pragma unroll
+    for (int u = 0; u < NE; u++) {
+        const uint32_t c = tid + NTH * u;
+        ex[u] = *(const v4u*)(a.exp14 + 8 * (c < 257 ? c : 256));
+    }
+    const TileRows tr = tile_rows(a, tile, own);
+    const uint32_t nv = tr.nrow * D;
+    int16_t vx[NV];
+#pragma unroll
+    for (int u = 0; u < NV; u++) {
+        const uint32_t i = tid + NTH * u < nv ? tid + NTH * u : 0;
+        vx[u] = a.qkv[(size_t)(tr.r0 + i / D) * a.ldqkv +
+                      (size_t)(a.num_heads + a.num_kv_heads) * D + (size_t)h * D + i % D];
+    }
     const int32_t sc = a.s_scores[base * TILE + lane];
-    // maxima of the tiles before this one (this lane's share), and this
-    // tile's
+    const int32_t mt = a.s_tmax[base];
+    // maxima of the tiles before this one (this lane's share)
     int32_t mprev = INT16_MIN;
-    for (uint32_t j = lane; j < tile; j += 64) {
+#pragma unroll
+    for (int u = 0; u < NM; u++) {
+        const uint32_t j = lane + 64 * u;
+        const int32_t v = a.s_tmax[(rh * a.max_tiles + (j < tile ? j : 0)) * G + gi];
+        mprev = j < tile && v > mprev ? v : mprev;
+    }
+    for (uint32_t j = lane + 64 * NM; j < tile; j += 64) {  // contexts beyond 256 tiles
         const int32_t v = a.s_tmax[(rh * a.max_tiles + j) * G + gi];
         mprev = v > mprev ? v : mprev;
     }
-    const int32_t mt = a.s_tmax[base];
-    for (uint32_t c = tid; c < 257; c += NTH)
-        *(v4u*)(sm.e14 + 8 * c) = *(const v4u*)(a.exp14 + 8 * c);
-    // the block's V rows that fall in this tile
-    const uint32_t r0 = tile * TILE > a.pos0 ? tile * TILE - a.pos0 : 0;
-    const uint32_t r1 = own < tile * TILE + TILE - 1 ? own - a.pos0 : tile * TILE + TILE - 1 - a.pos0;
-    if (tile * TILE + TILE > a.pos0) {
-        for (uint32_t i = tid; i < (r1 + 1 - r0) * D; i += NTH) {
-            const uint32_t r = r0 + i / D, e = i % D;
-            sm.kv[r][e] = a.qkv[(size_t)r * a.ldqkv +
-                                (size_t)(a.num_heads + a.num_kv_heads) * D + (size_t)h * D + e];
-        }
+    SplitRegs regs;
+    slice_load_v<D>(a, h, tile, w, lane, regs);
+#pragma unroll
+    for (int u = 0; u < NE; u++) {
+        const uint32_t c = tid + NTH * u;
+        if (c < 257) *(v4u*)(sm.e14 + 8 * c) = ex[u];
     }
-    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < NV; u++) {
+        const uint32_t i = tid + NTH * u;
+        if (i < nv) sm.kv[tr.r0 + i / D][i % D] = vx[u];
+    }
+    lds_barrier();
     // ---- probabilities under the running max after this tile ----
     const int32_t m0 = wave_max(mprev);        // running max before the tile
     const int32_t mn = mt > m0 ? mt : m0;      // and after it
@@ -1332,9 +1471,11 @@ __global__ __launch_bounds__(D * 2) void attention_tile_pv_kernel(AttnArgs a) {
     // ---- PV over half hh of the tile for element e ----
     const uint32_t el = lane & 31, hh = lane >> 5, e = 32 * w + el;
     v4u vr[4];
+    slice_v_rows(sm.scr[w], regs, lane, vr);
 #pragma unroll
-    for (int c = 0; c < 4; c++) vr[c] = vc[c];
-    for (uint32_t r = r0; tile * TILE + TILE > a.pos0 && r <= r1; r++) {
+    for (int c = 0; c < 4; c++)  // chunks holding no cached position: zero
+        vr[c] = tile * TILE + 32 * hh + 8 * c < a.pos0 ? vr[c] : v4u{0, 0, 0, 0};
+    for (uint32_t r = tr.r0; r < tr.r0 + tr.nrow; r++) {
         const uint32_t slot = paired((a.pos0 + r) % TILE);
         if (slot / 32 != hh) continue;
 #pragma unroll
@@ -1377,32 +1518,59 @@ __global__ __launch_bounds__(D * 2) void attention_tile_pv_kernel(AttnArgs a) {
         a.vcache[page_off<D>(a, h, tile) + tid * TILE + paired(own % TILE)] = sm.kv[t][tid];
     // ---- the last tile of this (row, query head) runs the recurrence ----
     if (!arrive_last(&a.counters[t * a.num_heads + g], ntiles, &sm.last)) return;
+    // A tile whose maximum does not raise the running max has factor
+    // exp(0) = 1.0 (rnd(v * 2^16, 16) = v): sum and acc take saturating
+    // 32-bit additions of exact int32 terms.  Steps padded with (maximum
+    // -128, sum 0, value 0) change nothing.
     int32_t m = INT16_MIN, sum = 0, acc = 0;
+    constexpr int PL = 64 * D / NTH;  // PV values per thread per piece
     for (uint32_t j0 = 0; j0 < ntiles; j0 += 64) {
         const uint32_t nj = ntiles - j0 < 64 ? ntiles - j0 : 64;
-        __syncthreads();  // the previous piece consumed
-        for (uint32_t i = tid; i < nj * D; i += NTH) {
-            const uint32_t j = i / D, ee = i % D;
-            sm.tv[j][ee] = ld_coherent(&a.s_tval[((rh * a.max_tiles + j0 + j) * G + gi) * D + ee]);
+        lds_barrier();  // the previous piece consumed
+        int16_t vals[PL];
+#pragma unroll
+        for (int u = 0; u < PL; u++) {  // loads first, all in flight
+            const uint32_t i = tid + NTH * u, j = i / D, ee = i % D;
+            vals[u] = j < nj ? ld_coherent(&a.s_tval[((rh * a.max_tiles + j0 + j) * G + gi) * D + ee])
+                             : (int16_t)0;
         }
-        for (uint32_t j = tid; j < nj; j += NTH) {
-            const size_t b = (rh * a.max_tiles + j0 + j) * G + gi;
-            sm.tmax[j] = a.s_tmax[b];
-            sm.tsum[j] = ld_coherent(&a.s_tsum[b]);
+        int32_t tm = INT16_MIN, tsv = 0;
+        if (tid < nj) {
+            const size_t b = (rh * a.max_tiles + j0 + tid) * G + gi;
+            tm = a.s_tmax[b];
+            tsv = ld_coherent(&a.s_tsum[b]);
         }
-        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < PL; u++) {
+            const uint32_t i = tid + NTH * u;
+            sm.tv[i / D][i % D] = vals[u];
+        }
+        if (tid < 64) {
+            sm.tmax[tid] = tm;
+            sm.tsum[tid] = tsv;
+        }
+        lds_barrier();
         if (tid < D) {
-            for (uint32_t j = 0; j < nj; j++) {
-                const int32_t tm = sm.tmax[j];
-                if (tm > m) {  // the running max moves: rescale
-                    const int64_t old = (int64_t)prob(sm.e14, m - tm) << 2;
-                    sum = fx_sat32(fx_rnd((int64_t)sum * old + ((int64_t)sm.tsum[j] << 18), 16));
-                    acc = fx_sat32(fx_rnd((int64_t)acc * old, 16));
-                    m = tm;
-                } else {  // factor exp(0) = 1.0: rnd(v * 2^16, 16) = v
-                    sum = fx_sat32((int64_t)sum + ((int64_t)sm.tsum[j] << 2));
+            for (uint32_t j = 0; j < nj; j += 8) {
+                int32_t tmv[8], tsk[8], tvv[8];
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    tmv[u] = sm.tmax[j + u];
+                    tsk[u] = sm.tsum[j + u];
+                    tvv[u] = sm.tv[j + u][tid];
                 }
-                acc = fx_sat32((int64_t)acc + ((int64_t)sm.tv[j][tid] << 8));
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    if (tmv[u] > m) {  // the running max moves: rescale
+                        const int64_t old = (int64_t)prob(sm.e14, m - tmv[u]) << 2;
+                        sum = fx_sat32(fx_rnd((int64_t)sum * old + ((int64_t)tsk[u] << 18), 16));
+                        acc = fx_sat32(fx_rnd((int64_t)acc * old, 16));
+                        m = tmv[u];
+                    } else {
+                        sum = __builtin_elementwise_add_sat(sum, tsk[u] << 2);
+                    }
+                    acc = __builtin_elementwise_add_sat(acc, tvv[u] * 256);
+                }
             }
         }
     }
@@ -1414,7 +1582,16 @@ __global__ __launch_bounds__(D * 2) void attention_tile_pv_kernel(AttnArgs a) {
 template <int D>
 static hipError_t launch_d(const AttnArgs& a, uint32_t rows, uint32_t kv_heads,
                            uint32_t chunks, hipStream_t st) {
-    if (chunks <= 1) {
+    const uint32_t tiles = (a.pos0 + rows + TILE - 1) / TILE;
+    if (D % 32 == 0 && tiles > kSplitHeadMaxTiles) {
+        constexpr int DT = D % 32 == 0 ? D : 32;
+        attention_tile_scores_kernel<DT><<<dim3(rows, a.num_heads, tiles), 2 * D, 0, st>>>(a);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        attention_tile_pv_kernel<DT><<<dim3(rows, a.num_heads, tiles), 2 * D, 0, st>>>(a);
+        return hipGetLastError();
+    }
+    if (D % 32 == 0 || chunks <= 1) {
         // a wavefront per (row, query head) for single rows and pairs; a
         // workgroup per (row, KV head) beyond (measured at configs[1])
         if (D % 32 == 0 && rows <= kSplitHeadRows)
@@ -1424,15 +1601,6 @@ static hipError_t launch_d(const AttnArgs& a, uint32_t rows, uint32_t kv_heads,
             attention_head_kernel<D><<<dim3(rows, a.num_heads), 64, 0, st>>>(a);
         else
             attention_fused_kernel<D><<<dim3(rows, kv_heads), NT, 0, st>>>(a);
-        return hipGetLastError();
-    }
-    if (D % 32 == 0) {
-        constexpr int DT = D % 32 == 0 ? D : 32;
-        const uint32_t tiles = (a.pos0 + rows + TILE - 1) / TILE;
-        attention_tile_scores_kernel<DT><<<dim3(rows, a.num_heads, tiles), 2 * D, 0, st>>>(a);
-        hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return e;
-        attention_tile_pv_kernel<DT><<<dim3(rows, a.num_heads, tiles), 2 * D, 0, st>>>(a);
         return hipGetLastError();
     }
     attention_scores_kernel<D><<<dim3(rows, kv_heads, chunks), NT, 0, st>>>(a);

@@ -95,6 +95,15 @@ __device__ __forceinline__ int16_t prob(const int16_t* exp14, int32_t x) {
     return exp14[x + 2048];
 }
 
+// Workgroup barrier that orders LDS only: a __syncthreads() fences every
+// address space and so waits for the workgroup's outstanding global loads
+// (the next tile's prefetch) as well.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Wavefront reductions over DPP row operations; the result is uniform.
 template <int CTRL, int ROWS>
 __device__ __forceinline__ int32_t dpp(int32_t old, int32_t v) {
