@@ -643,11 +643,11 @@ __global__ __launch_bounds__(64) void attention_head_kernel(AttnArgs a) {
         const bool blk = p >= a.pos0 && p <= own;
         const int16_t* kb = sm.kc[blk ? p - a.pos0 : 0];
         v4u kr[D / 8];
-        s16x2 mk = {-32768, -32768};
+        uint32_t mk = 0;
 #pragma unroll
         for (int cc = 0; cc < D / 8; cc++)
-            kr[cc] = clamp4m(blk ? *(const v4u*)(kb + 8 * cc) : rows.k[cc], mk);
-        const bool kcorr = __any(sat_any(mk));
+            kr[cc] = clamp4(blk ? *(const v4u*)(kb + 8 * cc) : rows.k[cc], mk);
+        const bool kcorr = __any(mk != 0);
         // q and c(q) are read inside the loop (hoisted, they would hold
         // 2 D/8 vector registers across it)
         uint32_t qoff = 0;
@@ -684,12 +684,12 @@ __global__ __launch_bounds__(64) void attention_head_kernel(AttnArgs a) {
             }
         }
         v4u vr[EW][TILE / 8];
-        s16x2 mv = {-32768, -32768};
+        uint32_t mv = 0;
 #pragma unroll
         for (int ei = 0; ei < EW; ei++)
 #pragma unroll
-            for (int cc = 0; cc < TILE / 8; cc++) vr[ei][cc] = clamp4m(rows.v[ei][cc], mv);
-        const bool vcorr = __any(sat_any(mv));
+            for (int cc = 0; cc < TILE / 8; cc++) vr[ei][cc] = clamp4(rows.v[ei][cc], mv);
+        const bool vcorr = __any(mv != 0);
 #pragma unroll
         for (int ei = 0; ei < EW; ei++) {
             if (lane + 64 * ei >= D) break;
@@ -891,13 +891,13 @@ __global__ __launch_bounds__(D * 2) void attention_split_head_kernel(AttnArgs a)
         const int16_t* kb = sm.kc[blk ? p - a.pos0 : 0] + 32 * w;
         v4u kr[4];
         slice_k_rows(sm.scr[w], cur, lane, kr);
-        s16x2 mk = {-32768, -32768};
+        uint32_t mk = 0;
 #pragma unroll
         for (int c = 0; c < 4; c++) {
             const v4u kv = blk ? *(const v4u*)(kb + 8 * c) : kr[c];
-            kr[c] = clamp4m(blk || cached ? kv : v4u{0, 0, 0, 0}, mk);
+            kr[c] = clamp4(blk || cached ? kv : v4u{0, 0, 0, 0}, mk);
         }
-        const bool kcorr = __any(sat_any(mk));
+        const bool kcorr = __any(mk != 0);
         int32_t b0 = 0, b1 = 0, b2 = 0, b3 = 0;
 #pragma unroll
         for (int c = 0; c < 4; c++) {
@@ -964,10 +964,10 @@ __global__ __launch_bounds__(D * 2) void attention_split_head_kernel(AttnArgs a)
             for (int c = 0; c < 4; c++)
                 if ((slot % 32) / 8 == (uint32_t)c) vr[c] = put_half(vr[c], slot % 8, sm.vc[r][e]);
         }
-        s16x2 mv = {-32768, -32768};
+        uint32_t mv = 0;
 #pragma unroll
-        for (int c = 0; c < 4; c++) vr[c] = clamp4m(vr[c], mv);
-        const bool vcorr = __any(sat_any(mv));
+        for (int c = 0; c < 4; c++) vr[c] = clamp4(vr[c], mv);
+        const bool vcorr = __any(mv != 0);
         b0 = b1 = b2 = b3 = 0;
 #pragma unroll
         for (int c = 0; c < 4; c++) {
@@ -1333,13 +1333,13 @@ __global__ __launch_bounds__(D * 2) void attention_tile_scores_kernel(AttnArgs a
     const int16_t* kb = sm.kv[blk ? p - a.pos0 : 0] + 32 * w;
     v4u kr[4];
     slice_k_rows(sm.scr[w], regs, lane, kr);
-    s16x2 mk = {-32768, -32768};
+    uint32_t mk = 0;
 #pragma unroll
     for (int c = 0; c < 4; c++) {
         const v4u kv = blk ? *(const v4u*)(kb + 8 * c) : kr[c];
-        kr[c] = clamp4m(blk || cached ? kv : v4u{0, 0, 0, 0}, mk);
+        kr[c] = clamp4(blk || cached ? kv : v4u{0, 0, 0, 0}, mk);
     }
-    const bool kcorr = __any(sat_any(mk));
+    const bool kcorr = __any(mk != 0);
     int32_t b0 = 0, b1 = 0, b2 = 0, b3 = 0;
 #pragma unroll
     for (int c = 0; c < 4; c++) {
@@ -1482,10 +1482,10 @@ __global__ __launch_bounds__(D * 2) void attention_tile_pv_kernel(AttnArgs a) {
         for (int c = 0; c < 4; c++)
             if ((slot % 32) / 8 == (uint32_t)c) vr[c] = put_half(vr[c], slot % 8, sm.kv[r][e]);
     }
-    s16x2 mv = {-32768, -32768};
+    uint32_t mv = 0;
 #pragma unroll
-    for (int c = 0; c < 4; c++) vr[c] = clamp4m(vr[c], mv);
-    const bool vcorr = __any(sat_any(mv));
+    for (int c = 0; c < 4; c++) vr[c] = clamp4(vr[c], mv);
+    const bool vcorr = __any(mv != 0);
     int32_t b0 = 0, b1 = 0, b2 = 0, b3 = 0;
 #pragma unroll
     for (int c = 0; c < 4; c++) {

@@ -60,25 +60,11 @@ __device__ __forceinline__ uint32_t clamp_word(uint32_t w) {
 __device__ __forceinline__ uint32_t sat_mask(uint32_t w) {
     return (w >> 11) & ~(w >> 15) & 0x00010001u;
 }
-// Clamped chunk, with the running packed maximum of clamped values in mx:
-// a value saturates exactly when its clamped value is 2048, so after a
-// row sat_any(mx) tells whether any did (3 VALU operations per word).
-__device__ __forceinline__ v4u clamp4m(v4u v, s16x2& mx) {
-    v4u r;
-    r.x = clamp_word(v.x);
-    r.y = clamp_word(v.y);
-    r.z = clamp_word(v.z);
-    r.w = clamp_word(v.w);
-    const s16x2 a = __builtin_elementwise_max(__builtin_bit_cast(s16x2, r.x),
-                                              __builtin_bit_cast(s16x2, r.y));
-    const s16x2 b = __builtin_elementwise_max(__builtin_bit_cast(s16x2, r.z),
-                                              __builtin_bit_cast(s16x2, r.w));
-    mx = __builtin_elementwise_max(mx, __builtin_elementwise_max(a, b));
-    return r;
-}
-__device__ __forceinline__ bool sat_any(s16x2 mx) {
-    return (mx[0] > mx[1] ? mx[0] : mx[1]) == 2048;
-}
+// Clamped chunk; `any` collects the saturation masks of its words, so
+// that after a row any != 0 tells whether a value saturated.  (A running
+// packed maximum of the clamped words compared with 2048 would be fewer
+// operations, but its reduction has been observed to compile to the
+// maximum of one word per chunk and miss values in the others.)
 __device__ __forceinline__ v4u clamp4(v4u v, uint32_t& any) {
     v4u r;
     r.x = clamp_word(v.x);

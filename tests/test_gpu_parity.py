@@ -253,6 +253,42 @@ def test_split_attention_p8_block_late_position():
     assert first_mismatch(vg, vc[0, 1, :n + 8]) is None
 
 
+@pytest.mark.parametrize("cfg,n,rows", [("B", 1020, 8), ("A", 317, 5), ("B", 256, 1),
+                                         ("B", 255, 2), ("B", 252, 8), ("A", 318, 1),
+                                         ("A", 382, 1), ("B", 319, 1)])
+def test_block_across_tile_boundary_late_context(cfg, n, rows):
+    """A block whose rows straddle a 64-position tile boundary after a
+    preloaded context, and contexts at the boundary between the
+    single-launch (<= 4 tiles) and per-tile attention paths: Task 18
+    output rows and every cache row bit-exact."""
+    import llm_accel
+    spec = workloads.CONFIG_B if cfg == "B" else workloads.CONFIG_A
+    synth = workloads.SyntheticModel(spec, layers=1)
+    max_seq = n + rows + 64
+    om = oracle_from_synthetic(synth, oracle_shape(spec, layers=1, max_seq=max_seq))
+    kc, vc = om.new_kv()
+    with llm_accel.Accelerator(accel_shape(spec, layers=1, max_seq=max_seq)) as a:
+        a.load_model(synth)
+        for h in range(spec.kv_heads):
+            k, v = synth.kv_rows(n, seed_offset=30 + h)
+            kc[0, h, :n], vc[0, h, :n] = k, v
+            a.kv_write(0, h, 0, k, v)
+        x = synth.hidden_rows(rows, seed_offset=31)
+        a.upload(2, x)
+        _say(f"case block across tile boundary cfg={cfg} n={n} rows={rows}")
+        rc, _ = a.task(18, 0, rows, n, 2, 0)
+        assert rc == 0
+        got = a.download(0, rows)
+        kv_got = [a.kv_read(0, h, 0, n + rows) for h in range(spec.kv_heads)]
+    code, want, _ = om.task((kc, vc), 18, 0, x, n)
+    assert code == 0
+    err = first_mismatch(got, want)
+    assert err is None, err
+    for h in range(spec.kv_heads):
+        assert first_mismatch(kv_got[h][0], kc[0, h, :n + rows]) is None
+        assert first_mismatch(kv_got[h][1], vc[0, h, :n + rows]) is None
+
+
 @pytest.mark.parametrize("n", [40, 150, 700])
 def test_saturating_kv_takes_exact_path(n):
     # K/V values beyond +-8.0 saturate in Q4.12; the kernel must switch to
@@ -279,6 +315,41 @@ def test_saturating_kv_takes_exact_path(n):
         got = a.download(0, 2)
     code, want, _ = om.task((kc, vc), 18, 0, x, n)
     assert first_mismatch(got, want) is None
+
+
+@pytest.mark.parametrize("cfg,n", [("B", 40), ("B", 700), ("A", 40), ("A", 700)])
+def test_saturation_only_outside_first_word(cfg, n):
+    """Saturating K / V values (>= 2048, Q4.12 +8.0) only in words 1-3 of
+    every bank-paired 8-element group (elements / positions j with
+    j % 4 != 0), never in word 0: the per-product correction must be
+    detected from any word of a chunk (single-launch and per-tile paths,
+    head_dim 128 and 64)."""
+    import llm_accel
+    spec = workloads.CONFIG_B if cfg == "B" else workloads.CONFIG_A
+    d = spec.head_dim
+    synth = workloads.SyntheticModel(spec, layers=1)
+    om = oracle_from_synthetic(synth, oracle_shape(spec, layers=1, max_seq=n + 8))
+    kc, vc = om.new_kv()
+    rng = np.random.default_rng(4000 + n)
+    elem_hot = (np.arange(d) % 4) != 0
+    pos_hot = (np.arange(n) % 4) != 0
+    with llm_accel.Accelerator(accel_shape(spec, layers=1, max_seq=n + 8)) as a:
+        a.load_model(synth)
+        for h in range(spec.kv_heads):
+            k = rng.integers(-200, 200, (n, d), dtype=np.int16)
+            v = rng.integers(-200, 200, (n, d), dtype=np.int16)
+            k[:, elem_hot] = rng.integers(2048, 4000, (n, int(elem_hot.sum())), dtype=np.int16)
+            v[pos_hot, :] = rng.integers(2048, 4000, (int(pos_hot.sum()), d), dtype=np.int16)
+            kc[0, h, :n], vc[0, h, :n] = k, v
+            a.kv_write(0, h, 0, k, v)
+        x = synth.hidden_rows(2, seed_offset=41)
+        a.upload(2, x)
+        _say(f"case saturation outside word 0 cfg={cfg} n={n}")
+        a.task(18, 0, 2, n, 2, 0)
+        got = a.download(0, 2)
+    code, want, _ = om.task((kc, vc), 18, 0, x, n)
+    err = first_mismatch(got, want)
+    assert err is None, err
 
 
 def test_accumulator_saturation_over_long_context():
