@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "kernels.h"
+
 namespace llm {
 
 struct AttnArgs {
@@ -46,5 +48,40 @@ constexpr uint32_t kMaxChunkTiles = 8;
 // the fused single-workgroup path.
 hipError_t launch_attention(const AttnArgs& a, uint32_t rows, uint32_t kv_heads,
                             uint32_t chunks, hipStream_t st);
+
+// Attention sublayer of decode rows in one launch: workgroups [0, nq) are
+// the QKV projection's 4-row blocks, [nq, nq + na) the attention of (row,
+// query head), the rest the O projection's blocks (with its residual and
+// FFN-norm epilogue).  Each later role issues its weight / cache loads,
+// then waits for the arrivals of the role it reads.
+struct SublayerArgs {
+    ProjArgs qkv, o;
+    AttnArgs at;
+    uint32_t nq, na, no;
+    // Arrival counters (kSyncWords words) grow across launches: QKV block
+    // b adds 1 to line b % kSyncQkvLines, so after launch e (1, 2, ...)
+    // line l holds e times its blocks per launch; every attention
+    // workgroup adds 1 to each of kSyncAttnLines lines, which then hold
+    // attn_base + na.  The host keeps epoch and attn_base (mod 2^32).
+    uint32_t* sync;
+    uint32_t epoch, attn_base;
+    uint32_t* host_abort;  // host-visible word, set when a wait gave up
+    uint32_t wait_limit;   // bound of one wait (100 MHz ticks)
+};
+constexpr uint32_t kSyncStride = 32;  // words between counters (one 128-byte line)
+constexpr uint32_t kSyncQkvLines = 32, kSyncAttnLines = 16;
+constexpr uint32_t kSyncAttn = kSyncQkvLines * kSyncStride;
+// Word of `sync` set when a wait gave up (cleared by the host).
+constexpr uint32_t kSyncAbort = kSyncAttn + kSyncAttnLines * kSyncStride;
+constexpr uint32_t kSyncWords = kSyncAbort + kSyncStride;
+
+// Whether the fused launch serves `rows` rows with this shape: head_dim
+// 64 or 128, the split-head attention path, every wavefront of both
+// projections within 4 k-steps, and the waiting workgroups unable to fill
+// the device on their own (so that the workgroups they wait for can
+// always be dispatched).
+bool sublayer_fused_ok(const SublayerArgs& s, uint32_t rows, int qkv_epi, int L_qkv, int L_o);
+hipError_t launch_attention_sublayer(const SublayerArgs& s, uint32_t rows, int qkv_epi,
+                                     hipStream_t st);
 
 }  // namespace llm

@@ -52,6 +52,7 @@
 #include "attn_common.h"
 #include "coherent.h"
 #include "fixed_point.h"
+#include "proj_common.h"
 
 namespace llm {
 
@@ -796,12 +797,18 @@ __device__ __forceinline__ void slice_v_rows(int16_t* scr, const SplitRegs& R, u
         vr[c] = *(const v4u*)(scr + (lane & 31) * VSROW + 32 * (lane >> 5) + 8 * c);
 }
 
-template <int D>
-__global__ __launch_bounds__(D * 2) void attention_split_head_kernel(AttnArgs a) {
+// Attention of row t, query head g on D / 32 wavefronts (one workgroup).
+// FUSED: the q / k / v rows are written by other workgroups of the same
+// launch; every load that does not depend on them (exp table, RoPE rows,
+// the first tile's cache slices) is issued, then wait() runs, then those
+// rows are read with device-coherent loads, and the output row is written
+// with device-coherent stores.  Returns false when wait() gave up.
+template <int D, bool FUSED, typename Wait>
+__device__ __forceinline__ bool split_head_body(const AttnArgs& a, uint32_t t, uint32_t g,
+                                                SplitSmem<D>& sm, Wait&& wait) {
     static_assert(D % 32 == 0, "split-head path: head_dim a multiple of 32");
     constexpr uint32_t NTH = D * 2;  // D / 32 wavefronts
-    __shared__ SplitSmem<D> sm;
-    const uint32_t t = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
+    const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63, w = tid >> 6;
     const uint32_t h = g / a.group;
     const uint32_t n = a.pos0 + t + 1, own = n - 1;
@@ -822,30 +829,39 @@ __global__ __launch_bounds__(D * 2) void attention_split_head_kernel(AttnArgs a)
     const uint32_t qc = tid < D / 2 ? tid : 0;
     const int16_t* qrow = a.qkv + (size_t)t * a.ldqkv + (size_t)g * D;
     const int16_t* qrope = a.rope + (size_t)own * D;
-    const int32_t qx0 = qrow[qc], qx1 = qrow[D / 2 + qc], qcs = qrope[qc], qsn = qrope[D / 2 + qc];
+    const int32_t qcs = qrope[qc], qsn = qrope[D / 2 + qc];
     const uint32_t nk = (t + 1) * (D / 2), nv = (t + 1) * D;
     int32_t kx[NK][4];
 #pragma unroll
     for (int u = 0; u < NK; u++) {
         const uint32_t i = tid + NTH * u < nk ? tid + NTH * u : 0;
         const uint32_t r = i / (D / 2), c = i % (D / 2);
-        const int16_t* krow = a.qkv + (size_t)r * a.ldqkv + (size_t)a.num_heads * D +
-                              (size_t)h * D;
         const int16_t* kr = a.rope + (size_t)(a.pos0 + r) * D;
-        kx[u][0] = krow[c];
-        kx[u][1] = krow[D / 2 + c];
         kx[u][2] = kr[c];
         kx[u][3] = kr[D / 2 + c];
+    }
+    SplitRegs regs;
+    slice_load<D>(a, h, 0, w, lane, regs);
+    if (FUSED && !wait()) return false;
+    // the block's q / k / v rows
+    auto ld_row = [&](const int16_t* p) -> int32_t { return FUSED ? ld_coherent(p) : *p; };
+    const int32_t qx0 = ld_row(qrow + qc), qx1 = ld_row(qrow + D / 2 + qc);
+#pragma unroll
+    for (int u = 0; u < NK; u++) {
+        const uint32_t i = tid + NTH * u < nk ? tid + NTH * u : 0;
+        const uint32_t r = i / (D / 2), c = i % (D / 2);
+        const int16_t* krow = a.qkv + (size_t)r * a.ldqkv + (size_t)a.num_heads * D +
+                              (size_t)h * D;
+        kx[u][0] = ld_row(krow + c);
+        kx[u][1] = ld_row(krow + D / 2 + c);
     }
     int16_t vx[NV];
 #pragma unroll
     for (int u = 0; u < NV; u++) {
         const uint32_t i = tid + NTH * u < nv ? tid + NTH * u : 0;
-        vx[u] = a.qkv[(size_t)(i / D) * a.ldqkv + (size_t)(a.num_heads + a.num_kv_heads) * D +
-                      (size_t)h * D + i % D];
+        vx[u] = (int16_t)ld_row(a.qkv + (size_t)(i / D) * a.ldqkv +
+                                (size_t)(a.num_heads + a.num_kv_heads) * D + (size_t)h * D + i % D);
     }
-    SplitRegs regs;
-    slice_load<D>(a, h, 0, w, lane, regs);
 #pragma unroll
     for (int u = 0; u < NE; u++) {
         const uint32_t c = tid + NTH * u;
@@ -998,8 +1014,14 @@ __global__ __launch_bounds__(D * 2) void attention_split_head_kernel(AttnArgs a)
         acc = fx_sat32((int64_t)acc + ((int64_t)tv << 8));
     }
     const int64_t inv = fx_inv_sum(sum);
-    if (hh == 0)
-        a.out[(size_t)t * a.ldo + (size_t)g * D + e] = fx_sat16(fx_rnd((int64_t)acc * inv, 16));
+    if (hh == 0) {
+        const int16_t y = fx_sat16(fx_rnd((int64_t)acc * inv, 16));
+        int16_t* po = a.out + (size_t)t * a.ldo + (size_t)g * D + e;
+        if (FUSED)
+            st_coherent(po, y);
+        else
+            *po = y;
+    }
     if (g % a.group == 0) {  // this row's K (rotated, paired) and V into the cache
         const uint32_t tile = own / TILE, slot = own % TILE;
         if (tid < D / 8)
@@ -1007,6 +1029,59 @@ __global__ __launch_bounds__(D * 2) void attention_split_head_kernel(AttnArgs a)
                 *(const v4u*)(sm.kc[t] + 8 * tid);
         if (tid < D) a.vcache[page_off<D>(a, h, tile) + tid * TILE + paired(slot)] = sm.vc[t][tid];
     }
+    return true;
+}
+
+template <int D>
+__global__ __launch_bounds__(D * 2) void attention_split_head_kernel(AttnArgs a) {
+    __shared__ SplitSmem<D> sm;
+    split_head_body<D, false>(a, blockIdx.x, blockIdx.y, sm, [] { return true; });
+}
+
+// ---------------------------------------------------------------------
+// Fused attention sublayer (decode rows, split-head attention): QKV
+// blocks, then attention workgroups, then O blocks, in one launch (see
+// SublayerArgs).  Hand-offs: the QKV and attention outputs are written
+// with device-coherent stores, each producing workgroup then arrives on a
+// counter, and the consumers poll (bounded) after issuing every load that
+// does not depend on them.  Arrivals are spread over counter lines so
+// that no line takes more than a few tens of atomics per launch (one
+// line for all 640 QKV blocks measured several microseconds of
+// serialised atomics).
+// ---------------------------------------------------------------------
+template <int D, int RT, int QEPI>
+__global__ __launch_bounds__(D * 2) void attention_sublayer_kernel(SublayerArgs s) {
+    constexpr int WPB = D / 32, SPW = 4;
+    __shared__ SplitSmem<D> sm;
+    __shared__ int64_t red[WPB * 4 * RT];
+    __shared__ uint32_t flag;
+    uint32_t* const sync = s.sync;
+    const uint32_t idx = blockIdx.x;
+    if (idx < s.nq) {
+        proj_block<RT, QEPI, WPB, SPW, false, true>(s.qkv, idx, red, [] { return true; });
+        arrive(sync + kSyncStride * (idx % kSyncQkvLines));
+        return;
+    }
+    if (idx < s.nq + s.na) {
+        const uint32_t k = idx - s.nq;
+        const uint32_t t = k / s.at.num_heads, g = k % s.at.num_heads;
+        if (!split_head_body<D, true>(s.at, t, g, sm, [&] {
+                const uint32_t per = s.nq / kSyncQkvLines, extra = s.nq % kSyncQkvLines;
+                return wait_counts(
+                    sync, kSyncStride, kSyncQkvLines,
+                    [&](uint32_t l) { return s.epoch * (per + (l < extra ? 1u : 0u)); },
+                    s.wait_limit, sync + kSyncAbort, s.host_abort, &flag);
+            }))
+            return;
+        arrive(sync + kSyncAttn, kSyncAttnLines, kSyncStride);
+        return;
+    }
+    const uint32_t b = idx - s.nq - s.na;
+    proj_block<RT, EPI_RESID, WPB, SPW, true, false>(s.o, b, red, [&] {
+        return wait_counts(
+            sync + kSyncAttn + kSyncStride * (b % kSyncAttnLines), 0, 1,
+            [&](uint32_t) { return s.attn_base + s.na; }, s.wait_limit, sync + kSyncAbort, s.host_abort, &flag);
+    });
 }
 
 // ---------------------------------------------------------------------
@@ -1623,6 +1698,64 @@ hipError_t launch_attention(const AttnArgs& a, uint32_t rows, uint32_t kv_heads,
     case 128: return launch_d<128>(a, rows, kv_heads, chunks, st);
     default: return hipErrorInvalidValue;
     }
+}
+
+
+template <int D, int RT, int QEPI>
+static int sublayer_capacity() {
+    static int cap = -1;
+    if (cap < 0) {
+        int per_cu = 0, cus = 0, dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                &per_cu, attention_sublayer_kernel<D, RT, QEPI>, 2 * D, 0) != hipSuccess)
+            return 0;
+        cap = per_cu * cus;
+    }
+    return cap;
+}
+
+template <int D, int RT>
+static int sublayer_capacity_q(int qkv_epi) {
+    return qkv_epi == EPI_STORE_NORM_IN ? sublayer_capacity<D, RT, EPI_STORE_NORM_IN>()
+                                        : sublayer_capacity<D, RT, EPI_STORE>();
+}
+
+bool sublayer_fused_ok(const SublayerArgs& s, uint32_t rows, int qkv_epi, int L_qkv, int L_o) {
+    const uint32_t D = s.at.head_dim;
+    if ((D != 64 && D != 128) || rows == 0 || rows > 2) return false;
+    if (qkv_epi != EPI_STORE && qkv_epi != EPI_STORE_NORM_IN) return false;
+    const uint32_t tiles = (s.at.pos0 + rows + TILE - 1) / TILE;
+    if (tiles > kSplitHeadMaxTiles || rows > kSplitHeadRows) return false;
+    // int32 sums of up to 4 k-steps per wavefront: widening interval >= 4
+    const uint32_t wpb = D / 32;
+    if (L_qkv < 4 || L_o < 4 || s.qkv.steps > 4 * wpb || s.o.steps > 4 * wpb) return false;
+    if (!s.sync || !s.host_abort) return false;
+    int cap = 0;
+    if (D == 64)
+        cap = rows == 1 ? sublayer_capacity_q<64, 1>(qkv_epi) : sublayer_capacity_q<64, 2>(qkv_epi);
+    else
+        cap = rows == 1 ? sublayer_capacity_q<128, 1>(qkv_epi) : sublayer_capacity_q<128, 2>(qkv_epi);
+    return (int64_t)s.na + s.no < cap;
+}
+
+template <int D, int RT>
+static void launch_sub(const SublayerArgs& s, int qkv_epi, hipStream_t st) {
+    const uint32_t grid = s.nq + s.na + s.no;
+    if (qkv_epi == EPI_STORE_NORM_IN)
+        attention_sublayer_kernel<D, RT, EPI_STORE_NORM_IN><<<grid, 2 * D, 0, st>>>(s);
+    else
+        attention_sublayer_kernel<D, RT, EPI_STORE><<<grid, 2 * D, 0, st>>>(s);
+}
+
+hipError_t launch_attention_sublayer(const SublayerArgs& s, uint32_t rows, int qkv_epi,
+                                     hipStream_t st) {
+    if (s.at.head_dim == 64)
+        rows == 1 ? launch_sub<64, 1>(s, qkv_epi, st) : launch_sub<64, 2>(s, qkv_epi, st);
+    else
+        rows == 1 ? launch_sub<128, 1>(s, qkv_epi, st) : launch_sub<128, 2>(s, qkv_epi, st);
+    return hipGetLastError();
 }
 
 }  // namespace llm

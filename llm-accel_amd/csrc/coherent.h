@@ -43,4 +43,71 @@ __device__ __forceinline__ bool arrive_last(uint32_t* counter, uint32_t expected
     return *lds_flag != 0;
 }
 
+// 16 bytes read with two device-coherent 8-byte loads (p 16-byte aligned).
+__device__ __forceinline__ uint4 ld_coherent16(const int16_t* p) {
+    const uint64_t lo = ld_coherent((const uint64_t*)p);
+    const uint64_t hi = ld_coherent((const uint64_t*)p + 1);
+    return make_uint4((uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi, (uint32_t)(hi >> 32));
+}
+
+// Every thread's coherent stores have completed; then one arrival per
+// workgroup on each of the `copies` counters counter[0], counter[stride], ...
+__device__ __forceinline__ void arrive(uint32_t* counter, uint32_t copies = 1,
+                                       uint32_t stride = 0) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x < copies)
+        __hip_atomic_fetch_add(counter + threadIdx.x * stride, 1u, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Default bound of one wait, in ticks of the 100 MHz constant clock
+// (20 ms): a wait that legitimately ends takes microseconds.
+constexpr uint32_t kWaitLimitTicks = 2000000;
+
+// Waits until counter[l * stride] has reached target(l) for every l < n
+// (n <= 64; counters grow across launches and are compared modulo 2^32),
+// the workgroup held at a barrier while wavefront 0 polls, lane l reading
+// counter l.  Every wait ends: past `limit` ticks, or when another
+// workgroup has given up (*abort != 0), it returns false (uniformly) and
+// the workgroup must leave; the one that gives up sets *abort and
+// *host_abort (host-visible memory read by the library after its next
+// synchronisation).  Progress needs the awaited workgroups to be
+// dispatched: the launcher only uses this in grids whose waiting
+// workgroups alone cannot fill the device.
+template <typename Target>
+__device__ __forceinline__ bool wait_counts(const uint32_t* counter, uint32_t stride, uint32_t n,
+                                            Target&& target, uint32_t limit, uint32_t* abort,
+                                            uint32_t* host_abort, uint32_t* lds_flag) {
+    if (threadIdx.x < 64) {
+        const uint32_t l = threadIdx.x;
+        const bool mine = l < n;
+        const uint32_t want = mine ? target(l) : 0u;
+        const uint32_t* p = counter + (mine ? l : 0u) * stride;
+        uint32_t ok = 1;
+        const uint64_t t0 = wall_clock64();
+        while (true) {
+            const uint32_t v = ld_coherent(p);
+            if (__all(!mine || (int32_t)(v - want) >= 0)) break;
+            if (ld_coherent(abort) != 0) {
+                ok = 0;
+                break;
+            }
+            if (wall_clock64() - t0 > limit) {
+                if (l == 0) {
+                    st_coherent(abort, 1u);
+                    __hip_atomic_store(host_abort, 1u, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_SYSTEM);
+                }
+                ok = 0;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+        if (l == 0) *lds_flag = ok;
+    }
+    __syncthreads();
+    return *lds_flag != 0;
+}
+
 }  // namespace llm

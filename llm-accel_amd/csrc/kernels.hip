@@ -12,6 +12,7 @@
 
 #include "coherent.h"
 #include "fixed_point.h"
+#include "proj_common.h"
 
 // Launch shapes (measured choices; overridable at build time for sweeps).
 #ifndef LLM_PROJ_WPB
@@ -46,34 +47,6 @@
 #endif
 
 namespace llm {
-
-typedef short s16x2 __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ int32_t dot2(uint32_t a, uint32_t b, int32_t c) {
-    // v_dot2_i32_i16, no clamp: exact while |c + a.lo*b.lo + a.hi*b.hi| <
-    // 2^31, which the host guarantees through the widening interval L.
-    return __builtin_amdgcn_sdot2(__builtin_bit_cast(s16x2, a),
-                                  __builtin_bit_cast(s16x2, b), c, false);
-}
-
-__device__ __forceinline__ int64_t dot2_wide(uint32_t a, uint32_t b) {
-    int32_t a0 = (int16_t)(a & 0xffff), a1 = (int16_t)(a >> 16);
-    int32_t b0 = (int16_t)(b & 0xffff), b1 = (int16_t)(b >> 16);
-    return (int64_t)(a0 * b0) + (int64_t)(a1 * b1);
-}
-
-// All-ones when `keep`, else zero, as a per-lane value the compiler cannot
-// turn back into a branch: a wave-uniform select would let it sink the
-// loads that feed the masked value into a conditional block, one memory
-// round trip after another.
-__device__ __forceinline__ uint32_t lane_mask(bool keep) {
-    uint32_t m = keep ? 0xffffffffu : 0u;
-    asm volatile("" : "+v"(m));
-    return m;
-}
-__device__ __forceinline__ uint4 and4(uint4 v, uint32_t m) {
-    return make_uint4(v.x & m, v.y & m, v.z & m, v.w & m);
-}
 
 // ---------------------------------------------------------------------
 // RMSNorm: one workgroup per row.
@@ -120,75 +93,6 @@ __global__ __launch_bounds__(256) void rmsnorm_const_kernel(
 // products, bounded by the host), then widen to int64; the 16 lanes of a
 // row and the 4 wavefronts reduce in int64.
 // ---------------------------------------------------------------------
-// Eight inputs normalised with a constant gain: rnd(x * gain * gamma, 16),
-// zero at columns >= cols.
-// |x * gain * gamma| < 2^15 * 2^13 * 2^15, so the product shifted right by 16
-// fits 32 bits before the saturation.
-__device__ __forceinline__ int32_t norm1(int32_t x, int32_t gg) {
-    const int32_t y = (int32_t)(((int64_t)x * gg + 32768) >> 16);
-    return y < -32768 ? -32768 : (y > 32767 ? 32767 : y);
-}
-// Eight inputs normalised with a constant gain: rnd(x * gain * gamma, 16);
-// columns >= cols have gamma 0 (the caller zeroes g there).
-__device__ __forceinline__ uint4 norm8(uint4 x, uint4 g, int32_t gain) {
-    uint32_t w[4] = {x.x, x.y, x.z, x.w};
-    const uint32_t gw[4] = {g.x, g.y, g.z, g.w};
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int32_t lo = norm1((int16_t)(w[i] & 0xffff), gain * (int16_t)(gw[i] & 0xffff));
-        const int32_t hi = norm1((int16_t)(w[i] >> 16), gain * (int16_t)(gw[i] >> 16));
-        w[i] = (uint32_t)(uint16_t)lo | ((uint32_t)hi << 16);
-    }
-    return make_uint4(w[0], w[1], w[2], w[3]);
-}
-
-// Epilogue operands that do not depend on the sums (residual, norm
-// gammas), fetched when the kernel starts so that the epilogue waits on no
-// memory round trip.
-struct EpiIn {
-    int32_t res, g0, g1;
-};
-template <int EPI>
-__device__ __forceinline__ EpiIn epi_fetch(const ProjArgs& a, uint32_t r, uint32_t n) {
-    EpiIn e{0, 0, 0};
-    if (EPI == EPI_RESID) {
-        e.res = a.res[(size_t)r * a.ldr + n];
-        if (a.norm_out) e.g0 = a.norm_gamma[n];
-        if (a.final_out) e.g1 = a.final_gamma[n];
-    }
-    return e;
-}
-
-// The Q8.8 exp table staged in LDS for the SiLU epilogue (one 16-byte
-// piece per thread; visible after the workgroup's next barrier).
-__device__ __forceinline__ void stage_exp8(const int16_t* exp8, int16_t* e8s) {
-    for (uint32_t c = threadIdx.x; c < 2056 / 8; c += blockDim.x)
-        *(uint4*)(e8s + 8 * c) = *(const uint4*)(exp8 + 8 * c);
-}
-
-// Output (r, n) of a projection from its exact sums (gate and up for
-// EPI_SILU): the reference's narrowing, then the epilogue.
-template <int EPI>
-__device__ __forceinline__ void proj_out(const ProjArgs& a, uint32_t r, uint32_t n,
-                                         int64_t t0, int64_t t1, const EpiIn& ei,
-                                         const int16_t* e8) {
-    int16_t y = fx_narrow_projection(t0);
-    if (EPI == EPI_RESID) {
-        y = fx_sat16((int32_t)y + ei.res);
-        if (a.norm_out)
-            a.norm_out[(size_t)r * a.ldn + n] = fx_sat16(fx_rnd(
-                (int64_t)y * a.norm_gain * ei.g0, 16));
-        if (a.final_out)
-            a.final_out[(size_t)r * a.ldn + n] = fx_sat16(fx_rnd(
-                (int64_t)y * a.norm_gain * ei.g1, 16));
-    } else if (EPI == EPI_SILU) {
-        const int16_t up = fx_narrow_projection(t1);
-        const int16_t sg = fx_silu(y, e8);
-        y = fx_sat16(fx_rnd((int64_t)sg * up, 8));
-    }
-    a.out[(size_t)r * a.ldo + n] = y;
-}
-
 // SPW > 0: every wavefront has at most SPW k-steps and issues all of their
 // loads (weights, activations, gammas) before the first product; loads past
 // its last step repeat that step (in bounds, products of zero).  SPW = 0:
@@ -385,7 +289,6 @@ __global__ __launch_bounds__(64 * WPB) void proj_kernel(ProjArgs a) {
 // reduction over the wavefronts, then the shared epilogue.
 // ---------------------------------------------------------------------
 typedef int32_t v4i __attribute__((ext_vector_type(4)));
-typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 
 // 16 int16 activations (two 16-byte loads) -> high bytes (hi_plane) or
 // biased low bytes, element e in byte e.

@@ -13,6 +13,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <chrono>
@@ -20,6 +21,7 @@
 #include <vector>
 
 #include "attention.h"
+#include "coherent.h"
 #include "fixed_point.h"
 #include "kernels.h"
 
@@ -38,6 +40,14 @@ int fail(int code, const std::string& msg) {
         if (e_ != hipSuccess)                                           \
             return fail(LLM_E_HIP, std::string(#expr) + ": " +          \
                                        hipGetErrorString(e_));          \
+    } while (0)
+
+// Stream synchronisation of a context, then the check that no wait
+// between workgroups of a launch gave up since the last one.
+#define SYNC_TRY(c)                                                     \
+    do {                                                                \
+        HIP_TRY(hipStreamSynchronize((c)->stream));                     \
+        if (int rc_ = check_waits(c)) return rc_;                       \
     } while (0)
 
 uint32_t round_up(uint32_t v, uint32_t m) { return (v + m - 1) / m * m; }
@@ -108,6 +118,16 @@ struct llm_ctx {
     int32_t* s_tsum = nullptr;
     int16_t* s_tval = nullptr;
     uint32_t* counters = nullptr;
+    // fused attention sublayer: arrival counters (zero between launches)
+    // and the host-visible word a kernel sets when one of its waits gave up
+    uint32_t* sync = nullptr;
+    uint32_t* host_abort = nullptr;
+    bool fused = true;                 // LLM_ACCEL_FUSED=0 disables it
+    uint32_t sync_epoch = 0;           // fused launches since the counters were zero
+    uint32_t sync_attn = 0;            // attention arrivals per line, mod 2^32
+    // bound of one wait (100 MHz ticks); LLM_ACCEL_WAIT_LIMIT overrides it
+    // (tests force the time-out path with a tiny value)
+    uint32_t wait_limit = 0;
     // RMSNorm gain: > 0 when it is the same for every row (hidden >= 128:
     // fm_t(hidden) saturates, recip() returns 0, the mean square is 0 and
     // the gain is rsqrt(0)); 0 selects the per-row reduction.
@@ -188,6 +208,19 @@ void harvest_timing(llm_ctx* c) {
         c->ev_pool.push_back(t.b);
     }
     c->pending.clear();
+}
+
+// After a synchronisation: a fused launch whose wait gave up (bounded
+// waits end the kernel instead of hanging) left its counters behind and
+// invalid results; clear both and report it.
+int check_waits(llm_ctx* c) {
+    if (!c->host_abort || __atomic_load_n(c->host_abort, __ATOMIC_ACQUIRE) == 0) return 0;
+    (void)hipMemsetAsync(c->sync, 0, llm::kSyncWords * 4, c->stream);
+    (void)hipStreamSynchronize(c->stream);
+    c->sync_epoch = c->sync_attn = 0;
+    __atomic_store_n(c->host_abort, 0u, __ATOMIC_RELEASE);
+    return fail(LLM_E_HIP, "a wait between workgroups of a fused launch timed out; "
+                           "results since the last synchronisation are invalid");
 }
 
 int dev_alloc(llm_ctx* c, void** p, size_t bytes) {
@@ -420,11 +453,7 @@ int enqueue_attention_sublayer(llm_ctx* c, uint32_t layer, uint32_t R,
         a.in_gain = c->const_gain;
         a.in_cols = c->H;
     }
-    {
-        TimedScope ts(c, LLM_K_QKV);
-        HIP_TRY(llm::launch_proj(a, norm_in ? llm::EPI_STORE_NORM_IN : llm::EPI_STORE,
-                                 mq.L, mq.n_pad / 4, st));
-    }
+    const int qkv_epi = norm_in ? llm::EPI_STORE_NORM_IN : llm::EPI_STORE;
     llm::AttnArgs at{};
     at.qkv = c->qkv;
     at.ldqkv = c->Nqkv;
@@ -458,10 +487,6 @@ int enqueue_attention_sublayer(llm_ctx* c, uint32_t layer, uint32_t R,
     if (c->chunk_tiles == 0 || c->chunk_tiles > llm::kMaxChunkTiles)
         return fail(LLM_E_STATE, "attention chunk must be 1..8 tiles");
     const uint32_t chunks = (uint32_t)cdiv(last_tiles, c->chunk_tiles);
-    {
-        TimedScope ts(c, LLM_K_ATTENTION);
-        HIP_TRY(llm::launch_attention(at, R, c->Hkv, chunks, st));
-    }
     const Matrix& mo = c->mat(layer, M_O);
     llm::ProjArgs o{};
     o.w0 = mo.d;
@@ -481,9 +506,37 @@ int enqueue_attention_sublayer(llm_ctx* c, uint32_t layer, uint32_t R,
         o.norm_gamma = c->norms + (size_t)(2 * layer + 1) * c->H;
         o.norm_gain = c->const_gain;
     }
-    {
-        TimedScope ts(c, LLM_K_OPROJ);
-        HIP_TRY(llm::launch_proj(o, llm::EPI_RESID, mo.L, mo.n_pad / 4, st));
+    llm::SublayerArgs sub{};
+    sub.qkv = a;
+    sub.o = o;
+    sub.at = at;
+    sub.nq = mq.n_pad / 4;
+    sub.na = R * c->Hq;
+    sub.no = mo.n_pad / 4;
+    sub.sync = c->sync;
+    sub.epoch = c->sync_epoch + 1;
+    sub.attn_base = c->sync_attn;
+    sub.host_abort = c->host_abort;
+    sub.wait_limit = c->wait_limit;
+    if (c->fused && !llm::proj_uses_mfma(a, qkv_epi) && !llm::proj_uses_mfma(o, llm::EPI_RESID) &&
+        llm::sublayer_fused_ok(sub, R, qkv_epi, mq.L, mo.L)) {
+        TimedScope ts(c, LLM_K_ATTN_SUBLAYER);
+        HIP_TRY(llm::launch_attention_sublayer(sub, R, qkv_epi, st));
+        c->sync_epoch = sub.epoch;
+        c->sync_attn = sub.attn_base + sub.na;
+    } else {
+        {
+            TimedScope ts(c, LLM_K_QKV);
+            HIP_TRY(llm::launch_proj(a, qkv_epi, mq.L, mq.n_pad / 4, st));
+        }
+        {
+            TimedScope ts(c, LLM_K_ATTENTION);
+            HIP_TRY(llm::launch_attention(at, R, c->Hkv, chunks, st));
+        }
+        {
+            TimedScope ts(c, LLM_K_OPROJ);
+            HIP_TRY(llm::launch_proj(o, llm::EPI_RESID, mo.L, mo.n_pad / 4, st));
+        }
     }
     invalidate_pair(c, out_pair);
     if (c->const_gain > 0) c->ffn_cache = {out_pair, layer};
@@ -700,8 +753,16 @@ int llm_ctx_create(const llm_shape_t* shape, int device, uint32_t num_pairs,
         (rc = dev_alloc(c, (void**)&c->s_tmax, rht * 2)) ||
         (rc = dev_alloc(c, (void**)&c->s_tsum, rht * 4)) ||
         (rc = dev_alloc(c, (void**)&c->s_tval, rht * d * 2)) ||
-        (rc = dev_alloc(c, (void**)&c->counters, (size_t)8 * c->Hq * 4)))
+        (rc = dev_alloc(c, (void**)&c->counters, (size_t)8 * c->Hq * 4)) ||
+        (rc = dev_alloc(c, (void**)&c->sync, (size_t)llm::kSyncWords * 4)))
         return cleanup(rc);
+    if (hipHostMalloc((void**)&c->host_abort, 64, hipHostMallocDefault) != hipSuccess)
+        return cleanup(fail(LLM_E_NOMEM, "hipHostMalloc failed"));
+    *c->host_abort = 0;
+    if (const char* e = std::getenv("LLM_ACCEL_FUSED")) c->fused = std::strcmp(e, "0") != 0;
+    c->wait_limit = llm::kWaitLimitTicks;
+    if (const char* e = std::getenv("LLM_ACCEL_WAIT_LIMIT"))
+        c->wait_limit = (uint32_t)std::strtoul(e, nullptr, 10);
     {
         const size_t rhc = (size_t)8 * c->Hkv * cdiv(c->tiles, c->chunk_tiles) * c->G;
         if ((rc = dev_alloc(c, (void**)&c->c_flag, rhc * 4)) ||
@@ -746,6 +807,7 @@ void llm_ctx_destroy(llm_ctx_t* c) {
         (void)hipEventDestroy(t.b);
     }
     for (void* p : c->allocations) (void)hipFree(p);
+    if (c->host_abort) (void)hipHostFree(c->host_abort);
     if (c->stream) (void)hipStreamDestroy(c->stream);
     delete c;
 }
@@ -841,7 +903,7 @@ int llm_hidden_upload(llm_ctx_t* c, uint32_t pair, const int16_t* rows,
     HIP_TRY(hipMemcpy2DAsync(c->pairs[pair], (size_t)c->Hp * 2, rows,
                              (size_t)c->H * 2, (size_t)c->H * 2, n,
                              hipMemcpyHostToDevice, c->stream));
-    HIP_TRY(hipStreamSynchronize(c->stream));
+    SYNC_TRY(c);
     return 0;
 }
 
@@ -853,7 +915,7 @@ int llm_hidden_download(llm_ctx_t* c, uint32_t pair, int16_t* rows,
     HIP_TRY(hipMemcpy2DAsync(rows, (size_t)c->H * 2, c->pairs[pair],
                              (size_t)c->Hp * 2, (size_t)c->H * 2, n,
                              hipMemcpyDeviceToHost, c->stream));
-    HIP_TRY(hipStreamSynchronize(c->stream));
+    SYNC_TRY(c);
     return 0;
 }
 
@@ -1014,7 +1076,7 @@ int llm_kv_read(llm_ctx_t* c, uint32_t layer, uint32_t h, uint32_t pos0,
     if (!c || layer >= c->L || h >= c->Hkv || pos0 + n > c->max_seq)
         return fail(LLM_E_ARG, "bad KV read arguments");
     HIP_TRY(hipSetDevice(c->device));
-    HIP_TRY(hipStreamSynchronize(c->stream));
+    SYNC_TRY(c);
     return kv_transfer(c, layer, h, pos0, n, k, v, false);
 }
 
@@ -1023,7 +1085,7 @@ int llm_kv_write(llm_ctx_t* c, uint32_t layer, uint32_t h, uint32_t pos0,
     if (!c || layer >= c->L || h >= c->Hkv || pos0 + n > c->max_seq)
         return fail(LLM_E_ARG, "bad KV write arguments");
     HIP_TRY(hipSetDevice(c->device));
-    HIP_TRY(hipStreamSynchronize(c->stream));
+    SYNC_TRY(c);
     return kv_transfer(c, layer, h, pos0, n, const_cast<int16_t*>(k),
                        const_cast<int16_t*>(v), true);
 }
@@ -1034,7 +1096,7 @@ int llm_kv_clear(llm_ctx_t* c) {
     const size_t bytes = (size_t)c->L * c->Hkv * c->tiles * 64 * c->d * 2;
     HIP_TRY(hipMemsetAsync(c->kcache, 0, bytes, c->stream));
     HIP_TRY(hipMemsetAsync(c->vcache, 0, bytes, c->stream));
-    HIP_TRY(hipStreamSynchronize(c->stream));
+    SYNC_TRY(c);
     return 0;
 }
 
@@ -1050,7 +1112,7 @@ void* llm_stream(llm_ctx_t* c) { return c ? (void*)c->stream : nullptr; }
 int llm_sync(llm_ctx_t* c) {
     if (!c) return fail(LLM_E_ARG, "null context");
     HIP_TRY(hipSetDevice(c->device));
-    HIP_TRY(hipStreamSynchronize(c->stream));
+    SYNC_TRY(c);
     return 0;
 }
 
@@ -1281,7 +1343,7 @@ int llm_lm_head_argmax(llm_ctx_t* c, uint32_t pair, uint32_t row0, uint32_t rows
     unsigned long long keys[8];
     HIP_TRY(hipMemcpyAsync(keys, c->lm_keys, rows * sizeof(unsigned long long),
                            hipMemcpyDeviceToHost, c->stream));
-    HIP_TRY(hipStreamSynchronize(c->stream));
+    SYNC_TRY(c);
     for (uint32_t r = 0; r < rows; r++) {
         tokens[r] = key_token(keys[r]);
         if (scores) scores[r] = key_score(keys[r]);

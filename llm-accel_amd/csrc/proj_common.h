@@ -1,0 +1,196 @@
+// proj_common.h -- projection arithmetic shared by the projection kernels
+// and the fused attention-sublayer kernel (internal to the library).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "attn_common.h"
+#include "coherent.h"
+#include "fixed_point.h"
+#include "kernels.h"
+
+namespace llm {
+namespace {
+
+__device__ __forceinline__ int64_t dot2_wide(uint32_t a, uint32_t b) {
+    int32_t a0 = (int16_t)(a & 0xffff), a1 = (int16_t)(a >> 16);
+    int32_t b0 = (int16_t)(b & 0xffff), b1 = (int16_t)(b >> 16);
+    return (int64_t)(a0 * b0) + (int64_t)(a1 * b1);
+}
+
+// All-ones when `keep`, else zero, as a per-lane value the compiler cannot
+// turn back into a branch: a wave-uniform select would let it sink the
+// loads that feed the masked value into a conditional block, one memory
+// round trip after another.
+__device__ __forceinline__ uint32_t lane_mask(bool keep) {
+    uint32_t m = keep ? 0xffffffffu : 0u;
+    asm volatile("" : "+v"(m));
+    return m;
+}
+__device__ __forceinline__ uint4 and4(uint4 v, uint32_t m) {
+    return make_uint4(v.x & m, v.y & m, v.z & m, v.w & m);
+}
+
+// One input normalised with a constant gain: rnd(x * gain * gamma, 16).
+// |x * gain * gamma| < 2^15 * 2^13 * 2^15, so the product shifted right by 16
+// fits 32 bits before the saturation.
+__device__ __forceinline__ int32_t norm1(int32_t x, int32_t gg) {
+    const int32_t y = (int32_t)(((int64_t)x * gg + 32768) >> 16);
+    return y < -32768 ? -32768 : (y > 32767 ? 32767 : y);
+}
+// Eight inputs normalised with a constant gain: rnd(x * gain * gamma, 16);
+// columns >= cols have gamma 0 (the caller zeroes g there).
+__device__ __forceinline__ uint4 norm8(uint4 x, uint4 g, int32_t gain) {
+    uint32_t w[4] = {x.x, x.y, x.z, x.w};
+    const uint32_t gw[4] = {g.x, g.y, g.z, g.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int32_t lo = norm1((int16_t)(w[i] & 0xffff), gain * (int16_t)(gw[i] & 0xffff));
+        const int32_t hi = norm1((int16_t)(w[i] >> 16), gain * (int16_t)(gw[i] >> 16));
+        w[i] = (uint32_t)(uint16_t)lo | ((uint32_t)hi << 16);
+    }
+    return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// Epilogue operands that do not depend on the sums (residual, norm
+// gammas), fetched when the kernel starts so that the epilogue waits on no
+// memory round trip.
+struct EpiIn {
+    int32_t res, g0, g1;
+};
+template <int EPI>
+__device__ __forceinline__ EpiIn epi_fetch(const ProjArgs& a, uint32_t r, uint32_t n) {
+    EpiIn e{0, 0, 0};
+    if (EPI == EPI_RESID) {
+        e.res = a.res[(size_t)r * a.ldr + n];
+        if (a.norm_out) e.g0 = a.norm_gamma[n];
+        if (a.final_out) e.g1 = a.final_gamma[n];
+    }
+    return e;
+}
+
+// The Q8.8 exp table staged in LDS for the SiLU epilogue (one 16-byte
+// piece per thread; visible after the workgroup's next barrier).
+__device__ __forceinline__ void stage_exp8(const int16_t* exp8, int16_t* e8s) {
+    for (uint32_t c = threadIdx.x; c < 2056 / 8; c += blockDim.x)
+        *(uint4*)(e8s + 8 * c) = *(const uint4*)(exp8 + 8 * c);
+}
+
+// Output (r, n) of a projection from its exact sums (gate and up for
+// EPI_SILU): the reference's narrowing, then the epilogue.
+// COH: the output is read by other workgroups of the same launch, so it is
+// written with a device-coherent store.
+template <int EPI, bool COH = false>
+__device__ __forceinline__ void proj_out(const ProjArgs& a, uint32_t r, uint32_t n,
+                                         int64_t t0, int64_t t1, const EpiIn& ei,
+                                         const int16_t* e8) {
+    int16_t y = fx_narrow_projection(t0);
+    if (EPI == EPI_RESID) {
+        y = fx_sat16((int32_t)y + ei.res);
+        if (a.norm_out)
+            a.norm_out[(size_t)r * a.ldn + n] = fx_sat16(fx_rnd(
+                (int64_t)y * a.norm_gain * ei.g0, 16));
+        if (a.final_out)
+            a.final_out[(size_t)r * a.ldn + n] = fx_sat16(fx_rnd(
+                (int64_t)y * a.norm_gain * ei.g1, 16));
+    } else if (EPI == EPI_SILU) {
+        const int16_t up = fx_narrow_projection(t1);
+        const int16_t sg = fx_silu(y, e8);
+        y = fx_sat16(fx_rnd((int64_t)sg * up, 8));
+    }
+    if (COH)
+        st_coherent(&a.out[(size_t)r * a.ldo + n], y);
+    else
+        a.out[(size_t)r * a.ldo + n] = y;
+}
+
+
+// One 4-row block b of a projection inside a fused launch, on WPB
+// wavefronts that each hold at most SPW k-steps (SPW no larger than the
+// widening interval: the int32 sums widen once).  Lane (i, j) owns row i
+// and columns 8j..8j+7 of a step, as in the projection kernel.  The weight
+// loads (and the norm gammas and epilogue operands) are issued first; then
+// wait() runs and only then the activations are loaded -- with
+// device-coherent loads when XCOH, for activations another workgroup of
+// the same launch wrote.  Steps past a wavefront's last repeat its last
+// address and are masked to zero at use, so that no branch separates a
+// load from its use.  red: LDS of WPB * 4 * RT int64.  Returns false when
+// wait() gave up (uniform over the workgroup).
+template <int RT, int EPI, int WPB, int SPW, bool XCOH, bool OCOH, typename Wait>
+__device__ __forceinline__ bool proj_block(const ProjArgs& a, uint32_t b, int64_t* red,
+                                           Wait&& wait) {
+    static_assert(EPI != EPI_SILU, "one matrix per block");
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int i = lane >> 4, j = lane & 15;
+    const int et = threadIdx.x;
+    const uint32_t en = b * 4 + et / RT, er = et % RT;
+    const bool eout = et < 4 * RT && er < a.rows && en < a.n;
+    EpiIn ei{0, 0, 0};
+    if (eout) ei = epi_fetch<EPI>(a, er, en);
+    const uint32_t S = a.steps;
+    const uint32_t s0 = wave * S / WPB, s1 = (wave + 1) * S / WPB;
+    const uint32_t cnt = s1 - s0;  // <= SPW (the launcher's choice)
+    const int16_t* wp = a.w0 + ((size_t)(b * S + s0) * 4 + i) * 128 + j * 8;
+    const int16_t* xp = a.x + (size_t)s0 * 128 + j * 8;
+    uint4 wv[SPW], gv[SPW];
+#pragma unroll
+    for (int u = 0; u < SPW; u++) {
+        const uint32_t du = cnt == 0 ? 0 : ((uint32_t)u < cnt ? u : cnt - 1);
+        wv[u] = *(const uint4*)(wp + (size_t)du * 512);
+        if (EPI == EPI_STORE_NORM_IN)
+            gv[u] = *(const uint4*)(a.in_gamma + (s0 + du) * 128 + j * 8);
+    }
+    if (!wait()) return false;
+    uint4 xv[SPW][RT];
+#pragma unroll
+    for (int u = 0; u < SPW; u++) {
+        const uint32_t du = cnt == 0 ? 0 : ((uint32_t)u < cnt ? u : cnt - 1);
+#pragma unroll
+        for (int r = 0; r < RT; r++) {
+            const int16_t* px = xp + (size_t)r * a.ldx + du * 128;
+            xv[u][r] = XCOH ? ld_coherent16(px) : *(const uint4*)px;
+        }
+    }
+    int32_t part[RT];
+#pragma unroll
+    for (int r = 0; r < RT; r++) part[r] = 0;
+#pragma unroll
+    for (int u = 0; u < SPW; u++) {
+        const uint4 w = and4(wv[u], lane_mask((uint32_t)u < cnt));
+#pragma unroll
+        for (int r = 0; r < RT; r++) {
+            const uint4 x = EPI == EPI_STORE_NORM_IN ? norm8(xv[u][r], gv[u], a.in_gain)
+                                                     : xv[u][r];
+            int32_t p = part[r];
+            p = dot2(w.x, x.x, p);
+            p = dot2(w.y, x.y, p);
+            p = dot2(w.z, x.z, p);
+            p = dot2(w.w, x.w, p);
+            part[r] = p;
+        }
+    }
+    int64_t acc[RT];
+#pragma unroll
+    for (int r = 0; r < RT; r++) {
+        acc[r] = part[r];
+#pragma unroll
+        for (int off = 8; off > 0; off >>= 1) acc[r] += __shfl_xor(acc[r], off, 64);
+    }
+    if (j == 0) {
+#pragma unroll
+        for (int r = 0; r < RT; r++) red[(wave * 4 + i) * RT + r] = acc[r];
+    }
+    lds_barrier();
+    if (eout) {
+        const int ii = et / RT;
+        int64_t tot = 0;
+#pragma unroll
+        for (int w = 0; w < WPB; w++) tot += red[(w * 4 + ii) * RT + er];
+        proj_out<EPI, OCOH>(a, er, en, tot, tot, ei, nullptr);
+    }
+    return true;
+}
+
+}  // namespace
+}  // namespace llm

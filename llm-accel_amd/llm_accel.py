@@ -35,7 +35,8 @@ EXPORTS = (
     "llm_bench_projection", "llm_load_lm_head", "llm_lm_head_argmax",
     "llm_generate",
 )
-KERNELS = ("rmsnorm", "qkv", "rope", "attention", "oproj", "gateup", "down")
+KERNELS = ("rmsnorm", "qkv", "rope", "attention", "oproj", "gateup", "down",
+           "attn_sublayer")
 
 
 class Shape(ctypes.Structure):

@@ -1,0 +1,155 @@
+"""Fused attention sublayer: QKV projection, attention and O projection of
+decode rows in one launch (the reference runs them as steps 0-3 of one
+Task 18, kernel/control_cache_8x64.cpp:5974-6164).  It engages where it
+applies, agrees bit for bit with the separate launches and with the
+oracle, and a wait between its workgroups that gives up is reported at the
+next synchronisation and leaves the context usable."""
+import os
+import sys
+
+import pytest
+
+import workloads
+from helpers import accel_shape, first_mismatch, oracle_from_synthetic, oracle_shape
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def _accel(spec, layers, max_seq, env):
+    """A context created with `env` set (read once, at creation)."""
+    import llm_accel
+    old = {k: os.environ.get(k) for k in env}
+    os.environ.update(env)
+    try:
+        return llm_accel.Accelerator(accel_shape(spec, layers=layers, max_seq=max_seq))
+    finally:
+        for k, v in old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+
+
+def _forward(acc, layers, rows, pos, pair_in=2):
+    """T18 / T19 over every layer; returns the hidden rows after each task."""
+    outs = []
+    pin, pout = pair_in, 0
+    for layer in range(layers):
+        for op in (18, 19):
+            rc, _ = acc.task(op, layer, rows, pos, pin, pout)
+            assert rc == 0
+            outs.append(acc.download(pout, rows))
+            pin, pout = pout, pin
+    return outs
+
+
+def test_fused_sublayer_engages_for_decode_rows():
+    """Decode rows (1 and 2) take the fused launch, an 8-row block does not;
+    every task's rows equal the oracle's."""
+    spec = workloads.CONFIG_B
+    synth = workloads.SyntheticModel(spec, seed=workloads.SEED, layers=1)
+    om = oracle_from_synthetic(synth, oracle_shape(spec, layers=1, max_seq=64))
+    kv = om.new_kv()
+    hidden = synth.hidden_rows(11)
+    acc = _accel(spec, 1, 64, {"LLM_ACCEL_FUSED": "1"})
+    with acc:
+        acc.load_model(synth)
+        for pos, rows in ((0, 8), (8, 1), (9, 2)):
+            _say(f"case B pos={pos} rows={rows}")
+            h = hidden[pos:pos + rows]
+            acc.upload(2, h)
+            acc.kernel_timing(True)
+            rc, _ = acc.task(18, 0, rows, pos, 2, 0)
+            assert rc == 0
+            got = acc.download(0, rows)
+            stats = acc.kernel_stats()
+            acc.kernel_timing(False)
+            code, want, _ = om.task(kv, 18, 0, h, pos)
+            assert code == 0
+            assert first_mismatch(got, want) is None
+            fused = stats["attn_sublayer"][0]
+            assert fused == (1 if rows <= 2 else 0), stats
+            assert stats["attention"][0] == (0 if rows <= 2 else 1), stats
+            rc, _ = acc.task(19, 0, rows, pos, 0, 1)
+            code, want19, _ = om.task(kv, 19, 0, want, pos)
+            assert first_mismatch(acc.download(1, rows), want19) is None
+
+
+@pytest.mark.parametrize("cfg", ["A", "B"])
+def test_fused_equals_separate_launches(cfg):
+    """The same decode sequence through the fused launch and through the
+    three separate launches: hidden rows after every task and the K/V cache
+    agree bit for bit."""
+    spec = workloads.CONFIG_A if cfg == "A" else workloads.CONFIG_B
+    layers = 2
+    synth = workloads.SyntheticModel(spec, seed=workloads.SEED + 7, layers=layers)
+    schedule = [(0, 8), (8, 1), (9, 2), (11, 1), (12, 2)]
+    hidden = synth.hidden_rows(14)
+    results = []
+    for fused in ("1", "0"):
+        acc = _accel(spec, layers, 128, {"LLM_ACCEL_FUSED": fused})
+        with acc:
+            acc.load_model(synth)
+            outs = []
+            for pos, rows in schedule:
+                _say(f"case {cfg} fused={fused} pos={pos} rows={rows}")
+                acc.upload(2, hidden[pos:pos + rows])
+                outs += _forward(acc, layers, rows, pos)
+            kvs = [acc.kv_read(layer, h, 0, 14) for layer in range(layers)
+                   for h in range(spec.kv_heads)]
+            results.append((outs, kvs))
+    (o1, k1), (o0, k0) = results
+    for i, (a, b) in enumerate(zip(o1, o0)):
+        assert first_mismatch(a, b) is None, f"task output {i}"
+    for i, ((ka, va), (kb, vb)) in enumerate(zip(k1, k0)):
+        assert first_mismatch(ka, kb) is None, f"K cache {i}"
+        assert first_mismatch(va, vb) is None, f"V cache {i}"
+
+
+def test_wait_time_out_is_reported_and_cleared():
+    """With a wait bound of 0 ticks every wait of a fused launch gives up
+    (the kernel still ends normally: every wait is bounded).  The next
+    synchronisation reports it, the one after that is clean, and tasks that
+    do not use the fused launch still match the oracle."""
+    import llm_accel
+    spec = workloads.CONFIG_B
+    synth = workloads.SyntheticModel(spec, seed=workloads.SEED, layers=1)
+    om = oracle_from_synthetic(synth, oracle_shape(spec, layers=1, max_seq=64))
+    kv = om.new_kv()
+    hidden = synth.hidden_rows(17)
+    acc = _accel(spec, 1, 64, {"LLM_ACCEL_FUSED": "1", "LLM_ACCEL_WAIT_LIMIT": "0"})
+    with acc:
+        acc.load_model(synth)
+        acc.upload(2, hidden[:8])
+        _say("case B P8 block before the forced time-out")
+        _forward(acc, 1, 8, 0)
+        om.task(kv, 18, 0, hidden[:8], 0)
+        acc.sync()
+        acc.upload(3, hidden[8:9])
+        _say("case B decode row with a 0-tick wait bound")
+        rc, _ = acc.task(18, 0, 1, 8, 3, 0)
+        assert rc == 0
+        with pytest.raises(llm_accel.AccelError, match="timed out"):
+            acc.sync()
+        acc.sync()  # cleared
+        # an 8-row block (separate launches) at a fresh position range
+        _say("case B P8 block after the time-out")
+        h = hidden[9:17]
+        acc.upload(2, h)
+        rc, _ = acc.task(18, 0, 8, 9, 2, 0)
+        got = acc.download(0, 8)
+        # the oracle's cache holds positions 0..7 and, like the aborted
+        # launch's, no position 8 row: give it the GPU's row 8 (whatever
+        # the aborted launch left) so that both attend over the same cache
+        for hh in range(spec.kv_heads):
+            k, v = acc.kv_read(0, hh, 8, 1)
+            kv[0][0, hh, 8] = k[0]
+            kv[1][0, hh, 8] = v[0]
+        code, want, _ = om.task(kv, 18, 0, h, 9)
+        assert code == 0
+        assert first_mismatch(got, want) is None
