@@ -125,32 +125,48 @@ def cpu_baseline(spec, synth, seconds):
     }
 
 
-def context_sweep(llm_accel, workloads, spec, synth):
+def load_copies(acc, synth, copies):
+    """`copies` distinct copies of synth's layer 0 as layers 0..copies-1:
+    copy c permutes the columns of every matrix by c (same bytes per
+    matrix, different addresses and values)."""
+    for c in range(copies):
+        for p in range(7):
+            w = synth.weight(0, p)
+            acc.load_projection(c, p, w if c == 0 else np.roll(w, c, axis=1))
+    acc.load_norms(np.concatenate([np.tile(synth.norms()[:2], (copies, 1)),
+                                   synth.norms()[2:3]]))
+
+
+def context_sweep(llm_accel, workloads, spec, synth, copies=4):
     """one layer, K/V preloaded with seeded Q8.8
     N(0, 0.3) to n positions, one decode forward (T18/T19/T20) at position
-    n; median of 5, the Infinity Cache flushed by a 512 MiB copy before
-    each forward."""
+    n.  The context holds `copies` copies of the layer, each with its own
+    K/V cache, and the forwards rotate over them, so that every forward
+    finds its weights and K/V evicted by the others (4 x (154 MB + K/V) >
+    the 256 MB Infinity Cache) without a flush kernel's dirty lines being
+    written back during it; median of 8 forwards after 4 warm-up ones."""
     nmax = 16384
-    shape = llm_accel.Shape(spec.vocab, spec.hidden, spec.inter, 1, spec.heads,
+    shape = llm_accel.Shape(spec.vocab, spec.hidden, spec.inter, copies, spec.heads,
                             spec.kv_heads, nmax + 64, 1e6)
     out = {}
     with llm_accel.Accelerator(shape, num_pairs=4) as a:
-        a.load_model(synth)
+        load_copies(a, synth, copies)
         for h in range(spec.kv_heads):
             k, v = synth.kv_rows(nmax, seed_offset=20 + h)
-            a.kv_write(0, h, 0, k, v)
+            for c in range(copies):
+                a.kv_write(c, h, 0, k, v)
         a.upload(3, synth.hidden_rows(1))
         for n in (128, 1024, 4096, 16384):
             times = []
-            for rep in range(6):
-                a.bench_copy(512 << 20, 1)
+            for rep in range(12):
+                layer = rep % copies
                 a.record(0)
-                a.task(18, 0, 1, n, 3, 0)
-                a.task(19, 0, 1, n, 0, 1)
+                a.task(18, layer, 1, n, 3, 0)
+                a.task(19, layer, 1, n, 0, 1)
                 a.task(20, 0, 1, n, 1, 0)
                 a.record(1)
                 a.sync()
-                if rep:
+                if rep >= 4:
                     times.append(a.elapsed_ms(0, 1) * 1e3)
             out[str(n)] = round(float(np.median(times)), 2)
     return out
@@ -217,13 +233,7 @@ def main():
     shape = llm_accel.Shape(spec.vocab, spec.hidden, spec.inter, C, spec.heads,
                             spec.kv_heads, 64, 1e6)
     acc = llm_accel.Accelerator(shape, num_pairs=4)
-    # Distinct copies: copy c permutes the columns of every matrix by c.
-    for c in range(C):
-        for p in range(7):
-            w = synth.weight(0, p)
-            acc.load_projection(c, p, w if c == 0 else np.roll(w, c, axis=1))
-    acc.load_norms(np.concatenate([np.tile(synth.norms()[:2], (C, 1)),
-                                   synth.norms()[2:3]]))
+    load_copies(acc, synth, C)
     prompt = synth.hidden_rows(8)
     row = synth.hidden_rows(9)[8:9]
     acc.upload(2, prompt)

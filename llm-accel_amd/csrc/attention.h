@@ -30,7 +30,9 @@ struct AttnArgs {
     int16_t* s_tmax;      // [8][kv_heads][max_tiles][group]
     int32_t* s_tsum;      // [8][kv_heads][max_tiles][group]
     int16_t* s_tval;      // [8][kv_heads][max_tiles][group][head_dim]
-    uint32_t* counters;   // [8][num_heads], zero between launches
+    uint32_t* counters;   // zero between launches: chunked path [8][kv_heads];
+                          // tile path kCounterStride words apart, per (row,
+                          // query head) 1 + tile_groups(max_tiles) of them
     // split path, per chunk of tiles and query head: whether the running
     // max rises inside the chunk, sum of its tile sums << 2, and per
     // element the sum of its tile PV values << 8 (the whole chunk's effect
@@ -40,6 +42,17 @@ struct AttnArgs {
     int32_t* c_tsum;      // [8][kv_heads][max_chunks][group]
     int32_t* c_sum;       // [8][kv_heads][max_chunks][group][head_dim]
 };
+
+// Tile-path arrivals: the tiles of a (row, query head) arrive in groups of
+// kArriveGroup on counters one 128-byte line apart, the last tile of each
+// group on the (row, query head)'s top counter (no line takes more than
+// kArriveGroup atomics: arrivals on one line serialise).
+constexpr uint32_t kArriveGroup = 16, kCounterStride = 32;
+constexpr uint32_t tile_groups(uint32_t tiles) { return (tiles + kArriveGroup - 1) / kArriveGroup; }
+// Words of `counters` for a context of `tiles` tiles per (layer, KV head).
+constexpr size_t counter_words(uint32_t num_heads, uint32_t tiles) {
+    return (size_t)8 * num_heads * (1 + tile_groups(tiles)) * kCounterStride;
+}
 
 // Tiles per split-path workgroup: at most kMaxChunkTiles.
 constexpr uint32_t kMaxChunkTiles = 8;

@@ -1323,7 +1323,7 @@ struct __attribute__((aligned(16))) TilePvSmem {
     int16_t p[NWH][TILE], cp[NWH][TILE];  // per wavefront: probabilities, c(p)
     int16_t e14[2056];                    // Q2.14 exp table
     uint32_t last;
-    union {
+    union __attribute__((aligned(16))) {
         int16_t scr[NWH][SLICE_SCRATCH];  // per wavefront: slice transposes
         struct {                          // then the recurrence operands of up
             int16_t tv[64][D];            // to 64 tiles: PV values
@@ -1587,27 +1587,40 @@ __global__ __launch_bounds__(D * 2) void attention_tile_pv_kernel(AttnArgs a) {
     int32_t tv = fx_sat32((int64_t)b0 + b1 + b2 + b3);
     tv = fx_sat32(fx_rnd((int64_t)tv * 1024, 16));
     tv = fx_sat16(fx_rnd(tv, 8));
-    if (hh == 0) st_coherent(&a.s_tval[base * D + e], (int16_t)tv);
+    {  // elements e..e+3 in one 8-byte store (lane % 4 == 0 of each half-wave)
+        const uint32_t t1 = (uint16_t)__shfl_down(tv, 1, 64), t2 = (uint16_t)__shfl_down(tv, 2, 64),
+                       t3 = (uint16_t)__shfl_down(tv, 3, 64);
+        const uint64_t q4 = (uint64_t)((uint16_t)tv | (t1 << 16)) | ((uint64_t)(t2 | (t3 << 16)) << 32);
+        if (hh == 0 && (lane & 3) == 0) st_coherent((uint64_t*)&a.s_tval[base * D + e], q4);
+    }
     if (tid == 0) st_coherent(&a.s_tsum[base], tsum);
     if (gi == 0 && own / TILE == tile && tid < D)  // this row's V into the cache
         a.vcache[page_off<D>(a, h, tile) + tid * TILE + paired(own % TILE)] = sm.kv[t][tid];
     // ---- the last tile of this (row, query head) runs the recurrence ----
-    if (!arrive_last(&a.counters[t * a.num_heads + g], ntiles, &sm.last)) return;
+    {
+        const uint32_t ng = tile_groups(a.max_tiles), grp = tile / kArriveGroup;
+        uint32_t* top = a.counters + ((size_t)t * a.num_heads + g) * (1 + ng) * kCounterStride;
+        const uint32_t in_grp = ntiles - grp * kArriveGroup < kArriveGroup
+                                    ? ntiles - grp * kArriveGroup : kArriveGroup;
+        if (!arrive_last(top + (1 + grp) * kCounterStride, in_grp, &sm.last)) return;
+        if (!arrive_last(top, tile_groups(ntiles), &sm.last)) return;
+    }
     // A tile whose maximum does not raise the running max has factor
     // exp(0) = 1.0 (rnd(v * 2^16, 16) = v): sum and acc take saturating
     // 32-bit additions of exact int32 terms.  Steps padded with (maximum
     // -128, sum 0, value 0) change nothing.
     int32_t m = INT16_MIN, sum = 0, acc = 0;
-    constexpr int PL = 64 * D / NTH;  // PV values per thread per piece
+    constexpr int PL = 64 * D / 4 / NTH;  // 4-value groups per thread per piece
     for (uint32_t j0 = 0; j0 < ntiles; j0 += 64) {
         const uint32_t nj = ntiles - j0 < 64 ? ntiles - j0 : 64;
         lds_barrier();  // the previous piece consumed
-        int16_t vals[PL];
+        uint64_t vals[PL];
 #pragma unroll
         for (int u = 0; u < PL; u++) {  // loads first, all in flight
-            const uint32_t i = tid + NTH * u, j = i / D, ee = i % D;
-            vals[u] = j < nj ? ld_coherent(&a.s_tval[((rh * a.max_tiles + j0 + j) * G + gi) * D + ee])
-                             : (int16_t)0;
+            const uint32_t i = 4 * (tid + NTH * u), j = i / D, ee = i % D;
+            vals[u] = j < nj ? ld_coherent((const uint64_t*)&a.s_tval[
+                                   ((rh * a.max_tiles + j0 + j) * G + gi) * D + ee])
+                             : 0ull;
         }
         int32_t tm = INT16_MIN, tsv = 0;
         if (tid < nj) {
@@ -1617,8 +1630,8 @@ __global__ __launch_bounds__(D * 2) void attention_tile_pv_kernel(AttnArgs a) {
         }
 #pragma unroll
         for (int u = 0; u < PL; u++) {
-            const uint32_t i = tid + NTH * u;
-            sm.tv[i / D][i % D] = vals[u];
+            const uint32_t i = 4 * (tid + NTH * u);
+            *(uint64_t*)&sm.tv[i / D][i % D] = vals[u];
         }
         if (tid < 64) {
             sm.tmax[tid] = tm;

@@ -118,7 +118,7 @@ struct llm_ctx {
     int32_t* s_tsum = nullptr;
     int16_t* s_tval = nullptr;
     uint32_t* counters = nullptr;
-    // fused attention sublayer: arrival counters (zero between launches)
+    // fused attention sublayer: arrival counters (growing across launches)
     // and the host-visible word a kernel sets when one of its waits gave up
     uint32_t* sync = nullptr;
     uint32_t* host_abort = nullptr;
@@ -753,7 +753,8 @@ int llm_ctx_create(const llm_shape_t* shape, int device, uint32_t num_pairs,
         (rc = dev_alloc(c, (void**)&c->s_tmax, rht * 2)) ||
         (rc = dev_alloc(c, (void**)&c->s_tsum, rht * 4)) ||
         (rc = dev_alloc(c, (void**)&c->s_tval, rht * d * 2)) ||
-        (rc = dev_alloc(c, (void**)&c->counters, (size_t)8 * c->Hq * 4)) ||
+        (rc = dev_alloc(c, (void**)&c->counters,
+                        std::max(llm::counter_words(c->Hq, c->tiles), (size_t)8 * c->Hkv) * 4)) ||
         (rc = dev_alloc(c, (void**)&c->sync, (size_t)llm::kSyncWords * 4)))
         return cleanup(rc);
     if (hipHostMalloc((void**)&c->host_abort, 64, hipHostMallocDefault) != hipSuccess)
