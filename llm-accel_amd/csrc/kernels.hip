@@ -114,8 +114,9 @@ __global__ __launch_bounds__(64 * WPB) void proj_kernel(ProjArgs a) {
     const bool efill = EPI == EPI_RESID && a.final_out && et < 32 && fr >= a.rows && fn < a.n;
     int16_t fill = 0;
     if (efill) fill = a.res[(size_t)fr * a.ldr + fn];
-    __shared__ int16_t e8s[EPI == EPI_SILU ? 2056 : 8];
-    if (EPI == EPI_SILU) stage_exp8(a.exp8, e8s);
+    // SiLU reads its 4 * RT table entries from the (L2-resident) table:
+    // staging the 4 KiB table in LDS per workgroup measured slower
+    const int16_t* e8s = a.exp8;
     const uint32_t S = a.steps;
     const uint32_t s0 = wave * S / WPB, s1 = (wave + 1) * S / WPB;
 

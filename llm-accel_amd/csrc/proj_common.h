@@ -70,13 +70,6 @@ __device__ __forceinline__ EpiIn epi_fetch(const ProjArgs& a, uint32_t r, uint32
     return e;
 }
 
-// The Q8.8 exp table staged in LDS for the SiLU epilogue (one 16-byte
-// piece per thread; visible after the workgroup's next barrier).
-__device__ __forceinline__ void stage_exp8(const int16_t* exp8, int16_t* e8s) {
-    for (uint32_t c = threadIdx.x; c < 2056 / 8; c += blockDim.x)
-        *(uint4*)(e8s + 8 * c) = *(const uint4*)(exp8 + 8 * c);
-}
-
 // Output (r, n) of a projection from its exact sums (gate and up for
 // EPI_SILU): the reference's narrowing, then the epilogue.
 // COH: the output is read by other workgroups of the same launch, so it is
