@@ -182,7 +182,11 @@ def request_loop(llm_accel, workloads, spec, layers, prompt_len, gen, emb, lm_he
     KV cache stay in HBM throughout.  decode tok/s = generated forwards /
     their time, LM head excluded (decode_token_s, host/host_qwen_8x64.cpp
     :9265-9273); times are host clocks around each forward, as the
-    reference reports them."""
+    reference reports them.  The request runs 3 times after a short
+    warm-up one; the figures are those of the run with the median total
+    time (a request occasionally meets a host-side stall of a few ms,
+    which would dominate the 2-layer configs[2])."""
+    runs = 3
     t0 = time.perf_counter()
     s = workloads.with_layers(spec, layers, max_seq=prompt_len + gen)
     synth = workloads.SyntheticModel(s)
@@ -194,9 +198,12 @@ def request_loop(llm_accel, workloads, spec, layers, prompt_len, gen, emb, lm_he
         del synth
         a.load_lm_head(lm_head)
         setup_s = time.perf_counter() - t0
-        # one short warm-up request (kernels, page tables), then the run
+        # one short warm-up request (kernels, page tables), then the runs
         a.generate(emb, prompt[:8], 8, layers, 2)
-        toks, st = a.generate(emb, prompt, 8, layers, gen)
+        results = sorted((a.generate(emb, prompt, 8, layers, gen) for _ in range(runs)),
+                         key=lambda r: r[1]["total_ms"])
+        toks, st = results[runs // 2]
+        assert all(r[0] == toks for r in results), "runs generated different tokens"
     dec_ms = st["generated_forward_ms"] / max(st["generated_forward_passes"], 1)
     blocks = st["prompt_forward_passes"]
     kv_bytes = 4 * spec.kv_heads * spec.head_dim * (prompt_len + gen / 2)
