@@ -90,10 +90,16 @@ constexpr uint32_t kSyncWords = kSyncAbort + kSyncStride;
 
 // Whether the fused launch serves `rows` rows with this shape: head_dim
 // 64 or 128, the split-head attention path, every wavefront of both
-// projections within 4 k-steps, and the waiting workgroups unable to fill
-// the device on their own (so that the workgroups they wait for can
-// always be dispatched).
-bool sublayer_fused_ok(const SublayerArgs& s, uint32_t rows, int qkv_epi, int L_qkv, int L_o);
+// projections within 4 k-steps, and the waiting workgroups fewer than the
+// `capacity` the device holds at once (so that the workgroups they wait
+// for can always be dispatched).
+bool sublayer_fused_ok(const SublayerArgs& s, uint32_t rows, int qkv_epi, int L_qkv, int L_o,
+                       int capacity);
+// QKV workgroups of the fused launch for `blocks` 4-row blocks.
+uint32_t sublayer_qkv_workgroups(uint32_t blocks);
+// Workgroups of the fused launch for (head_dim, rows, QKV epilogue) that
+// the device holds at once (`cus` compute units); 0 when unsupported.
+int sublayer_capacity(uint32_t head_dim, uint32_t rows, int qkv_epi, int cus);
 hipError_t launch_attention_sublayer(const SublayerArgs& s, uint32_t rows, int qkv_epi,
                                      hipStream_t st);
 

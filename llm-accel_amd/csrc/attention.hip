@@ -1049,16 +1049,23 @@ __global__ __launch_bounds__(D * 2) void attention_split_head_kernel(AttnArgs a)
 // line for all 640 QKV blocks measured several microseconds of
 // serialised atomics).
 // ---------------------------------------------------------------------
+#ifndef LLM_SUB_QKV_NB
+#define LLM_SUB_QKV_NB 1
+#endif
+// QKV blocks per workgroup of the fused attention sublayer
+constexpr uint32_t kSubQkvBlocks = LLM_SUB_QKV_NB;
+
 template <int D, int RT, int QEPI>
 __global__ __launch_bounds__(D * 2) void attention_sublayer_kernel(SublayerArgs s) {
     constexpr int WPB = D / 32, SPW = 4;
     __shared__ SplitSmem<D> sm;
-    __shared__ int64_t red[WPB * 4 * RT];
+    __shared__ int64_t red[kSubQkvBlocks * WPB * 4 * RT];
     __shared__ uint32_t flag;
     uint32_t* const sync = s.sync;
     const uint32_t idx = blockIdx.x;
     if (idx < s.nq) {
-        proj_block<RT, QEPI, WPB, SPW, false, true>(s.qkv, idx, red, [] { return true; });
+        proj_block<RT, QEPI, WPB, SPW, false, true, kSubQkvBlocks>(s.qkv, idx, red,
+                                                                  [] { return true; });
         arrive(sync + kSyncStride * (idx % kSyncQkvLines));
         return;
     }
@@ -1715,27 +1722,36 @@ hipError_t launch_attention(const AttnArgs& a, uint32_t rows, uint32_t kv_heads,
 
 
 template <int D, int RT, int QEPI>
-static int sublayer_capacity() {
-    static int cap = -1;
-    if (cap < 0) {
-        int per_cu = 0, cus = 0, dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                &per_cu, attention_sublayer_kernel<D, RT, QEPI>, 2 * D, 0) != hipSuccess)
-            return 0;
-        cap = per_cu * cus;
-    }
-    return cap;
+static int sublayer_capacity_of(int cus) {
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &per_cu, attention_sublayer_kernel<D, RT, QEPI>, 2 * D, 0) != hipSuccess)
+        return 0;
+    return per_cu * cus;
 }
 
 template <int D, int RT>
-static int sublayer_capacity_q(int qkv_epi) {
-    return qkv_epi == EPI_STORE_NORM_IN ? sublayer_capacity<D, RT, EPI_STORE_NORM_IN>()
-                                        : sublayer_capacity<D, RT, EPI_STORE>();
+static int sublayer_capacity_q(int qkv_epi, int cus) {
+    return qkv_epi == EPI_STORE_NORM_IN ? sublayer_capacity_of<D, RT, EPI_STORE_NORM_IN>(cus)
+                                        : sublayer_capacity_of<D, RT, EPI_STORE>(cus);
 }
 
-bool sublayer_fused_ok(const SublayerArgs& s, uint32_t rows, int qkv_epi, int L_qkv, int L_o) {
+int sublayer_capacity(uint32_t head_dim, uint32_t rows, int qkv_epi, int cus) {
+    if (head_dim == 64)
+        return rows == 1 ? sublayer_capacity_q<64, 1>(qkv_epi, cus)
+                         : sublayer_capacity_q<64, 2>(qkv_epi, cus);
+    if (head_dim == 128)
+        return rows == 1 ? sublayer_capacity_q<128, 1>(qkv_epi, cus)
+                         : sublayer_capacity_q<128, 2>(qkv_epi, cus);
+    return 0;
+}
+
+uint32_t sublayer_qkv_workgroups(uint32_t blocks) {
+    return (blocks + kSubQkvBlocks - 1) / kSubQkvBlocks;
+}
+
+bool sublayer_fused_ok(const SublayerArgs& s, uint32_t rows, int qkv_epi, int L_qkv, int L_o,
+                       int capacity) {
     const uint32_t D = s.at.head_dim;
     if ((D != 64 && D != 128) || rows == 0 || rows > 2) return false;
     if (qkv_epi != EPI_STORE && qkv_epi != EPI_STORE_NORM_IN) return false;
@@ -1745,12 +1761,7 @@ bool sublayer_fused_ok(const SublayerArgs& s, uint32_t rows, int qkv_epi, int L_
     const uint32_t wpb = D / 32;
     if (L_qkv < 4 || L_o < 4 || s.qkv.steps > 4 * wpb || s.o.steps > 4 * wpb) return false;
     if (!s.sync || !s.host_abort) return false;
-    int cap = 0;
-    if (D == 64)
-        cap = rows == 1 ? sublayer_capacity_q<64, 1>(qkv_epi) : sublayer_capacity_q<64, 2>(qkv_epi);
-    else
-        cap = rows == 1 ? sublayer_capacity_q<128, 1>(qkv_epi) : sublayer_capacity_q<128, 2>(qkv_epi);
-    return (int64_t)s.na + s.no < cap;
+    return (int64_t)s.na + s.no < capacity;
 }
 
 template <int D, int RT>

@@ -128,6 +128,10 @@ struct llm_ctx {
     // bound of one wait (100 MHz ticks); LLM_ACCEL_WAIT_LIMIT overrides it
     // (tests force the time-out path with a tiny value)
     uint32_t wait_limit = 0;
+    // residency of the fused launch per (rows - 1, QKV epilogue is the
+    // input norm): -1 until first needed
+    int sub_cap[2][2] = {{-1, -1}, {-1, -1}};
+    int cus = 0;
     // RMSNorm gain: > 0 when it is the same for every row (hidden >= 128:
     // fm_t(hidden) saturates, recip() returns 0, the mean square is 0 and
     // the gain is rsqrt(0)); 0 selects the per-row reduction.
@@ -510,7 +514,7 @@ int enqueue_attention_sublayer(llm_ctx* c, uint32_t layer, uint32_t R,
     sub.qkv = a;
     sub.o = o;
     sub.at = at;
-    sub.nq = mq.n_pad / 4;
+    sub.nq = llm::sublayer_qkv_workgroups(mq.n_pad / 4);
     sub.na = R * c->Hq;
     sub.no = mo.n_pad / 4;
     sub.sync = c->sync;
@@ -518,8 +522,14 @@ int enqueue_attention_sublayer(llm_ctx* c, uint32_t layer, uint32_t R,
     sub.attn_base = c->sync_attn;
     sub.host_abort = c->host_abort;
     sub.wait_limit = c->wait_limit;
+    int cap = 0;
+    if (c->fused && R <= 2) {
+        int& cc = c->sub_cap[R - 1][qkv_epi == llm::EPI_STORE_NORM_IN];
+        if (cc < 0) cc = llm::sublayer_capacity(c->d, R, qkv_epi, c->cus);
+        cap = cc;
+    }
     if (c->fused && !llm::proj_uses_mfma(a, qkv_epi) && !llm::proj_uses_mfma(o, llm::EPI_RESID) &&
-        llm::sublayer_fused_ok(sub, R, qkv_epi, mq.L, mo.L)) {
+        llm::sublayer_fused_ok(sub, R, qkv_epi, mq.L, mo.L, cap)) {
         TimedScope ts(c, LLM_K_ATTN_SUBLAYER);
         HIP_TRY(llm::launch_attention_sublayer(sub, R, qkv_epi, st));
         c->sync_epoch = sub.epoch;
@@ -761,6 +771,9 @@ int llm_ctx_create(const llm_shape_t* shape, int device, uint32_t num_pairs,
         return cleanup(fail(LLM_E_NOMEM, "hipHostMalloc failed"));
     *c->host_abort = 0;
     if (const char* e = std::getenv("LLM_ACCEL_FUSED")) c->fused = std::strcmp(e, "0") != 0;
+    if (hipDeviceGetAttribute(&c->cus, hipDeviceAttributeMultiprocessorCount, c->device) !=
+        hipSuccess)
+        return cleanup(fail(LLM_E_HIP, "device attribute query failed"));
     c->wait_limit = llm::kWaitLimitTicks;
     if (const char* e = std::getenv("LLM_ACCEL_WAIT_LIMIT"))
         c->wait_limit = (uint32_t)std::strtoul(e, nullptr, 10);

@@ -99,38 +99,50 @@ __device__ __forceinline__ void proj_out(const ProjArgs& a, uint32_t r, uint32_t
 }
 
 
-// One 4-row block b of a projection inside a fused launch, on WPB
-// wavefronts that each hold at most SPW k-steps (SPW no larger than the
-// widening interval: the int32 sums widen once).  Lane (i, j) owns row i
-// and columns 8j..8j+7 of a step, as in the projection kernel.  The weight
-// loads (and the norm gammas and epilogue operands) are issued first; then
-// wait() runs and only then the activations are loaded -- with
-// device-coherent loads when XCOH, for activations another workgroup of
-// the same launch wrote.  Steps past a wavefront's last repeat its last
-// address and are masked to zero at use, so that no branch separates a
-// load from its use.  red: LDS of WPB * 4 * RT int64.  Returns false when
-// wait() gave up (uniform over the workgroup).
-template <int RT, int EPI, int WPB, int SPW, bool XCOH, bool OCOH, typename Wait>
+// NB consecutive 4-row blocks NB b .. NB b + NB - 1 of a projection inside
+// a fused launch, on WPB wavefronts that each hold at most SPW k-steps of
+// every block (SPW no larger than the widening interval: the int32 sums
+// widen once).  Lane (i, j) owns row i and columns 8j..8j+7 of a step, as
+// in the projection kernel; the blocks share the activation loads.  The
+// weight loads (and the norm gammas and epilogue operands) are issued
+// first; then wait() runs and only then the activations are loaded --
+// with device-coherent loads when XCOH, for activations another workgroup
+// of the same launch wrote.  Steps past a wavefront's last repeat its last
+// address and blocks past the matrix its last block; both are masked at
+// use, so that no branch separates a load from its use.  red: LDS of
+// NB * WPB * 4 * RT int64.  Returns false when wait() gave up (uniform
+// over the workgroup).
+template <int RT, int EPI, int WPB, int SPW, bool XCOH, bool OCOH, int NB = 1, typename Wait>
 __device__ __forceinline__ bool proj_block(const ProjArgs& a, uint32_t b, int64_t* red,
                                            Wait&& wait) {
     static_assert(EPI != EPI_SILU, "one matrix per block");
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int i = lane >> 4, j = lane & 15;
     const int et = threadIdx.x;
-    const uint32_t en = b * 4 + et / RT, er = et % RT;
-    const bool eout = et < 4 * RT && er < a.rows && en < a.n;
+    const uint32_t nblocks = (a.n + 3) / 4;
+    // epilogue thread et < 4 RT NB: block et / (4 RT), output row et % RT
+    const uint32_t eb = NB * b + et / (4 * RT), en = eb * 4 + (et % (4 * RT)) / RT, er = et % RT;
+    const bool eout = et < 4 * RT * NB && er < a.rows && en < a.n;
     EpiIn ei{0, 0, 0};
     if (eout) ei = epi_fetch<EPI>(a, er, en);
     const uint32_t S = a.steps;
     const uint32_t s0 = wave * S / WPB, s1 = (wave + 1) * S / WPB;
     const uint32_t cnt = s1 - s0;  // <= SPW (the launcher's choice)
-    const int16_t* wp = a.w0 + ((size_t)(b * S + s0) * 4 + i) * 128 + j * 8;
     const int16_t* xp = a.x + (size_t)s0 * 128 + j * 8;
-    uint4 wv[SPW], gv[SPW];
+    uint4 wv[NB][SPW], gv[SPW];
+#pragma unroll
+    for (int nb = 0; nb < NB; nb++) {
+        const uint32_t bb = NB * b + nb < nblocks ? NB * b + nb : nblocks - 1;
+        const int16_t* wp = a.w0 + ((size_t)(bb * S + s0) * 4 + i) * 128 + j * 8;
+#pragma unroll
+        for (int u = 0; u < SPW; u++) {
+            const uint32_t du = cnt == 0 ? 0 : ((uint32_t)u < cnt ? u : cnt - 1);
+            wv[nb][u] = *(const uint4*)(wp + (size_t)du * 512);
+        }
+    }
 #pragma unroll
     for (int u = 0; u < SPW; u++) {
         const uint32_t du = cnt == 0 ? 0 : ((uint32_t)u < cnt ? u : cnt - 1);
-        wv[u] = *(const uint4*)(wp + (size_t)du * 512);
         if (EPI == EPI_STORE_NORM_IN)
             gv[u] = *(const uint4*)(a.in_gamma + (s0 + du) * 128 + j * 8);
     }
@@ -145,41 +157,45 @@ __device__ __forceinline__ bool proj_block(const ProjArgs& a, uint32_t b, int64_
             xv[u][r] = XCOH ? ld_coherent16(px) : *(const uint4*)px;
         }
     }
-    int32_t part[RT];
+    int32_t part[NB][RT];
 #pragma unroll
-    for (int r = 0; r < RT; r++) part[r] = 0;
+    for (int nb = 0; nb < NB; nb++)
+#pragma unroll
+        for (int r = 0; r < RT; r++) part[nb][r] = 0;
 #pragma unroll
     for (int u = 0; u < SPW; u++) {
-        const uint4 w = and4(wv[u], lane_mask((uint32_t)u < cnt));
+        const uint32_t keep = lane_mask((uint32_t)u < cnt);
 #pragma unroll
         for (int r = 0; r < RT; r++) {
             const uint4 x = EPI == EPI_STORE_NORM_IN ? norm8(xv[u][r], gv[u], a.in_gain)
                                                      : xv[u][r];
-            int32_t p = part[r];
-            p = dot2(w.x, x.x, p);
-            p = dot2(w.y, x.y, p);
-            p = dot2(w.z, x.z, p);
-            p = dot2(w.w, x.w, p);
-            part[r] = p;
+#pragma unroll
+            for (int nb = 0; nb < NB; nb++) {
+                const uint4 w = and4(wv[nb][u], keep);
+                int32_t p = part[nb][r];
+                p = dot2(w.x, x.x, p);
+                p = dot2(w.y, x.y, p);
+                p = dot2(w.z, x.z, p);
+                p = dot2(w.w, x.w, p);
+                part[nb][r] = p;
+            }
         }
     }
-    int64_t acc[RT];
 #pragma unroll
-    for (int r = 0; r < RT; r++) {
-        acc[r] = part[r];
+    for (int nb = 0; nb < NB; nb++)
 #pragma unroll
-        for (int off = 8; off > 0; off >>= 1) acc[r] += __shfl_xor(acc[r], off, 64);
-    }
-    if (j == 0) {
+        for (int r = 0; r < RT; r++) {
+            int64_t acc = part[nb][r];
 #pragma unroll
-        for (int r = 0; r < RT; r++) red[(wave * 4 + i) * RT + r] = acc[r];
-    }
+            for (int off = 8; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+            if (j == 0) red[((nb * WPB + wave) * 4 + i) * RT + r] = acc;
+        }
     lds_barrier();
     if (eout) {
-        const int ii = et / RT;
+        const int nb = et / (4 * RT), ii = (et % (4 * RT)) / RT;
         int64_t tot = 0;
 #pragma unroll
-        for (int w = 0; w < WPB; w++) tot += red[(w * 4 + ii) * RT + er];
+        for (int w = 0; w < WPB; w++) tot += red[((nb * WPB + w) * 4 + ii) * RT + er];
         proj_out<EPI, OCOH>(a, er, en, tot, tot, ei, nullptr);
     }
     return true;
