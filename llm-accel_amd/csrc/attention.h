@@ -71,18 +71,20 @@ struct SublayerArgs {
     ProjArgs qkv, o;
     AttnArgs at;
     uint32_t nq, na, no;
-    // Arrival counters (kSyncWords words) grow across launches: QKV block
-    // b adds 1 to line b % kSyncQkvLines, so after launch e (1, 2, ...)
-    // line l holds e times its blocks per launch; every attention
-    // workgroup adds 1 to each of kSyncAttnLines lines, which then hold
-    // attn_base + na.  The host keeps epoch and attn_base (mod 2^32).
+    // Arrival counters (kSyncWords words) grow across launches: QKV
+    // workgroup b adds 1 to line b % kSyncQkvLines, which held qkv_base[l]
+    // before the launch; every attention workgroup adds 1 to each of
+    // kSyncAttnLines lines, which held attn_base.  The host keeps the
+    // bases (mod 2^32).
     uint32_t* sync;
-    uint32_t epoch, attn_base;
+    uint32_t qkv_base[32];
+    uint32_t attn_base;
     uint32_t* host_abort;  // host-visible word, set when a wait gave up
     uint32_t wait_limit;   // bound of one wait (100 MHz ticks)
 };
 constexpr uint32_t kSyncStride = 32;  // words between counters (one 128-byte line)
 constexpr uint32_t kSyncQkvLines = 32, kSyncAttnLines = 16;
+static_assert(sizeof(SublayerArgs::qkv_base) == kSyncQkvLines * 4, "one base per QKV line");
 constexpr uint32_t kSyncAttn = kSyncQkvLines * kSyncStride;
 // Word of `sync` set when a wait gave up (cleared by the host).
 constexpr uint32_t kSyncAbort = kSyncAttn + kSyncAttnLines * kSyncStride;
@@ -95,8 +97,9 @@ constexpr uint32_t kSyncWords = kSyncAbort + kSyncStride;
 // for can always be dispatched).
 bool sublayer_fused_ok(const SublayerArgs& s, uint32_t rows, int qkv_epi, int L_qkv, int L_o,
                        int capacity);
-// QKV workgroups of the fused launch for `blocks` 4-row blocks.
+// QKV and O workgroups of the fused launch for `blocks` 4-row blocks.
 uint32_t sublayer_qkv_workgroups(uint32_t blocks);
+uint32_t sublayer_o_workgroups(uint32_t blocks);
 // Workgroups of the fused launch for (head_dim, rows, QKV epilogue) that
 // the device holds at once (`cus` compute units); 0 when unsupported.
 int sublayer_capacity(uint32_t head_dim, uint32_t rows, int qkv_epi, int cus);

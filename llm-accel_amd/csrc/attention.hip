@@ -1055,11 +1055,16 @@ __global__ __launch_bounds__(D * 2) void attention_split_head_kernel(AttnArgs a)
 // QKV blocks per workgroup of the fused attention sublayer
 constexpr uint32_t kSubQkvBlocks = LLM_SUB_QKV_NB;
 
+// O blocks per workgroup of the fused attention sublayer (half the waiting
+// workgroups of one block each, at the same measured time)
+constexpr uint32_t kSubOBlocks = 2;
+
 template <int D, int RT, int QEPI>
 __global__ __launch_bounds__(D * 2) void attention_sublayer_kernel(SublayerArgs s) {
     constexpr int WPB = D / 32, SPW = 4;
+    constexpr uint32_t NBR = kSubQkvBlocks > kSubOBlocks ? kSubQkvBlocks : kSubOBlocks;
     __shared__ SplitSmem<D> sm;
-    __shared__ int64_t red[kSubQkvBlocks * WPB * 4 * RT];
+    __shared__ int64_t red[NBR * WPB * 4 * RT];
     __shared__ uint32_t flag;
     uint32_t* const sync = s.sync;
     const uint32_t idx = blockIdx.x;
@@ -1076,7 +1081,7 @@ __global__ __launch_bounds__(D * 2) void attention_sublayer_kernel(SublayerArgs 
                 const uint32_t per = s.nq / kSyncQkvLines, extra = s.nq % kSyncQkvLines;
                 return wait_counts(
                     sync, kSyncStride, kSyncQkvLines,
-                    [&](uint32_t l) { return s.epoch * (per + (l < extra ? 1u : 0u)); },
+                    [&](uint32_t l) { return s.qkv_base[l] + per + (l < extra ? 1u : 0u); },
                     s.wait_limit, sync + kSyncAbort, s.host_abort, &flag);
             }))
             return;
@@ -1084,7 +1089,7 @@ __global__ __launch_bounds__(D * 2) void attention_sublayer_kernel(SublayerArgs 
         return;
     }
     const uint32_t b = idx - s.nq - s.na;
-    proj_block<RT, EPI_RESID, WPB, SPW, true, false>(s.o, b, red, [&] {
+    proj_block<RT, EPI_RESID, WPB, SPW, true, false, kSubOBlocks>(s.o, b, red, [&] {
         return wait_counts(
             sync + kSyncAttn + kSyncStride * (b % kSyncAttnLines), 0, 1,
             [&](uint32_t) { return s.attn_base + s.na; }, s.wait_limit, sync + kSyncAbort, s.host_abort, &flag);
@@ -1748,6 +1753,9 @@ int sublayer_capacity(uint32_t head_dim, uint32_t rows, int qkv_epi, int cus) {
 
 uint32_t sublayer_qkv_workgroups(uint32_t blocks) {
     return (blocks + kSubQkvBlocks - 1) / kSubQkvBlocks;
+}
+uint32_t sublayer_o_workgroups(uint32_t blocks) {
+    return (blocks + kSubOBlocks - 1) / kSubOBlocks;
 }
 
 bool sublayer_fused_ok(const SublayerArgs& s, uint32_t rows, int qkv_epi, int L_qkv, int L_o,

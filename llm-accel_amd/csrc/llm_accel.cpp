@@ -11,6 +11,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <iterator>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -123,7 +124,7 @@ struct llm_ctx {
     uint32_t* sync = nullptr;
     uint32_t* host_abort = nullptr;
     bool fused = true;                 // LLM_ACCEL_FUSED=0 disables it
-    uint32_t sync_epoch = 0;           // fused launches since the counters were zero
+    uint32_t sync_qkv[32] = {};        // QKV arrivals per line so far, mod 2^32
     uint32_t sync_attn = 0;            // attention arrivals per line, mod 2^32
     // bound of one wait (100 MHz ticks); LLM_ACCEL_WAIT_LIMIT overrides it
     // (tests force the time-out path with a tiny value)
@@ -221,7 +222,8 @@ int check_waits(llm_ctx* c) {
     if (!c->host_abort || __atomic_load_n(c->host_abort, __ATOMIC_ACQUIRE) == 0) return 0;
     (void)hipMemsetAsync(c->sync, 0, llm::kSyncWords * 4, c->stream);
     (void)hipStreamSynchronize(c->stream);
-    c->sync_epoch = c->sync_attn = 0;
+    std::fill(std::begin(c->sync_qkv), std::end(c->sync_qkv), 0u);
+    c->sync_attn = 0;
     __atomic_store_n(c->host_abort, 0u, __ATOMIC_RELEASE);
     return fail(LLM_E_HIP, "a wait between workgroups of a fused launch timed out; "
                            "results since the last synchronisation are invalid");
@@ -516,9 +518,9 @@ int enqueue_attention_sublayer(llm_ctx* c, uint32_t layer, uint32_t R,
     sub.at = at;
     sub.nq = llm::sublayer_qkv_workgroups(mq.n_pad / 4);
     sub.na = R * c->Hq;
-    sub.no = mo.n_pad / 4;
+    sub.no = llm::sublayer_o_workgroups(mo.n_pad / 4);
     sub.sync = c->sync;
-    sub.epoch = c->sync_epoch + 1;
+    std::copy(std::begin(c->sync_qkv), std::end(c->sync_qkv), sub.qkv_base);
     sub.attn_base = c->sync_attn;
     sub.host_abort = c->host_abort;
     sub.wait_limit = c->wait_limit;
@@ -532,8 +534,10 @@ int enqueue_attention_sublayer(llm_ctx* c, uint32_t layer, uint32_t R,
         llm::sublayer_fused_ok(sub, R, qkv_epi, mq.L, mo.L, cap)) {
         TimedScope ts(c, LLM_K_ATTN_SUBLAYER);
         HIP_TRY(llm::launch_attention_sublayer(sub, R, qkv_epi, st));
-        c->sync_epoch = sub.epoch;
-        c->sync_attn = sub.attn_base + sub.na;
+        // counter values after this launch
+        for (uint32_t l = 0; l < llm::kSyncQkvLines; l++)
+            c->sync_qkv[l] += sub.nq / llm::kSyncQkvLines + (l < sub.nq % llm::kSyncQkvLines);
+        c->sync_attn += sub.na;
     } else {
         {
             TimedScope ts(c, LLM_K_QKV);
