@@ -153,3 +153,43 @@ def test_wait_time_out_is_reported_and_cleared():
         code, want, _ = om.task(kv, 18, 0, h, 9)
         assert code == 0
         assert first_mismatch(got, want) is None
+
+
+@pytest.mark.parametrize("cfg", ["A", "B"])
+def test_fused_rows_across_tile_boundaries(cfg):
+    """Decode blocks of 1-2 rows in the fused launch at and across the
+    boundaries of its 4 tiles (the block's own K/V rows split over two
+    tiles, the last row of the 4th tile): every task's rows and every K/V
+    row equal the oracle's."""
+    spec = workloads.CONFIG_A if cfg == "A" else workloads.CONFIG_B
+    schedule = [(63, 2), (127, 2), (128, 1), (191, 2), (254, 2)]
+    synth = workloads.SyntheticModel(spec, seed=workloads.SEED + 13, layers=1)
+    om = oracle_from_synthetic(synth, oracle_shape(spec, layers=1, max_seq=256))
+    kv = om.new_kv()
+    pre = [synth.kv_rows(256, seed_offset=70 + h) for h in range(spec.kv_heads)]
+    hidden = synth.hidden_rows(2 * len(schedule))
+    acc = _accel(spec, 1, 256, {"LLM_ACCEL_FUSED": "1"})
+    with acc:
+        acc.load_model(synth)
+        for h, (k, v) in enumerate(pre):
+            # every position the schedule does not write: preloaded
+            acc.kv_write(0, h, 0, k, v)
+            kv[0][0, h, :] = k
+            kv[1][0, h, :] = v
+        for i, (pos, rows) in enumerate(schedule):
+            _say(f"case {cfg} fused rows={rows} at {pos}")
+            h = hidden[2 * i:2 * i + rows]
+            acc.upload(2, h)
+            acc.kernel_timing(True)
+            rc, _ = acc.task(18, 0, rows, pos, 2, 0)
+            assert rc == 0
+            got = acc.download(0, rows)
+            assert acc.kernel_stats()["attn_sublayer"][0] == 1
+            acc.kernel_timing(False)
+            code, want, _ = om.task(kv, 18, 0, h, pos)
+            assert code == 0
+            assert first_mismatch(got, want) is None, f"rows {rows} at {pos}"
+        for hh in range(spec.kv_heads):
+            k, v = acc.kv_read(0, hh, 0, 256)
+            assert first_mismatch(k, kv[0][0, hh]) is None, f"K head {hh}"
+            assert first_mismatch(v, kv[1][0, hh]) is None, f"V head {hh}"
