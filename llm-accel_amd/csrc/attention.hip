@@ -1623,32 +1623,43 @@ __global__ __launch_bounds__(D * 2) void attention_tile_pv_kernel(AttnArgs a) {
     // -128, sum 0, value 0) change nothing.
     int32_t m = INT16_MIN, sum = 0, acc = 0;
     constexpr int PL = 64 * D / 4 / NTH;  // 4-value groups per thread per piece
+    // A piece's operands are loaded while the previous piece is computed.
+    struct Piece {
+        uint64_t vals[PL];
+        int32_t tm, tsv;
+    };
+    auto load_piece = [&](uint32_t j0, Piece& pc) {
+        const uint32_t nj = j0 < ntiles ? (ntiles - j0 < 64 ? ntiles - j0 : 64) : 0;
+#pragma unroll
+        for (int u = 0; u < PL; u++) {  // all in flight
+            const uint32_t i = 4 * (tid + NTH * u), j = i / D, ee = i % D;
+            pc.vals[u] = j < nj ? ld_coherent((const uint64_t*)&a.s_tval[
+                                      ((rh * a.max_tiles + j0 + j) * G + gi) * D + ee])
+                                : 0ull;
+        }
+        pc.tm = INT16_MIN;
+        pc.tsv = 0;
+        if (tid < nj) {
+            const size_t b = (rh * a.max_tiles + j0 + tid) * G + gi;
+            pc.tm = a.s_tmax[b];
+            pc.tsv = ld_coherent(&a.s_tsum[b]);
+        }
+    };
+    Piece cur;
+    load_piece(0, cur);
     for (uint32_t j0 = 0; j0 < ntiles; j0 += 64) {
         const uint32_t nj = ntiles - j0 < 64 ? ntiles - j0 : 64;
         lds_barrier();  // the previous piece consumed
-        uint64_t vals[PL];
-#pragma unroll
-        for (int u = 0; u < PL; u++) {  // loads first, all in flight
-            const uint32_t i = 4 * (tid + NTH * u), j = i / D, ee = i % D;
-            vals[u] = j < nj ? ld_coherent((const uint64_t*)&a.s_tval[
-                                   ((rh * a.max_tiles + j0 + j) * G + gi) * D + ee])
-                             : 0ull;
-        }
-        int32_t tm = INT16_MIN, tsv = 0;
-        if (tid < nj) {
-            const size_t b = (rh * a.max_tiles + j0 + tid) * G + gi;
-            tm = a.s_tmax[b];
-            tsv = ld_coherent(&a.s_tsum[b]);
-        }
 #pragma unroll
         for (int u = 0; u < PL; u++) {
             const uint32_t i = 4 * (tid + NTH * u);
-            *(uint64_t*)&sm.tv[i / D][i % D] = vals[u];
+            *(uint64_t*)&sm.tv[i / D][i % D] = cur.vals[u];
         }
         if (tid < 64) {
-            sm.tmax[tid] = tm;
-            sm.tsum[tid] = tsv;
+            sm.tmax[tid] = cur.tm;
+            sm.tsum[tid] = cur.tsv;
         }
+        if (j0 + 64 < ntiles) load_piece(j0 + 64, cur);
         lds_barrier();
         if (tid < D) {
             for (uint32_t j = 0; j < nj; j += 8) {
@@ -1658,6 +1669,24 @@ __global__ __launch_bounds__(D * 2) void attention_tile_pv_kernel(AttnArgs a) {
                     tmv[u] = sm.tmax[j + u];
                     tsk[u] = sm.tsum[j + u];
                     tvv[u] = sm.tv[j + u][tid];
+                }
+                // Eight tiles none of which raises the running max, with sum
+                // and every lane's acc far enough from the int32 bounds that
+                // eight terms (sum: tile sums << 2 <= 2^22 each; acc: tile
+                // values << 8 <= 2^23 each) cannot saturate: one addition.
+                int32_t mx8 = tmv[0];
+#pragma unroll
+                for (int u = 1; u < 8; u++) mx8 = tmv[u] > mx8 ? tmv[u] : mx8;
+                const bool flat = __builtin_amdgcn_readfirstlane(mx8) <= m &&
+                                  sum <= INT32_MAX - (8 << 22) &&
+                                  __all(acc <= INT32_MAX - (8 << 23) && acc >= INT32_MIN + (8 << 23));
+                if (flat) {
+                    int32_t ts = 0, tvs = 0;
+#pragma unroll
+                    for (int u = 0; u < 8; u++) ts += tsk[u], tvs += tvv[u];
+                    sum += ts << 2;
+                    acc += tvs * 256;
+                    continue;
                 }
 #pragma unroll
                 for (int u = 0; u < 8; u++) {
