@@ -30,6 +30,7 @@ struct AttnArgs {
     int16_t* s_tmax;      // [8][kv_heads][max_tiles][group]
     int32_t* s_tsum;      // [8][kv_heads][max_tiles][group]
     int16_t* s_tval;      // [8][kv_heads][max_tiles][group][head_dim]
+    uint32_t grid_rows, grid_tiles;  // tile path: rows and tiles of the launch
     uint32_t* counters;   // zero between launches: chunked path [8][kv_heads];
                           // tile path kCounterStride words apart, per (row,
                           // query head) 1 + tile_groups(max_tiles) of them

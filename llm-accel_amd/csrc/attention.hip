@@ -1357,13 +1357,41 @@ __device__ __forceinline__ TileRows tile_rows(const AttnArgs& a, uint32_t tile, 
     return r;
 }
 
+// Workgroup -> (row, query head, tile) of the tile path.  Workgroups go to
+// the 8 XCDs round robin by linear index; the query heads of one (row, KV
+// head, tile), which read the same K / V page, are placed on one XCD one
+// after another, so that all but the first find the page in that XCD's L2
+// (heads placed on 8 XCDs read each page 8 times from memory).  The grid
+// is padded to whole groups of 8 (row, KV head, tile) triples.
+struct TileWg {
+    uint32_t t, g, tile;
+    bool valid;
+};
+__device__ __forceinline__ TileWg tile_wg(const AttnArgs& a) {
+    const uint32_t L = blockIdx.x, x = L % 8, seq = L / 8, G = a.group;
+    const uint32_t triple = (seq / G) * 8 + x;  // ((row, tile), KV head)
+    const uint32_t h = triple % a.num_kv_heads, rt = triple / a.num_kv_heads;
+    TileWg w;
+    w.t = rt / a.grid_tiles;
+    w.tile = rt % a.grid_tiles;
+    w.g = h * G + seq % G;
+    w.valid = w.t < a.grid_rows;
+    return w;
+}
+__host__ __device__ inline uint32_t tile_grid(uint32_t rows, uint32_t tiles, uint32_t kv_heads,
+                                              uint32_t group) {
+    return 8 * group * ((rows * tiles * kv_heads + 7) / 8);
+}
+
 template <int D>
 __global__ __launch_bounds__(D * 2) void attention_tile_scores_kernel(AttnArgs a) {
     static_assert(D % 32 == 0, "tile path: head_dim a multiple of 32");
     constexpr uint32_t NTH = D * 2;
     constexpr int NK = (8 * (D / 2) + NTH - 1) / NTH;  // block K items per thread
     __shared__ TileScoresSmem<D> sm;
-    const uint32_t t = blockIdx.x, g = blockIdx.y, tile = blockIdx.z, tid = threadIdx.x;
+    const TileWg wg = tile_wg(a);
+    if (!wg.valid) return;  // padding
+    const uint32_t t = wg.t, g = wg.g, tile = wg.tile, tid = threadIdx.x;
     const uint32_t n = a.pos0 + t + 1, own = n - 1;
     if (tile * TILE >= n) return;  // beyond this row's context
     const uint32_t lane = tid & 63, w = tid >> 6;
@@ -1494,7 +1522,9 @@ __global__ __launch_bounds__(D * 2) void attention_tile_pv_kernel(AttnArgs a) {
     constexpr int NV = (8 * D + NTH - 1) / NTH;  // block V elements per thread
     constexpr int NM = 4;                        // tile maxima per lane (tiles < 256)
     __shared__ TilePvSmem<D> sm;
-    const uint32_t t = blockIdx.x, g = blockIdx.y, tile = blockIdx.z, tid = threadIdx.x;
+    const TileWg wg = tile_wg(a);
+    if (!wg.valid) return;  // padding
+    const uint32_t t = wg.t, g = wg.g, tile = wg.tile, tid = threadIdx.x;
     const uint32_t n = a.pos0 + t + 1, own = n - 1;
     if (tile * TILE >= n) return;  // beyond this row's context
     const uint32_t ntiles = (n + TILE - 1) / TILE;
@@ -1714,10 +1744,14 @@ static hipError_t launch_d(const AttnArgs& a, uint32_t rows, uint32_t kv_heads,
     const uint32_t tiles = (a.pos0 + rows + TILE - 1) / TILE;
     if (D % 32 == 0 && tiles > kSplitHeadMaxTiles) {
         constexpr int DT = D % 32 == 0 ? D : 32;
-        attention_tile_scores_kernel<DT><<<dim3(rows, a.num_heads, tiles), 2 * D, 0, st>>>(a);
+        AttnArgs g = a;
+        g.grid_rows = rows;
+        g.grid_tiles = tiles;
+        const uint32_t grid = tile_grid(rows, tiles, a.num_kv_heads, a.group);
+        attention_tile_scores_kernel<DT><<<grid, 2 * D, 0, st>>>(g);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
-        attention_tile_pv_kernel<DT><<<dim3(rows, a.num_heads, tiles), 2 * D, 0, st>>>(a);
+        attention_tile_pv_kernel<DT><<<grid, 2 * D, 0, st>>>(g);
         return hipGetLastError();
     }
     if (D % 32 == 0 || chunks <= 1) {
