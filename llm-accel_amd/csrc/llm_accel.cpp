@@ -781,6 +781,20 @@ int llm_ctx_create(const llm_shape_t* shape, int device, uint32_t num_pairs,
     c->wait_limit = llm::kWaitLimitTicks;
     if (const char* e = std::getenv("LLM_ACCEL_WAIT_LIMIT"))
         c->wait_limit = (uint32_t)std::strtoul(e, nullptr, 10);
+    // Test hook: every arrival counter (and the host's copy) starts at
+    // LLM_ACCEL_SYNC_START instead of 0, e.g. just below 2^32 so that the
+    // counters wrap within a few launches.
+    if (const char* e = std::getenv("LLM_ACCEL_SYNC_START")) {
+        const uint32_t v = (uint32_t)std::strtoul(e, nullptr, 0);
+        std::vector<uint32_t> init(llm::kSyncWords, 0);
+        for (uint32_t l = 0; l < llm::kSyncQkvLines; l++) init[l * llm::kSyncStride] = v;
+        for (uint32_t l = 0; l < llm::kSyncAttnLines; l++)
+            init[llm::kSyncAttn + l * llm::kSyncStride] = v;
+        if (hipMemcpy(c->sync, init.data(), init.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
+            return cleanup(fail(LLM_E_HIP, "counter initialisation failed"));
+        std::fill(std::begin(c->sync_qkv), std::end(c->sync_qkv), v);
+        c->sync_attn = v;
+    }
     {
         const size_t rhc = (size_t)8 * c->Hkv * cdiv(c->tiles, c->chunk_tiles) * c->G;
         if ((rc = dev_alloc(c, (void**)&c->c_flag, rhc * 4)) ||

@@ -193,3 +193,44 @@ def test_fused_rows_across_tile_boundaries(cfg):
             k, v = acc.kv_read(0, hh, 0, 256)
             assert first_mismatch(k, kv[0][0, hh]) is None, f"K head {hh}"
             assert first_mismatch(v, kv[1][0, hh]) is None, f"V head {hh}"
+
+
+@pytest.mark.parametrize("start", [0, 0xFFFFFF80])
+def test_fused_long_mixed_sequence(start):
+    """A long sequence mixing fused launches (1-2 rows) with separate ones
+    (8-row and 5-row blocks) over two layers, checked against the oracle
+    after every task: the host's copies of the arrival counters stay in
+    step with the device's.  Started just below 2^32 the counters wrap
+    within a few launches (the waits compare modulo 2^32)."""
+    spec = workloads.CONFIG_A
+    layers = 2
+    synth = workloads.SyntheticModel(spec, seed=workloads.SEED + 17, layers=layers)
+    om = oracle_from_synthetic(synth, oracle_shape(spec, layers=layers, max_seq=128))
+    kv = om.new_kv()
+    schedule = [(0, 8)] + [(8 + i, 1) for i in range(6)] + [(14, 5)] + \
+               [(19 + 2 * i, 2) for i in range(6)] + [(31, 1), (32, 8)] + \
+               [(40 + i, 1) for i in range(6)]
+    total = sum(r for _, r in schedule)
+    hidden = synth.hidden_rows(total)
+    acc = _accel(spec, layers, 128, {"LLM_ACCEL_FUSED": "1",
+                                     "LLM_ACCEL_SYNC_START": str(start)})
+    with acc:
+        acc.load_model(synth)
+        row0 = 0
+        for pos, rows in schedule:
+            h = hidden[row0:row0 + rows]
+            row0 += rows
+            _say(f"case A start={start:#x} pos={pos} rows={rows}")
+            acc.upload(2, h)
+            cur = h
+            pin, pout = 2, 0
+            for layer in range(layers):
+                for op in (18, 19):
+                    rc, _ = acc.task(op, layer, rows, pos, pin, pout)
+                    assert rc == 0
+                    code, want, _ = om.task(kv, op, layer, cur, pos)
+                    assert code == 0
+                    err = first_mismatch(acc.download(pout, rows), want)
+                    assert err is None, f"op {op} layer {layer} at {pos}: {err}"
+                    cur = want
+                    pin, pout = pout, pin
