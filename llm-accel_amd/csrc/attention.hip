@@ -764,9 +764,18 @@ struct SplitRegs {
 // rows are used.
 //   K: load c, lane l = position 16 c + l / 4, elements 8 (l % 4) ..
 //   V: load c, lane l = V^T row 8 c + l / 8, positions 8 (l % 8) ..
-template <int D>
+template <int D, bool SKIP = false>
 __device__ __forceinline__ void slice_load(const AttnArgs& a, uint32_t h, uint32_t tile,
                                            uint32_t w, uint32_t lane, SplitRegs& R) {
+    // SKIP: a tile that holds no cached position (the block's first rows
+    // at the start of the context) reads nothing, every value would be
+    // masked (not in the fused launch, where the branch costs more than
+    // the loads it saves)
+    if (SKIP && tile * TILE >= a.pos0) {
+#pragma unroll
+        for (int c = 0; c < 4; c++) R.k[c] = R.v[c] = v4u{0, 0, 0, 0};
+        return;
+    }
     const uint32_t tp = tile < a.tiles ? tile : a.tiles - 1;
     const int16_t* kp = a.kcache + page_off<D>(a, h, tp) + 32 * w + 8 * (lane & 3);
     const int16_t* vp = a.vcache + page_off<D>(a, h, tp) + (size_t)32 * w * TILE + 8 * lane;
@@ -841,7 +850,7 @@ __device__ __forceinline__ bool split_head_body(const AttnArgs& a, uint32_t t, u
         kx[u][3] = kr[D / 2 + c];
     }
     SplitRegs regs;
-    slice_load<D>(a, h, 0, w, lane, regs);
+    slice_load<D, !FUSED>(a, h, 0, w, lane, regs);
     if (FUSED && !wait()) return false;
     // the block's q / k / v rows
     auto ld_row = [&](const int16_t* p) -> int32_t { return FUSED ? ld_coherent(p) : *p; };
@@ -898,7 +907,7 @@ __device__ __forceinline__ bool split_head_body(const AttnArgs& a, uint32_t t, u
     for (uint32_t tile = 0; tile < ntiles; tile++) {
         const SplitRegs cur = regs;
         // the next tile's slices (a repeat of this tile's on the last one)
-        slice_load<D>(a, h, tile + 1 < ntiles ? tile + 1 : tile, w, lane, regs);
+        slice_load<D, !FUSED>(a, h, tile + 1 < ntiles ? tile + 1 : tile, w, lane, regs);
         // ---- QK partials over this wavefront's elements ----
         const uint32_t p = tile * TILE + lane;
         const bool valid = p < n;
