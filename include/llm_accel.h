@@ -225,6 +225,24 @@ int llm_load_lm_head(llm_ctx_t* ctx, const int16_t* table, uint32_t vocab);
 int llm_lm_head_argmax(llm_ctx_t* ctx, uint32_t pair, uint32_t row0,
                        uint32_t rows, uint32_t* tokens, int64_t* scores);
 
+/* No counterpart in the reference.  For callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops): the
+ * argmax of llm_lm_head_argmax() over memory the caller owns, with no
+ * context and no allocation.  table is device memory [vocab][hidden] raw
+ * int16 (the reference's row-major LM head); rows is device memory
+ * [row_count][ld]; tokens (uint32 [row_count]) and scores (int64
+ * [row_count], optional) are device memory.  Work is enqueued on `stream`
+ * (a hipStream_t; NULL = the null stream) and not waited for.  Limits:
+ * row_count <= 8, vocab < 2^18, hidden <= 16384 and a multiple of 8, ld a
+ * multiple of 8, table and rows 16-byte aligned; larger sizes return
+ * LLM_E_ARG.  Its scratch is 64 bytes of static device memory per device,
+ * shared by every call on that device: calls that overlap on one device
+ * race. */
+int llm_lm_head_argmax_static(const int16_t* table, uint32_t vocab,
+                              uint32_t hidden, const int16_t* rows,
+                              uint32_t ld, uint32_t row_count,
+                              uint32_t* tokens, int64_t* scores, void* stream);
+
 /* Report of llm_generate (the QWEN_8X64_E2E_PROFILE fields of the
  * reference's generate mode, host/host_qwen_8x64.cpp:9264-9336). */
 typedef struct {

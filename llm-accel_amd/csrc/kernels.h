@@ -71,6 +71,9 @@ constexpr uint32_t kMfRows = 16;
 constexpr uint32_t kMfCols = 64;
 constexpr uint32_t kMfRecord = 2048;
 
+// Records `msg` as the text llm_last_error() returns; returns `code`.
+int set_last_error(int code, const char* msg);
+
 hipError_t launch_copy(const uint4* src, uint4* dst, size_t n16,
                        hipStream_t st);
 
@@ -80,6 +83,10 @@ hipError_t launch_copy(const uint4* src, uint4* dst, size_t n16,
 // ties.  keys[r] must be zero on entry; it receives
 // ((score + 2^45) << 18) | (2^18 - 1 - v) of the winner.
 constexpr uint32_t kArgmaxVocabMax = (1u << 18) - 1;
+__device__ __forceinline__ unsigned long long argmax_key(int64_t score, uint32_t v) {
+    return ((unsigned long long)(score + ((int64_t)1 << 45)) << 18) |
+           (unsigned long long)(kArgmaxVocabMax - v);
+}
 hipError_t launch_lm_argmax(const int16_t* w, uint32_t steps, uint32_t n,
                             const int16_t* x, uint32_t ldx, uint32_t rows, int L,
                             unsigned long long* keys, hipStream_t st);

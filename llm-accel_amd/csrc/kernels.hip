@@ -530,11 +530,6 @@ __global__ __launch_bounds__(64 * KS) void proj_mfma_kernel(ProjArgs a, uint32_t
 // goes into one 64-bit atomicMax per row.  The key orders by score, then
 // by smaller v, so equal scores resolve to the first index.
 // ---------------------------------------------------------------------
-__device__ __forceinline__ unsigned long long argmax_key(int64_t score, uint32_t v) {
-    return ((unsigned long long)(score + ((int64_t)1 << 45)) << 18) |
-           (unsigned long long)(kArgmaxVocabMax - v);
-}
-
 template <int RT, int L>
 __global__ __launch_bounds__(256) void lm_argmax_kernel(const int16_t* __restrict__ w,
                                                         uint32_t S, uint32_t n,

@@ -51,6 +51,14 @@ int fail(int code, const std::string& msg) {
         if (int rc_ = check_waits(c)) return rc_;                       \
     } while (0)
 
+}  // namespace
+
+namespace llm {
+int set_last_error(int code, const char* msg) { return fail(code, msg); }
+}  // namespace llm
+
+namespace {
+
 uint32_t round_up(uint32_t v, uint32_t m) { return (v + m - 1) / m * m; }
 uint64_t cdiv(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
 

@@ -33,7 +33,7 @@ EXPORTS = (
     "llm_event_record", "llm_event_elapsed_ms", "llm_exp_tables",
     "llm_kernel_timing", "llm_kernel_stats", "llm_bench_copy",
     "llm_bench_projection", "llm_load_lm_head", "llm_lm_head_argmax",
-    "llm_generate",
+    "llm_generate", "llm_lm_head_argmax_static",
 )
 KERNELS = ("rmsnorm", "qkv", "rope", "attention", "oproj", "gateup", "down",
            "attn_sublayer")
@@ -136,6 +136,8 @@ def load_library(path=LIB_PATH):
                                         _u32, _u32, _u32,
                                         ctypes.POINTER(ctypes.c_uint32),
                                         ctypes.POINTER(GenerateStats)]),
+        "llm_lm_head_argmax_static": (ctypes.c_int, [vp, _u32, _u32, vp, _u32,
+                                                     _u32, vp, vp, vp]),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)
