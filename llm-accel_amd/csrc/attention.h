@@ -104,7 +104,8 @@ uint32_t sublayer_o_workgroups(uint32_t blocks);
 // Workgroups of the fused launch for (head_dim, rows, QKV epilogue) that
 // the device holds at once (`cus` compute units); 0 when unsupported.
 int sublayer_capacity(uint32_t head_dim, uint32_t rows, int qkv_epi, int cus);
+// L: the smaller widening interval of the QKV and O matrices.
 hipError_t launch_attention_sublayer(const SublayerArgs& s, uint32_t rows, int qkv_epi,
-                                     hipStream_t st);
+                                     int L, hipStream_t st);
 
 }  // namespace llm

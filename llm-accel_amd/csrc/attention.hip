@@ -1068,7 +1068,7 @@ constexpr uint32_t kSubQkvBlocks = LLM_SUB_QKV_NB;
 // workgroups of one block each, at the same measured time)
 constexpr uint32_t kSubOBlocks = 2;
 
-template <int D, int RT, int QEPI>
+template <int D, int RT, int QEPI, int LW>
 __global__ __launch_bounds__(D * 2) void attention_sublayer_kernel(SublayerArgs s) {
     constexpr int WPB = D / 32, SPW = 4;
     constexpr uint32_t NBR = kSubQkvBlocks > kSubOBlocks ? kSubQkvBlocks : kSubOBlocks;
@@ -1078,8 +1078,8 @@ __global__ __launch_bounds__(D * 2) void attention_sublayer_kernel(SublayerArgs 
     uint32_t* const sync = s.sync;
     const uint32_t idx = blockIdx.x;
     if (idx < s.nq) {
-        proj_block<RT, QEPI, WPB, SPW, false, true, kSubQkvBlocks>(s.qkv, idx, red,
-                                                                  [] { return true; });
+        proj_block<RT, QEPI, WPB, SPW, false, true, LW, kSubQkvBlocks>(s.qkv, idx, red,
+                                                                      [] { return true; });
         arrive(sync + kSyncStride * (idx % kSyncQkvLines));
         return;
     }
@@ -1098,7 +1098,7 @@ __global__ __launch_bounds__(D * 2) void attention_sublayer_kernel(SublayerArgs 
         return;
     }
     const uint32_t b = idx - s.nq - s.na;
-    proj_block<RT, EPI_RESID, WPB, SPW, true, false, kSubOBlocks>(s.o, b, red, [&] {
+    proj_block<RT, EPI_RESID, WPB, SPW, true, false, LW, kSubOBlocks>(s.o, b, red, [&] {
         return wait_counts(
             sync + kSyncAttn + kSyncStride * (b % kSyncAttnLines), 0, 1,
             [&](uint32_t) { return s.attn_base + s.na; }, s.wait_limit, sync + kSyncAbort, s.host_abort, &flag);
@@ -1798,13 +1798,18 @@ hipError_t launch_attention(const AttnArgs& a, uint32_t rows, uint32_t kv_heads,
 }
 
 
+// The smallest residency over the widening variants of the launch.
 template <int D, int RT, int QEPI>
 static int sublayer_capacity_of(int cus) {
-    int per_cu = 0;
+    int per_cu[3] = {0, 0, 0};
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &per_cu, attention_sublayer_kernel<D, RT, QEPI>, 2 * D, 0) != hipSuccess)
+            &per_cu[0], attention_sublayer_kernel<D, RT, QEPI, 4>, 2 * D, 0) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &per_cu[1], attention_sublayer_kernel<D, RT, QEPI, 1>, 2 * D, 0) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &per_cu[2], attention_sublayer_kernel<D, RT, QEPI, 0>, 2 * D, 0) != hipSuccess)
         return 0;
-    return per_cu * cus;
+    return std::min({per_cu[0], per_cu[1], per_cu[2]}) * cus;
 }
 
 template <int D, int RT>
@@ -1837,28 +1842,40 @@ bool sublayer_fused_ok(const SublayerArgs& s, uint32_t rows, int qkv_epi, int L_
     if (qkv_epi != EPI_STORE && qkv_epi != EPI_STORE_NORM_IN) return false;
     const uint32_t tiles = (s.at.pos0 + rows + TILE - 1) / TILE;
     if (tiles > kSplitHeadMaxTiles || rows > kSplitHeadRows) return false;
-    // int32 sums of up to 4 k-steps per wavefront: widening interval >= 4
+    // up to 4 k-steps per wavefront (any widening interval: see launch_sub)
     const uint32_t wpb = D / 32;
-    if (L_qkv < 4 || L_o < 4 || s.qkv.steps > 4 * wpb || s.o.steps > 4 * wpb) return false;
+    (void)L_qkv;
+    (void)L_o;
+    if (s.qkv.steps > 4 * wpb || s.o.steps > 4 * wpb) return false;
     if (!s.sync || !s.host_abort) return false;
     return (int64_t)s.na + s.no < capacity;
 }
 
-template <int D, int RT>
-static void launch_sub(const SublayerArgs& s, int qkv_epi, hipStream_t st) {
+template <int D, int RT, int LW>
+static void launch_sub_l(const SublayerArgs& s, int qkv_epi, hipStream_t st) {
     const uint32_t grid = s.nq + s.na + s.no;
     if (qkv_epi == EPI_STORE_NORM_IN)
-        attention_sublayer_kernel<D, RT, EPI_STORE_NORM_IN><<<grid, 2 * D, 0, st>>>(s);
+        attention_sublayer_kernel<D, RT, EPI_STORE_NORM_IN, LW><<<grid, 2 * D, 0, st>>>(s);
     else
-        attention_sublayer_kernel<D, RT, EPI_STORE><<<grid, 2 * D, 0, st>>>(s);
+        attention_sublayer_kernel<D, RT, EPI_STORE, LW><<<grid, 2 * D, 0, st>>>(s);
+}
+
+// The int32 sums of the QKV and O roles (up to 4 k-steps per wavefront)
+// widen once when both matrices' widening intervals reach 4, after every
+// step when they are at least 1, and every product otherwise.
+template <int D, int RT>
+static void launch_sub(const SublayerArgs& s, int qkv_epi, int L, hipStream_t st) {
+    if (L >= 4) launch_sub_l<D, RT, 4>(s, qkv_epi, st);
+    else if (L >= 1) launch_sub_l<D, RT, 1>(s, qkv_epi, st);
+    else launch_sub_l<D, RT, 0>(s, qkv_epi, st);
 }
 
 hipError_t launch_attention_sublayer(const SublayerArgs& s, uint32_t rows, int qkv_epi,
-                                     hipStream_t st) {
+                                     int L, hipStream_t st) {
     if (s.at.head_dim == 64)
-        rows == 1 ? launch_sub<64, 1>(s, qkv_epi, st) : launch_sub<64, 2>(s, qkv_epi, st);
+        rows == 1 ? launch_sub<64, 1>(s, qkv_epi, L, st) : launch_sub<64, 2>(s, qkv_epi, L, st);
     else
-        rows == 1 ? launch_sub<128, 1>(s, qkv_epi, st) : launch_sub<128, 2>(s, qkv_epi, st);
+        rows == 1 ? launch_sub<128, 1>(s, qkv_epi, L, st) : launch_sub<128, 2>(s, qkv_epi, L, st);
     return hipGetLastError();
 }
 

@@ -162,14 +162,21 @@ __global__ __launch_bounds__(64 * WPB) void proj_kernel(ProjArgs a) {
             for (int m = 0; m < NM; m++)
 #pragma unroll
                 for (int r = 0; r < RT; r++) {
-                    int32_t p = part[m][r];
-                    p = dot2(wv[u][m].x, xv[u][r].x, p);
-                    p = dot2(wv[u][m].y, xv[u][r].y, p);
-                    p = dot2(wv[u][m].z, xv[u][r].z, p);
-                    p = dot2(wv[u][m].w, xv[u][r].w, p);
-                    part[m][r] = p;
+                    if (L == 0) {  // any weight: every product widened
+                        acc[m][r] += dot2_wide(wv[u][m].x, xv[u][r].x) +
+                                     dot2_wide(wv[u][m].y, xv[u][r].y) +
+                                     dot2_wide(wv[u][m].z, xv[u][r].z) +
+                                     dot2_wide(wv[u][m].w, xv[u][r].w);
+                    } else {
+                        int32_t p = part[m][r];
+                        p = dot2(wv[u][m].x, xv[u][r].x, p);
+                        p = dot2(wv[u][m].y, xv[u][r].y, p);
+                        p = dot2(wv[u][m].z, xv[u][r].z, p);
+                        p = dot2(wv[u][m].w, xv[u][r].w, p);
+                        part[m][r] = p;
+                    }
                 }
-            if (L < SPW && (u + 1) % L == 0) {
+            if (L != 0 && L < SPW && (u + 1) % L == 0) {
 #pragma unroll
                 for (int m = 0; m < NM; m++)
 #pragma unroll
@@ -644,9 +651,11 @@ __global__ __launch_bounds__(256) void copy_kernel(const uint4* __restrict__ src
 // ---------------------------------------------------------------------
 template <int RT, int EPI, int W, int SPW>
 static void launch_proj_s(const ProjArgs& a, int L, uint32_t blocks, hipStream_t st) {
-    // SPW <= 4: the int32 sums of a wavefront's steps widen once at the
-    // end (L >= 4)
-    proj_kernel<RT, 4, EPI, W, SPW><<<blocks, 64 * W, 0, st>>>(a);
+    // SPW <= 4: with L >= 4 the int32 sums of a wavefront's steps widen
+    // once at the end; L 1..3 widens after every step, L 0 every product
+    if (L >= 4) proj_kernel<RT, 4, EPI, W, SPW><<<blocks, 64 * W, 0, st>>>(a);
+    else if (L >= 1) proj_kernel<RT, 1, EPI, W, SPW><<<blocks, 64 * W, 0, st>>>(a);
+    else proj_kernel<RT, 0, EPI, W, SPW><<<blocks, 64 * W, 0, st>>>(a);
 }
 
 template <int RT, int EPI, int W>
@@ -656,7 +665,7 @@ static hipError_t launch_proj_w(const ProjArgs& a, int L, uint32_t blocks,
     // reductions (the down projection: 6) measured faster with the loop,
     // two steps of loads at a time, at lower register use
     const uint32_t spw = (a.steps + W - 1) / W;
-    if (RT <= 2 && L >= 4 && spw <= 4) {
+    if (RT <= 2 && spw <= 4) {
         if (spw <= 2) launch_proj_s<RT, EPI, W, 2>(a, L, blocks, st);
         else launch_proj_s<RT, EPI, W, 4>(a, L, blocks, st);
         return hipGetLastError();

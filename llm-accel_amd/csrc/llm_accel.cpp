@@ -541,7 +541,7 @@ int enqueue_attention_sublayer(llm_ctx* c, uint32_t layer, uint32_t R,
     if (c->fused && !llm::proj_uses_mfma(a, qkv_epi) && !llm::proj_uses_mfma(o, llm::EPI_RESID) &&
         llm::sublayer_fused_ok(sub, R, qkv_epi, mq.L, mo.L, cap)) {
         TimedScope ts(c, LLM_K_ATTN_SUBLAYER);
-        HIP_TRY(llm::launch_attention_sublayer(sub, R, qkv_epi, st));
+        HIP_TRY(llm::launch_attention_sublayer(sub, R, qkv_epi, std::min(mq.L, mo.L), st));
         // counter values after this launch
         for (uint32_t l = 0; l < llm::kSyncQkvLines; l++)
             c->sync_qkv[l] += sub.nq / llm::kSyncQkvLines + (l < sub.nq % llm::kSyncQkvLines);

@@ -110,9 +110,12 @@ __device__ __forceinline__ void proj_out(const ProjArgs& a, uint32_t r, uint32_t
 // of the same launch wrote.  Steps past a wavefront's last repeat its last
 // address and blocks past the matrix its last block; both are masked at
 // use, so that no branch separates a load from its use.  red: LDS of
-// NB * WPB * 4 * RT int64.  Returns false when wait() gave up (uniform
-// over the workgroup).
-template <int RT, int EPI, int WPB, int SPW, bool XCOH, bool OCOH, int NB = 1, typename Wait>
+// NB * WPB * 4 * RT int64.  LW: the int32 sums widen once at the end (4:
+// the matrix's widening interval covers SPW steps), after every step (1)
+// or every product is widened (0).  Returns false when wait() gave up
+// (uniform over the workgroup).
+template <int RT, int EPI, int WPB, int SPW, bool XCOH, bool OCOH, int LW, int NB = 1,
+          typename Wait>
 __device__ __forceinline__ bool proj_block(const ProjArgs& a, uint32_t b, int64_t* red,
                                            Wait&& wait) {
     static_assert(EPI != EPI_SILU, "one matrix per block");
@@ -158,10 +161,11 @@ __device__ __forceinline__ bool proj_block(const ProjArgs& a, uint32_t b, int64_
         }
     }
     int32_t part[NB][RT];
+    int64_t wide[NB][RT];
 #pragma unroll
     for (int nb = 0; nb < NB; nb++)
 #pragma unroll
-        for (int r = 0; r < RT; r++) part[nb][r] = 0;
+        for (int r = 0; r < RT; r++) part[nb][r] = 0, wide[nb][r] = 0;
 #pragma unroll
     for (int u = 0; u < SPW; u++) {
         const uint32_t keep = lane_mask((uint32_t)u < cnt);
@@ -172,12 +176,18 @@ __device__ __forceinline__ bool proj_block(const ProjArgs& a, uint32_t b, int64_
 #pragma unroll
             for (int nb = 0; nb < NB; nb++) {
                 const uint4 w = and4(wv[nb][u], keep);
-                int32_t p = part[nb][r];
-                p = dot2(w.x, x.x, p);
-                p = dot2(w.y, x.y, p);
-                p = dot2(w.z, x.z, p);
-                p = dot2(w.w, x.w, p);
-                part[nb][r] = p;
+                if (LW == 0) {
+                    wide[nb][r] += dot2_wide(w.x, x.x) + dot2_wide(w.y, x.y) +
+                                   dot2_wide(w.z, x.z) + dot2_wide(w.w, x.w);
+                } else {
+                    int32_t p = part[nb][r];
+                    p = dot2(w.x, x.x, p);
+                    p = dot2(w.y, x.y, p);
+                    p = dot2(w.z, x.z, p);
+                    p = dot2(w.w, x.w, p);
+                    part[nb][r] = p;
+                    if (LW == 1) wide[nb][r] += p, part[nb][r] = 0;
+                }
             }
         }
     }
@@ -185,7 +195,7 @@ __device__ __forceinline__ bool proj_block(const ProjArgs& a, uint32_t b, int64_
     for (int nb = 0; nb < NB; nb++)
 #pragma unroll
         for (int r = 0; r < RT; r++) {
-            int64_t acc = part[nb][r];
+            int64_t acc = wide[nb][r] + part[nb][r];
 #pragma unroll
             for (int off = 8; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
             if (j == 0) red[((nb * WPB + wave) * 4 + i) * RT + r] = acc;
