@@ -151,7 +151,12 @@ def test_kat1_post_ffn_fingerprint():
                               k["post_ffn_first"])
 
 
+_generate_cache = {}
+
+
 def _run_generate(layers):
+    if layers in _generate_cache:
+        return _generate_cache[layers]
     m = orc.Model(orc.profile("qwen2.5-3b"), layers, True)
     m.init_reference_random(20260718, orc.UID_DIVREJ)
     emb = m.embedding()
@@ -168,6 +173,7 @@ def _run_generate(layers):
         _, h, _ = m.task(kv, 19, layer, h, 8)
     _, fin1, _ = m.task(kv, 20, 0, h, 8)
     tok1 = orc.lm_head_argmax(emb, fin1[0])
+    _generate_cache[layers] = ([tok0, tok1], fin)
     return [tok0, tok1], fin
 
 
@@ -181,3 +187,33 @@ def test_kat2_qwen3b_one_layer_tokens():
 def test_kat3_qwen3b_two_layer_tokens():
     toks, _ = _run_generate(2)
     assert toks == KAT["kat3_qwen3b_l2"]["generated"]
+
+
+_SILU_XFAIL = pytest.mark.xfail(
+    strict=True,
+    reason="parity unpinned: the reference's hls::exp<16,8> (SiLU, host/host_qwen_8x64.cpp"
+           ":578-586) is not floor(e^x*256) at every entry; the final hidden rows after "
+           "the FFN differ from the reference's in low bits, so their FNV-1a checksums "
+           "do not reproduce (the sampled tokens do)")
+
+
+@pytest.mark.slow
+@_SILU_XFAIL
+@pytest.mark.parametrize("pos", range(8))
+def test_kat2_qwen3b_one_layer_final_hidden_checksums(pos):
+    """results/qwen3b-e2e-20260820/host.evidence.log:40-47: FNV-1a-64 of the
+    final-normed row of each prompt position (position 7 golden-verified,
+    :53)."""
+    _, fin = _run_generate(1)
+    want = int(KAT["kat2_qwen3b_l1"]["final_hidden_checksums"][pos], 16)
+    assert orc.checksum(fin[pos]) == want
+
+
+@pytest.mark.slow
+@_SILU_XFAIL
+def test_kat3_qwen3b_two_layer_final_hidden_checksum_pos7():
+    """results/qwen3b-e2e-l2-20260821/host.evidence.log:49: position 7's
+    final-normed row after two layers (golden-verified)."""
+    _, fin = _run_generate(2)
+    want = int(KAT["kat3_qwen3b_l2"]["final_hidden_checksum_pos7"], 16)
+    assert orc.checksum(fin[7]) == want
