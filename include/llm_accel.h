@@ -195,7 +195,8 @@ enum {
     LLM_K_GATEUP = 5,    /* gate | up projection + SiLU * up           */
     LLM_K_DOWN = 6,      /* down projection + residual                 */
     LLM_K_ATTN_SUBLAYER = 7, /* QKV + attention + O in one launch (decode) */
-    LLM_K_COUNT = 8
+    LLM_K_DECODE_STACK = 8,  /* a run of decode sublayers in one launch   */
+    LLM_K_COUNT = 9
 };
 int llm_kernel_timing(llm_ctx_t* ctx, int enable);
 int llm_kernel_stats(llm_ctx_t* ctx, uint32_t kernel, uint64_t* launches,

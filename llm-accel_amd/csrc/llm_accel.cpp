@@ -23,6 +23,7 @@
 
 #include "attention.h"
 #include "coherent.h"
+#include "decode_stack.h"
 #include "fixed_point.h"
 #include "kernels.h"
 
@@ -171,6 +172,24 @@ struct llm_ctx {
     double kernel_ms[LLM_K_COUNT] = {};
     uint64_t kernel_n[LLM_K_COUNT] = {};
 
+    // Persistent decode launches (decode_stack.hip): decode tasks (1-2
+    // rows, Task 18 / 19 / 16) are collected and run as one launch when
+    // the caller next needs a result or issues anything else.
+    uint32_t ds_nwg[2] = {0, 0};      // workgroups for 1 / 2 rows; 0: unavailable
+    uint32_t* ds_sync = nullptr;      // arrival counters (kStackSyncWords)
+    uint32_t ds_occ[llm::kStackGroups] = {};  // group occurrences so far, mod 2^32
+    uint32_t ds_start = 0;            // counter value at creation
+    bool ds_enabled = false;          // LLM_ACCEL_STACK=1 enables
+    size_t ds_layer_stride = 0;       // elements between layers' matrices
+    struct DsStep {
+        uint32_t layer;
+        int in, out;
+        uint32_t ffn;
+    };
+    std::vector<DsStep> ds_pending;
+    uint32_t ds_rows = 0, ds_pos = 0;
+    int ds_lw = 4;                    // widening of the pending run (4 or 1)
+
     // LM head [vocab][hidden] (tile4x128) and the argmax keys of 8 rows
     Matrix lm;
     uint32_t lm_vocab = 0;
@@ -229,9 +248,12 @@ void harvest_timing(llm_ctx* c) {
 int check_waits(llm_ctx* c) {
     if (!c->host_abort || __atomic_load_n(c->host_abort, __ATOMIC_ACQUIRE) == 0) return 0;
     (void)hipMemsetAsync(c->sync, 0, llm::kSyncWords * 4, c->stream);
+    if (c->ds_sync) (void)hipMemsetAsync(c->ds_sync, 0, llm::kStackSyncWords * 4, c->stream);
     (void)hipStreamSynchronize(c->stream);
     std::fill(std::begin(c->sync_qkv), std::end(c->sync_qkv), 0u);
     c->sync_attn = 0;
+    std::fill(std::begin(c->ds_occ), std::end(c->ds_occ), 0u);
+    c->ds_start = 0;
     __atomic_store_n(c->host_abort, 0u, __ATOMIC_RELEASE);
     return fail(LLM_E_HIP, "a wait between workgroups of a fused launch timed out; "
                            "results since the last synchronisation are invalid");
@@ -633,7 +655,147 @@ int enqueue_ffn_sublayer(llm_ctx* c, uint32_t layer, uint32_t R, int in_pair,
     return 0;
 }
 
+// Whether decode task (op, R rows at pos, layer) can join a persistent
+// launch; *lw receives the widening it needs (4 or 1).
+bool ds_eligible(const llm_ctx* c, uint32_t R, uint32_t pos, uint32_t layer, int* lw) {
+    if (!c->ds_enabled || R == 0 || R > 2 || c->ds_nwg[R - 1] == 0) return false;
+    if (c->d != llm::kStackHeadDim || c->const_gain <= 0) return false;
+    if (c->Hp / llm::kStepCols > llm::kStackMaxStepsH ||
+        c->Ip / llm::kStepCols > llm::kStackMaxStepsI)
+        return false;
+    const uint32_t nwg = c->ds_nwg[R - 1];
+    const uint32_t nbq = (c->Nqkv + 3) / 4, nbo = (c->H + 3) / 4;
+    if (R * c->Hq > nwg || 2 * nwg < nbq || 2 * nwg < nbo) return false;
+    // the attention of the persistent launch is the split-head path
+    if (pos + R > 4 * llm::kTile) return false;
+    int L = 16;
+    for (int m = 0; m < M_COUNT; m++)
+        L = std::min(L, const_cast<llm_ctx*>(c)->mat(layer, m).L);
+    if (L < 1) return false;
+    *lw = L >= 4 ? 4 : 1;
+    return true;
+}
+
+// Runs the collected decode tasks as one persistent launch.
+int ds_flush(llm_ctx* c) {
+    if (c->ds_pending.empty()) return 0;
+    const uint32_t R = c->ds_rows;
+    llm::StackArgs a{};
+    a.nsteps = (uint32_t)c->ds_pending.size();
+    for (uint32_t k = 0; k < a.nsteps; k++) {
+        const auto& p = c->ds_pending[k];
+        a.steps[k] = {c->pairs[p.in], c->pairs[p.out], p.layer, p.ffn};
+    }
+    a.rows = R;
+    a.pos0 = c->ds_pos;
+    a.H = c->H;
+    a.I = c->I;
+    a.Hp = c->Hp;
+    a.Ip = c->Ip;
+    a.Nqkv = c->Nqkv;
+    for (int m = 0; m < M_COUNT; m++) a.w[m] = c->mat(0, m).d;
+    a.layer_stride = c->ds_layer_stride;
+    a.norms = c->norms;
+    a.gain = c->const_gain;
+    a.L = c->L;
+    a.exp8 = c->exp8;
+    llm::AttnArgs& at = a.at;
+    at.qkv = c->qkv;
+    at.ldqkv = c->Nqkv;
+    at.rope = c->rope;
+    at.kcache = c->kcache;
+    at.vcache = c->vcache;
+    at.tiles = c->tiles;
+    at.pos0 = c->ds_pos;
+    at.num_heads = c->Hq;
+    at.num_kv_heads = c->Hkv;
+    at.group = c->G;
+    at.head_dim = c->d;
+    at.qk_scale = c->qk_scale;
+    at.exp14 = c->exp14;
+    at.out = c->attn;
+    at.ldo = c->Hp;
+    a.kv_layer_stride = (size_t)c->Hkv * c->tiles * llm::kTile * c->d;
+    a.qkv = c->qkv;
+    a.attn = c->attn;
+    a.act = c->act;
+    const auto& last = c->ds_pending.back();
+    a.final_out = last.ffn ? c->xn_final : nullptr;
+    a.sync = c->ds_sync;
+    std::copy(std::begin(c->ds_occ), std::end(c->ds_occ), a.occ);
+    a.start = c->ds_start;
+    a.abort = c->sync + llm::kSyncAbort;
+    a.host_abort = c->host_abort;
+    a.wait_limit = c->wait_limit;
+    {
+        TimedScope ts(c, LLM_K_DECODE_STACK);
+        HIP_TRY(llm::launch_decode_stack(a, c->ds_nwg[R - 1], c->ds_lw, c->stream));
+    }
+    for (const auto& p : c->ds_pending) {
+        if (p.ffn) {
+            c->ds_occ[3]++;
+            c->ds_occ[4]++;
+        } else {
+            c->ds_occ[0]++;
+            c->ds_occ[1]++;
+            c->ds_occ[2]++;
+        }
+    }
+    // the launch writes no normalised side copies but the final norm of
+    // its last FFN sublayer (rows R..7 copied from that sublayer's input)
+    c->attn_cache.pair = c->ffn_cache.pair = -1;
+    c->final_cache.pair = c->final_cache.src = -1;
+    if (last.ffn) c->final_cache = {last.out, last.in, R};
+    c->ds_pending.clear();
+    return 0;
+}
+
+// Collects decode task op (16, 18 or 19) when it can join a persistent
+// launch; returns 1 when it was taken, 0 when the caller runs it itself
+// (after the collected ones), < 0 on error.
+int ds_collect(llm_ctx* c, uint32_t op, uint32_t layer, uint32_t R, uint32_t pos, int in,
+               int out) {
+    int lw = 4;
+    const uint32_t n = op == LLM_OP_DECODER_LAYER ? 2 : 1;
+    if (!ds_eligible(c, R, pos, layer, &lw)) {
+        const int rc = ds_flush(c);
+        return rc < 0 ? rc : 0;
+    }
+    if (!c->ds_pending.empty() &&
+        (R != c->ds_rows || pos != c->ds_pos ||
+         c->ds_pending.size() + n > llm::kStackMaxSteps)) {
+        const int rc = ds_flush(c);
+        if (rc < 0) return rc;
+    }
+    if (c->ds_pending.empty()) {
+        c->ds_rows = R;
+        c->ds_pos = pos;
+        c->ds_lw = 4;
+    }
+    c->ds_lw = std::min(c->ds_lw, lw);
+    if (op == LLM_OP_ATTENTION_SUBLAYER) {
+        c->ds_pending.push_back({layer, in, out, 0});
+    } else if (op == LLM_OP_FFN_SUBLAYER) {
+        c->ds_pending.push_back({layer, in, out, 1});
+    } else {
+        c->ds_pending.push_back({layer, in, out, 0});
+        c->ds_pending.push_back({layer, out, out, 1});
+    }
+    return 1;
+}
+
 }  // namespace
+
+namespace llm {
+// Every entry point that observes or changes device state runs the
+// collected decode tasks first.
+int flush_pending(llm_ctx* c) { return ds_flush(c); }
+}  // namespace llm
+
+#define FLUSH_TRY(c)                                         \
+    do {                                                     \
+        if (int rc_ = ds_flush(c)) return rc_;               \
+    } while (0)
 
 extern "C" {
 
@@ -832,6 +994,31 @@ int llm_ctx_create(const llm_shape_t* shape, int device, uint32_t num_pairs,
     }
     if (fx_recip(fx_sat16((int64_t)c->H * 256)) == 0)
         c->const_gain = fx_rmsnorm_gain(0, c->H);
+    {
+        // persistent decode launches: counters, residency, layer stride
+        if ((rc = dev_alloc(c, (void**)&c->ds_sync, (size_t)llm::kStackSyncWords * 4)))
+            return cleanup(rc);
+        if (const char* e = std::getenv("LLM_ACCEL_STACK")) c->ds_enabled = std::strcmp(e, "1") == 0;
+        if (const char* e = std::getenv("LLM_ACCEL_SYNC_START")) {
+            const uint32_t v = (uint32_t)std::strtoul(e, nullptr, 0);
+            std::vector<uint32_t> init(llm::kStackSyncWords, 0);
+            for (uint32_t l = 0; l < llm::kStackGroups * llm::kStackLines; l++)
+                init[l * llm::kStackStride] = v;
+            if (hipMemcpy(c->ds_sync, init.data(), init.size() * 4, hipMemcpyHostToDevice) !=
+                hipSuccess)
+                return cleanup(fail(LLM_E_HIP, "counter initialisation failed"));
+            c->ds_start = v;
+        }
+        if (d == llm::kStackHeadDim) {
+            c->ds_nwg[0] = llm::stack_workgroups(c->cus, 1);
+            c->ds_nwg[1] = llm::stack_workgroups(c->cus, 2);
+        }
+        c->ds_layer_stride = c->L > 1 ? (size_t)(c->mat(1, 0).d - c->mat(0, 0).d) : 0;
+        for (uint32_t l = 0; l < c->L; l++)
+            for (int m = 0; m < M_COUNT; m++)
+                if (c->mat(l, m).d != c->mat(0, m).d + l * c->ds_layer_stride)
+                    c->ds_enabled = false;
+    }
     *out = c;
     return 0;
 }
@@ -839,6 +1026,7 @@ int llm_ctx_create(const llm_shape_t* shape, int device, uint32_t num_pairs,
 void llm_ctx_destroy(llm_ctx_t* c) {
     if (!c) return;
     (void)hipSetDevice(c->device);
+    (void)ds_flush(c);
     if (c->stream) (void)hipStreamSynchronize(c->stream);
     for (auto e : c->events) (void)hipEventDestroy(e);
     for (auto e : c->ev_pool) (void)hipEventDestroy(e);
@@ -857,6 +1045,7 @@ int llm_load_projection(llm_ctx_t* c, uint32_t layer, uint32_t proj,
     if (!c || !w || layer >= c->L || proj > LLM_PROJ_DOWN)
         return fail(LLM_E_ARG, "bad projection load arguments");
     HIP_TRY(hipSetDevice(c->device));
+    FLUSH_TRY(c);
     int rc;
     switch (proj) {
     case LLM_PROJ_Q:
@@ -928,6 +1117,7 @@ int llm_load_packed_shards(llm_ctx_t* c, const int16_t* const shards[16],
 int llm_load_norms(llm_ctx_t* c, const int16_t* norms) {
     if (!c || !norms) return fail(LLM_E_ARG, "null argument");
     HIP_TRY(hipSetDevice(c->device));
+    FLUSH_TRY(c);
     HIP_TRY(hipMemcpy(c->norms, norms, (size_t)(2 * c->L + 1) * c->H * 2,
                       hipMemcpyHostToDevice));
     c->norms_loaded = true;
@@ -939,6 +1129,7 @@ int llm_hidden_upload(llm_ctx_t* c, uint32_t pair, const int16_t* rows,
     if (!c || !rows || pair >= c->pairs.size() || n > 8)
         return fail(LLM_E_ARG, "bad hidden upload arguments");
     HIP_TRY(hipSetDevice(c->device));
+    FLUSH_TRY(c);
     invalidate_pair(c, (int)pair);
     HIP_TRY(hipMemcpy2DAsync(c->pairs[pair], (size_t)c->Hp * 2, rows,
                              (size_t)c->H * 2, (size_t)c->H * 2, n,
@@ -952,6 +1143,7 @@ int llm_hidden_download(llm_ctx_t* c, uint32_t pair, int16_t* rows,
     if (!c || !rows || pair >= c->pairs.size() || n > 8)
         return fail(LLM_E_ARG, "bad hidden download arguments");
     HIP_TRY(hipSetDevice(c->device));
+    FLUSH_TRY(c);
     HIP_TRY(hipMemcpy2DAsync(rows, (size_t)c->H * 2, c->pairs[pair],
                              (size_t)c->Hp * 2, (size_t)c->H * 2, n,
                              hipMemcpyDeviceToHost, c->stream));
@@ -1012,12 +1204,13 @@ int llm_task(llm_ctx_t* c, uint32_t op, uint32_t layer, uint32_t token_count,
     if (op > LLM_OP_FINAL_NORM) return reject(LLM_STATUS_BAD_OPERATOR);
     if (op == LLM_OP_NOP) return LLM_STATUS_OK;
     if (layer >= c->L) return reject(LLM_STATUS_BAD_LAYER);
-    const int16_t* in = c->pairs[in_pair];
-    int16_t* out = c->pairs[out_pair];
     const int ip = (int)in_pair, opr = (int)out_pair;
     if (hipSetDevice(c->device) != hipSuccess)
         return fail(LLM_E_HIP, "hipSetDevice failed");
     if (op == LLM_OP_FINAL_NORM) {
+        FLUSH_TRY(c);
+        const int16_t* in = c->pairs[in_pair];
+        int16_t* out = c->pairs[out_pair];
         if (token_count == 0) return reject(LLM_STATUS_BAD_TOKEN_COUNT);
         if (!c->norms_loaded) return fail(LLM_E_STATE, "norm table not loaded");
         const auto& fc = c->final_cache;
@@ -1044,6 +1237,12 @@ int llm_task(llm_ctx_t* c, uint32_t op, uint32_t layer, uint32_t token_count,
         int rc = check_layer_loaded(c, layer, op != LLM_OP_FFN_SUBLAYER,
                                     op != LLM_OP_ATTENTION_SUBLAYER);
         if (rc) return rc;
+        rc = ds_collect(c, op, layer, token_count, position, ip, opr);
+        if (rc < 0) return rc;
+        if (rc == 1) {
+            fill_counters(c, op, token_count, position, st);
+            return LLM_STATUS_OK;
+        }
         if (op == LLM_OP_ATTENTION_SUBLAYER) {
             rc = enqueue_attention_sublayer(c, layer, token_count, position, ip, opr);
         } else if (op == LLM_OP_FFN_SUBLAYER) {
@@ -1116,6 +1315,7 @@ int llm_kv_read(llm_ctx_t* c, uint32_t layer, uint32_t h, uint32_t pos0,
     if (!c || layer >= c->L || h >= c->Hkv || pos0 + n > c->max_seq)
         return fail(LLM_E_ARG, "bad KV read arguments");
     HIP_TRY(hipSetDevice(c->device));
+    FLUSH_TRY(c);
     SYNC_TRY(c);
     return kv_transfer(c, layer, h, pos0, n, k, v, false);
 }
@@ -1125,6 +1325,7 @@ int llm_kv_write(llm_ctx_t* c, uint32_t layer, uint32_t h, uint32_t pos0,
     if (!c || layer >= c->L || h >= c->Hkv || pos0 + n > c->max_seq)
         return fail(LLM_E_ARG, "bad KV write arguments");
     HIP_TRY(hipSetDevice(c->device));
+    FLUSH_TRY(c);
     SYNC_TRY(c);
     return kv_transfer(c, layer, h, pos0, n, const_cast<int16_t*>(k),
                        const_cast<int16_t*>(v), true);
@@ -1133,6 +1334,7 @@ int llm_kv_write(llm_ctx_t* c, uint32_t layer, uint32_t h, uint32_t pos0,
 int llm_kv_clear(llm_ctx_t* c) {
     if (!c) return fail(LLM_E_ARG, "null context");
     HIP_TRY(hipSetDevice(c->device));
+    FLUSH_TRY(c);
     const size_t bytes = (size_t)c->L * c->Hkv * c->tiles * 64 * c->d * 2;
     HIP_TRY(hipMemsetAsync(c->kcache, 0, bytes, c->stream));
     HIP_TRY(hipMemsetAsync(c->vcache, 0, bytes, c->stream));
@@ -1142,16 +1344,23 @@ int llm_kv_clear(llm_ctx_t* c) {
 
 void* llm_pair_device_ptr(llm_ctx_t* c, uint32_t pair) {
     if (!c || pair >= c->pairs.size()) return nullptr;
+    if (hipSetDevice(c->device) != hipSuccess || ds_flush(c)) return nullptr;
     invalidate_pair(c, (int)pair);  // the caller may write through it
     c->exported[pair] = 1;          // and keeps using this address
     return c->pairs[pair];
 }
 
-void* llm_stream(llm_ctx_t* c) { return c ? (void*)c->stream : nullptr; }
+void* llm_stream(llm_ctx_t* c) {
+    if (!c) return nullptr;
+    // work collected for a persistent launch goes onto the stream first
+    if (hipSetDevice(c->device) != hipSuccess || ds_flush(c)) return nullptr;
+    return (void*)c->stream;
+}
 
 int llm_sync(llm_ctx_t* c) {
     if (!c) return fail(LLM_E_ARG, "null context");
     HIP_TRY(hipSetDevice(c->device));
+    FLUSH_TRY(c);
     SYNC_TRY(c);
     return 0;
 }
@@ -1159,6 +1368,7 @@ int llm_sync(llm_ctx_t* c) {
 int llm_event_record(llm_ctx_t* c, uint32_t slot) {
     if (!c || slot >= 1024) return fail(LLM_E_ARG, "bad event slot");
     HIP_TRY(hipSetDevice(c->device));
+    FLUSH_TRY(c);
     if (c->events.empty()) {
         c->events.resize(1024);
         for (auto& e : c->events) HIP_TRY(hipEventCreate(&e));
@@ -1178,6 +1388,7 @@ int llm_event_elapsed_ms(llm_ctx_t* c, uint32_t a, uint32_t b, float* ms) {
 int llm_kernel_timing(llm_ctx_t* c, int enable) {
     if (!c) return fail(LLM_E_ARG, "null context");
     HIP_TRY(hipSetDevice(c->device));
+    FLUSH_TRY(c);
     harvest_timing(c);
     for (int k = 0; k < LLM_K_COUNT; k++) c->kernel_ms[k] = 0, c->kernel_n[k] = 0;
     c->timing = enable != 0;
@@ -1188,6 +1399,7 @@ int llm_kernel_stats(llm_ctx_t* c, uint32_t kernel, uint64_t* launches,
                      double* total_ms) {
     if (!c || kernel >= LLM_K_COUNT) return fail(LLM_E_ARG, "bad kernel id");
     HIP_TRY(hipSetDevice(c->device));
+    FLUSH_TRY(c);
     harvest_timing(c);
     if (launches) *launches = c->kernel_n[kernel];
     if (total_ms) *total_ms = c->kernel_ms[kernel];
@@ -1203,6 +1415,7 @@ int llm_bench_projection(llm_ctx_t* c, uint32_t kernel, uint32_t rows,
         kernel != LLM_K_GATEUP && kernel != LLM_K_DOWN)
         return fail(LLM_E_ARG, "not a projection kernel");
     HIP_TRY(hipSetDevice(c->device));
+    FLUSH_TRY(c);
     auto launch = [&](uint32_t layer) -> hipError_t {
         llm::ProjArgs a{};
         a.rows = rows;
@@ -1256,6 +1469,7 @@ int llm_bench_copy(llm_ctx_t* c, uint64_t bytes, uint32_t iters, float* ms) {
     if (!c || !ms || bytes < 16 || iters == 0)
         return fail(LLM_E_ARG, "bad copy arguments");
     HIP_TRY(hipSetDevice(c->device));
+    FLUSH_TRY(c);
     const size_t n16 = bytes / 16;
     void *src = nullptr, *dst = nullptr;
     HIP_TRY(hipMalloc(&src, n16 * 16));
@@ -1349,6 +1563,7 @@ int llm_load_lm_head(llm_ctx_t* c, const int16_t* table, uint32_t vocab) {
         return fail(LLM_E_ARG, "bad LM head arguments");
     if (c->H > 16384) return fail(LLM_E_ARG, "hidden too large for the argmax key");
     HIP_TRY(hipSetDevice(c->device));
+    FLUSH_TRY(c);
     Matrix& m = c->lm;
     const uint32_t n_pad = round_up(vocab, llm::kBlockRows);
     if (!m.d || m.n != vocab) {
@@ -1376,6 +1591,7 @@ int llm_lm_head_argmax(llm_ctx_t* c, uint32_t pair, uint32_t row0, uint32_t rows
         return fail(LLM_E_ARG, "bad LM head argmax arguments");
     if (!c->lm_vocab) return fail(LLM_E_STATE, "LM head not loaded");
     HIP_TRY(hipSetDevice(c->device));
+    FLUSH_TRY(c);
     HIP_TRY(hipMemsetAsync(c->lm_keys, 0, 8 * sizeof(unsigned long long), c->stream));
     HIP_TRY(llm::launch_lm_argmax(c->lm.d, c->lm.steps, c->lm_vocab,
                                   c->pairs[pair] + (size_t)row0 * c->Hp, c->Hp, rows,

@@ -36,7 +36,7 @@ EXPORTS = (
     "llm_generate", "llm_lm_head_argmax_static",
 )
 KERNELS = ("rmsnorm", "qkv", "rope", "attention", "oproj", "gateup", "down",
-           "attn_sublayer")
+           "attn_sublayer", "decode_stack")
 
 
 class Shape(ctypes.Structure):

@@ -21,8 +21,12 @@ def _say(msg):
 
 
 def _accel(spec, layers, max_seq, env):
-    """A context created with `env` set (read once, at creation)."""
+    """A context created with `env` set (read once, at creation).  Decode
+    tasks here take the fused sublayer or the separate launches: the
+    persistent decode launch (tests/test_gpu_stack.py) is switched off."""
     import llm_accel
+    env = dict(env)
+    env.setdefault("LLM_ACCEL_STACK", "0")
     old = {k: os.environ.get(k) for k in env}
     os.environ.update(env)
     try:
