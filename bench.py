@@ -1,20 +1,23 @@
 """Benchmark of the resident decoder-layer path on one MI355X.
 
-Workload: one Qwen2.5-3B-shaped decoder layer
-(hidden 2048, 16 query / 2 KV heads of 128, SwiGLU 11008), P8/G2: one
-8-row prefill block (Task 18 -> 19 -> 20 at position 0) then one
-single-row decode forward (Task 18 -> 19 -> 20 at position 8).  The LM-head
-argmax stays on the host and outside the timed region, as in the
-reference's decode_token_s (host/host_qwen_8x64.cpp:9265-9273).
+Headline: the full 36-layer Qwen2.5-3B-shaped
+model (hidden 2048, 16 query / 2 KV heads of 128, SwiGLU 11008; seeded
+synthetic weights, embedding and LM head), one request P1024/G128 through
+llm_generate: the 1024-token prompt as 128 blocks of 8 rows through every
+layer, then 128 sampled tokens (device LM-head argmax of the last row),
+with a one-row forward through the 36 layers for every token but the
+last.  A step is one such request: W untimed requests, then K timed ones.
+`value` = decode tok/s as the reference defines it (decode_token_s,
+host/host_qwen_8x64.cpp:9265-9273): generated forwards / their time, the
+LM head excluded, aggregated over the K requests; forward times are
+stream-event times (the loop waits only for each token's argmax keys).
 
-A step is one such P8/G2 pass over one layer.  The context holds
-`--copies` distinct weight copies of the layer and step s uses copy
-s % copies, so the streamed working set (8 x 154 MB by default) exceeds
-the 256 MB Infinity Cache and the measured bandwidth is HBM bandwidth.
-The timed region runs the K prefill blocks, then the K decode forwards.
-Inputs (prompt rows, decode row) are resident in HBM before timing.
+Extras: configs[1] (one layer, P8/G2: an 8-row prefill block and a decode
+forward at position 8, over `--copies` weight copies so that the streamed
+working set exceeds the 256 MB Infinity Cache), per-kernel times, the
+configs[3] context sweep and the configs[2] request (2 layers, P16/G8).
 
-Prints one JSON line.  `value` = decode forwards per second of the layer.
+Prints one JSON line.
 """
 import argparse
 import json
@@ -46,7 +49,7 @@ def parse():
     ap.add_argument("--sweep", action=argparse.BooleanOptionalAction, default=True,
                     help="configs[3] decode context sweep (extra field)")
     ap.add_argument("--full", action=argparse.BooleanOptionalAction, default=True,
-                    help="configs[2] and configs[4] request loops (extra fields)")
+                    help="configs[2] request loop (extra field)")
     return ap.parse_args()
 
 
@@ -84,44 +87,45 @@ def load_traffic():
     return None
 
 
-def cpu_baseline(spec, synth, seconds):
-    """The oracle (single thread) on a bounded sample of the same workload:
-    P8 blocks and decode forwards of layer copy 0, for about `seconds`."""
+def cpu_baseline(spec, synth, seconds, layers=36, position=1024):
+    """The oracle (single thread) on a bounded sample of the headline
+    workload: decode forwards (Task 18 / 19 / 20) of one layer at position
+    `position` over a KV cache of `position` seeded positions, for about
+    `seconds`; the model's rate is one over `layers` such forwards."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     from oracle import orc
     from helpers import oracle_from_synthetic, oracle_shape
     orc.lib.orc_set_threads(1)
-    om = oracle_from_synthetic(synth, oracle_shape(spec, layers=1, max_seq=64))
+    om = oracle_from_synthetic(synth, oracle_shape(spec, layers=1,
+                                                   max_seq=position + 64))
     kv = om.new_kv()
-    prompt = synth.hidden_rows(8)
-    row = synth.hidden_rows(9)[8:9]
-    p8_times, dec_times = [], []
+    for h in range(spec.kv_heads):
+        k, v = synth.kv_rows(position, seed_offset=20 + h)
+        kv[0][0, h, :position] = k
+        kv[1][0, h, :position] = v
+    row = synth.hidden_rows(1)
+    times = []
     t_end = time.perf_counter() + seconds
     while True:
         t0 = time.perf_counter()
-        _, x, _ = om.task(kv, 18, 0, prompt, 0)
-        _, x, _ = om.task(kv, 19, 0, x, 0)
-        om.task(kv, 20, 0, x, 0)
+        _, x, _ = om.task(kv, 18, 0, row, position)
+        _, x, _ = om.task(kv, 19, 0, x, position)
+        om.task(kv, 20, 0, x, position)
         t1 = time.perf_counter()
-        _, x, _ = om.task(kv, 18, 0, row, 8)
-        _, x, _ = om.task(kv, 19, 0, x, 8)
-        om.task(kv, 20, 0, x, 8)
-        t2 = time.perf_counter()
-        p8_times.append(t1 - t0)
-        dec_times.append(t2 - t1)
-        if t2 > t_end:
+        times.append(t1 - t0)
+        if t1 > t_end:
             break
-    dec = float(np.mean(dec_times))
+    per_layer = float(np.mean(times))
     return {
-        "value": 1.0 / dec,
-        "unit": "decode tok/s (1 Qwen2.5-3B-shaped layer)",
+        "value": 1.0 / (layers * per_layer),
+        "unit": f"decode tok/s ({layers}-layer Qwen2.5-3B-shaped model)",
         "cores": 1,
         "kind": "port",
-        "sample": (f"{len(dec_times)} x (P8 block + decode forward) of "
-                   f"configs[1] layer copy 0, oracle C restatement, 1 thread "
-                   f"on {cpu_model_name()} ({os.cpu_count()} host threads)"),
-        "p8_block_us": float(np.mean(p8_times)) * 1e6,
-        "decode_forward_us": dec * 1e6,
+        "sample": (f"{len(times)} one-layer decode forwards (Task 18/19/20) at position "
+                   f"{position} over a {position}-position seeded KV cache, oracle C "
+                   f"restatement, 1 thread on {cpu_model_name()} ({os.cpu_count()} host "
+                   f"threads); model rate = 1 / ({layers} x the mean forward)"),
+        "decode_forward_us_per_layer": per_layer * 1e6,
     }
 
 
@@ -172,21 +176,18 @@ def context_sweep(llm_accel, workloads, spec, synth, copies=4):
     return out
 
 
-def request_loop(llm_accel, workloads, spec, layers, prompt_len, gen, emb, lm_head):
+def request_loop(llm_accel, workloads, spec, layers, prompt_len, gen, emb, lm_head,
+                 warmup=1, runs=3):
     """`layers` Qwen2.5-3B-shaped layers
     (seeded synthetic weights, embedding and LM head), the reference's
     generate loop through llm_generate: the prompt in 8-row blocks through
     every layer (Task 18 / 19 per layer, Task 20 after the last block), then
     `gen` sampled tokens, each the device LM-head argmax of the last row
     with a one-row forward for every token but the last; hidden state and
-    KV cache stay in HBM throughout.  decode tok/s = generated forwards /
-    their time, LM head excluded (decode_token_s, host/host_qwen_8x64.cpp
-    :9265-9273); times are host clocks around each forward, as the
-    reference reports them.  The request runs 3 times after a short
-    warm-up one; the figures are those of the run with the median total
-    time (a request occasionally meets a host-side stall of a few ms,
-    which would dominate the 2-layer configs[2])."""
-    runs = 3
+    KV cache stay in HBM throughout.  `warmup` untimed requests, then `runs`
+    timed ones; decode tok/s = generated forwards / their stream-event
+    time over the timed requests, LM head excluded (decode_token_s,
+    host/host_qwen_8x64.cpp:9265-9273)."""
     t0 = time.perf_counter()
     s = workloads.with_layers(spec, layers, max_seq=prompt_len + gen)
     synth = workloads.SyntheticModel(s)
@@ -198,28 +199,43 @@ def request_loop(llm_accel, workloads, spec, layers, prompt_len, gen, emb, lm_he
         del synth
         a.load_lm_head(lm_head)
         setup_s = time.perf_counter() - t0
-        # one short warm-up request (kernels, page tables), then the runs
-        a.generate(emb, prompt[:8], 8, layers, 2)
-        results = sorted((a.generate(emb, prompt, 8, layers, gen) for _ in range(runs)),
-                         key=lambda r: r[1]["total_ms"])
-        toks, st = results[runs // 2]
-        assert all(r[0] == toks for r in results), "runs generated different tokens"
-    dec_ms = st["generated_forward_ms"] / max(st["generated_forward_passes"], 1)
-    blocks = st["prompt_forward_passes"]
+        for _ in range(warmup):
+            a.generate(emb, prompt, 8, layers, gen)
+        a.sync()
+        th0 = time.perf_counter()
+        results = [a.generate(emb, prompt, 8, layers, gen) for _ in range(runs)]
+        a.sync()
+        timed_s = time.perf_counter() - th0
+    toks = results[0][0]
+    assert all(r[0] == toks for r in results), "requests generated different tokens"
+    stats = [r[1] for r in results]
+    passes = sum(st["generated_forward_passes"] for st in stats)
+    fwd_ms = sum(st["generated_forward_ms"] for st in stats)
+    dec_ms = fwd_ms / max(passes, 1)
+    med = sorted(stats, key=lambda st: st["total_ms"])[runs // 2]
+    blocks = med["prompt_forward_passes"]
     kv_bytes = 4 * spec.kv_heads * spec.head_dim * (prompt_len + gen / 2)
     return {
         "workload": f"{layers} layers, P{prompt_len}/G{gen}, 8-row prompt blocks, "
                     "device LM-head argmax",
+        "requests_timed": runs,
+        "requests_warmup": warmup,
+        "timed_s": timed_s,
         "decode_tok_s": 1e3 / dec_ms,
         "decode_forward_ms": dec_ms,
         "decode_hbm_frac": layers * (layer_bytes(spec) + kv_bytes) / (dec_ms * 1e-3)
                            / 1e9 / HBM_PEAK_GBS,
-        "prompt_ms": st["prompt_forward_ms"],
-        "p8_block_us_per_layer": st["prompt_forward_ms"] * 1e3 / (blocks * layers),
-        "time_to_first_token_ms": st["time_to_first_token_ms"],
-        "lm_head_ms_per_token": st["lm_head_ms"] / max(st["generated_tokens"], 1),
-        "total_ms": st["total_ms"],
-        "coarse_tasks": st["coarse_task_count"],
+        "decode_wall_tok_s": sum(st["generated_tokens"] - 1 for st in stats)
+                             / max(sum(st["generated_wall_ms"] for st in stats), 1e-9) * 1e3,
+        "prompt_ms": med["prompt_forward_ms"],
+        "p8_block_us_per_layer": med["prompt_forward_ms"] * 1e3 / (blocks * layers),
+        "time_to_first_token_ms": med["time_to_first_token_ms"],
+        "lm_head_ms_per_token": med["lm_head_ms"] / max(med["generated_tokens"], 1),
+        "request_ms": float(np.mean([st["total_ms"] for st in stats])),
+        "coarse_tasks": med["coarse_task_count"],
+        "input_migrations": med["input_migrations"],
+        "output_migrations": med["output_migrations"],
+        "kv_migrations": med["kv_migrations"],
         "first_tokens": toks[:4],
         "setup_s": round(setup_s, 1),
     }
@@ -314,17 +330,16 @@ def main():
     copy_gbs = 2 * copy_bytes / copy_ms / 1e6
     acc.close()
     sweep = context_sweep(llm_accel, workloads, spec, synth) if args.sweep else None
-    full = None
-    if args.full:
-        # seeded embedding table and LM head [151936][2048], shared by both
-        tables = workloads.SyntheticModel(workloads.with_layers(spec, 0))
-        emb, lm_head = tables.embedding(), tables.lm_head()
-        full = {
-            "configs[2]": request_loop(llm_accel, workloads, spec, 2, 16, 8, emb, lm_head),
-            "configs[4]": request_loop(llm_accel, workloads, spec, 36, 1024, 128,
-                                       emb, lm_head),
-        }
-        del emb, lm_head
+    # seeded embedding table and LM head [151936][2048], shared by the
+    # request loops
+    tables = workloads.SyntheticModel(workloads.with_layers(spec, 0))
+    emb, lm_head = tables.embedding(), tables.lm_head()
+    c2 = (request_loop(llm_accel, workloads, spec, 2, 16, 8, emb, lm_head)
+          if args.full else None)
+    # the headline: W untimed and K timed configs[4] requests
+    c4 = request_loop(llm_accel, workloads, spec, 36, 1024, 128, emb, lm_head,
+                      warmup=args.warmup, runs=K)
+    del emb, lm_head
 
     lb = layer_bytes(spec)
     gu_bytes = gateup_bytes(spec, 1)
@@ -332,37 +347,48 @@ def main():
     traffic = load_traffic()
     out = {
         "metric": METRIC,
-        "value": 1e6 / dec_us,
-        "unit": "decode tok/s (1 Qwen2.5-3B-shaped layer)",
+        "value": c4["decode_tok_s"],
+        "unit": "decode tok/s (36-layer Qwen2.5-3B-shaped model, P1024/G128)",
         "n_gpus": 1,
         "steps": K,
         "warmup": args.warmup,
-        "ms_per_step": total_ms / K,
+        "ms_per_step": c4["request_ms"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int16",
         "data": "synthetic",
         "config": {
-            "workload": ("configs[1]: one Qwen2.5-3B-shaped decoder layer "
-                         "(H 2048, 16/2 heads x 128, I 11008), P8/G2 = one "
-                         "8-row prefill block + one decode forward, Task "
-                         "18/19/20, host LM head excluded"),
-            "layer_copies": C,
+            "workload": ("configs[4]: 36 Qwen2.5-3B-shaped decoder layers (H 2048, "
+                         "16/2 heads x 128, I 11008), one request P1024/G128 per "
+                         "step: 128 8-row prompt blocks, 128 sampled tokens (device "
+                         "LM-head argmax, excluded from the rate), Task 18/19/20"),
+            "layers": 36,
             "weight_bytes_per_layer": lb,
             "seed": workloads.SEED,
         },
-        "p8_block_us": p8_us,
-        "decode_forward_us": dec_us,
-        "decode_hbm_frac": lb / (dec_us * 1e-6) / 1e9 / HBM_PEAK_GBS,
-        "p8_hbm_frac": lb / (p8_us * 1e-6) / 1e9 / HBM_PEAK_GBS,
-        "host_wall_ms_per_step": (t_host1 - t_host0) * 1e3 / K,
-        "decode_forward_with_host_io_us": dec_io_us,
-        "kernel_us_decode": {k: round(v[1], 3) for k, v in kdec.items()},
-        "kernel_us_p8": {k: round(v[1], 3) for k, v in kp8.items()},
+        "decode_forward_ms": c4["decode_forward_ms"],
+        "decode_hbm_frac": c4["decode_hbm_frac"],
+        "decode_wall_tok_s": c4["decode_wall_tok_s"],
+        "configs[4]": c4,
+        "configs[1]": {
+            "workload": ("one Qwen2.5-3B-shaped layer, P8/G2: an 8-row prefill "
+                         "block and a decode forward at position 8, Task 18/19/20, "
+                         f"K={K} of each over {C} layer copies"),
+            "decode_tok_s": 1e6 / dec_us,
+            "p8_block_us": p8_us,
+            "decode_forward_us": dec_us,
+            "decode_hbm_frac": lb / (dec_us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+            "p8_hbm_frac": lb / (p8_us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+            "ms_per_pass": total_ms / K,
+            "host_wall_ms_per_pass": (t_host1 - t_host0) * 1e3 / K,
+            "decode_forward_with_host_io_us": dec_io_us,
+            "kernel_us_decode": {k: round(v[1], 3) for k, v in kdec.items()},
+            "kernel_us_p8": {k: round(v[1], 3) for k, v in kp8.items()},
+        },
         "copy_kernel_gbs": copy_gbs,
         "decode_forward_us_by_context": sweep,
-        "request_loops": full,
+        "configs[2]": c2,
         "roofline": {
             "kernel": "proj_kernel<1,*,EPI_SILU> (gate|up + SiLU*up, decode row)",
             "bound": "hbm",
@@ -377,6 +403,7 @@ def main():
     }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(spec, synth, args.cpu_seconds)
+        out["cpu_baseline"]["gpu_over_cpu"] = out["value"] / out["cpu_baseline"]["value"]
     print(json.dumps(out), flush=True)
 
 

@@ -245,7 +245,10 @@ int llm_lm_head_argmax_static(const int16_t* table, uint32_t vocab,
                               uint32_t* tokens, int64_t* scores, void* stream);
 
 /* Report of llm_generate (the QWEN_8X64_E2E_PROFILE fields of the
- * reference's generate mode, host/host_qwen_8x64.cpp:9264-9336). */
+ * reference's generate mode, host/host_qwen_8x64.cpp:9264-9336).  Forward
+ * and LM-head times are stream-event times on the device (a forward from
+ * before its rows' copy to after its last task); the generate loop waits
+ * only for each sampled token's argmax keys. */
 typedef struct {
     uint32_t prompt_tokens;
     uint32_t generated_tokens;
@@ -255,12 +258,34 @@ typedef struct {
     uint32_t output_materializations;
     uint32_t released_prompt_blocks;
     uint32_t reserved0;
-    double prompt_forward_ms;
-    double time_to_first_token_ms;
-    double generated_forward_ms;
-    double lm_head_ms;
-    double total_ms;
+    double prompt_forward_ms;         /* all prompt blocks */
+    double time_to_first_token_ms;    /* host clock, call to first token */
+    double generated_forward_ms;      /* sum over the sampled tokens' forwards */
+    double lm_head_ms;                /* sum over the argmax launches */
+    double total_ms;                  /* host clock of the call */
+    double generated_wall_ms;         /* host clock from the first token to the
+                                         last (the generated forwards and their
+                                         argmaxes) */
+    /* Residency (tests/test_coarse_task_residency_contract.sh:63-80 of the
+     * reference): host -> device copies of hidden rows (one per forward),
+     * device -> host copies of hidden rows (0: the argmax runs on the
+     * device and returns 8-byte keys), KV transfers (0), key read-backs
+     * (one per sampled token). */
+    uint32_t input_migrations;
+    uint32_t output_migrations;
+    uint32_t kv_migrations;
+    uint32_t argmax_readbacks;
 } llm_generate_stats_t;
+
+/* Line sink of the request loop.  With a sink set, llm_generate brackets
+ * every task with stream events, synchronises after every forward and
+ * passes the reference's report lines (host/host_qwen_8x64.cpp:1342-1352,
+ * :7684-7711, :7885-7909, :9264-9336): COARSE_TASK_PROGRESS per task,
+ * COARSE_TASK_PREFILL_BLOCK per prompt block, COARSE_TASK_STACK per
+ * sampled-token forward and one QWEN_8X64_E2E_PROFILE line, key=value
+ * fields separated by spaces.  NULL removes the sink. */
+typedef void (*llm_log_fn)(const char* line, void* user);
+int llm_set_log(llm_ctx_t* ctx, llm_log_fn fn, void* user);
 
 /* The reference's generate loop with coarse tasks (host/host_qwen_8x64.cpp
  * :9016-9136 with run_prompt_block :7840-7884 and run_token :7665-7712):

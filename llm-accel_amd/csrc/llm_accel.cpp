@@ -195,6 +195,21 @@ struct llm_ctx {
     uint32_t lm_vocab = 0;
     unsigned long long* lm_keys = nullptr;
 
+    // Request loop (llm_generate): pinned staging of the embedding rows of
+    // one request (copied to the device asynchronously, one forward's
+    // rows at a time), pinned argmax keys, stream events, the optional line
+    // sink, and counts of host <-> device transfers over the context's life.
+    int16_t* stage = nullptr;
+    size_t stage_rows = 0;
+    unsigned long long* keys_host = nullptr;
+    std::vector<hipEvent_t> gen_events;
+    llm_log_fn log_fn = nullptr;
+    void* log_user = nullptr;
+    uint64_t n_h2d_rows = 0;   // hidden-row uploads (calls)
+    uint64_t n_d2h_rows = 0;   // hidden-row downloads (calls)
+    uint64_t n_kv_moves = 0;   // KV reads / writes (calls)
+    uint64_t n_argmax = 0;     // argmax key read-backs (calls)
+
     Matrix& mat(uint32_t layer, int m) { return mats[layer * M_COUNT + m]; }
 };
 
@@ -1036,6 +1051,9 @@ void llm_ctx_destroy(llm_ctx_t* c) {
     }
     for (void* p : c->allocations) (void)hipFree(p);
     if (c->host_abort) (void)hipHostFree(c->host_abort);
+    if (c->stage) (void)hipHostFree(c->stage);
+    if (c->keys_host) (void)hipHostFree(c->keys_host);
+    for (auto e : c->gen_events) (void)hipEventDestroy(e);
     if (c->stream) (void)hipStreamDestroy(c->stream);
     delete c;
 }
@@ -1134,6 +1152,7 @@ int llm_hidden_upload(llm_ctx_t* c, uint32_t pair, const int16_t* rows,
     HIP_TRY(hipMemcpy2DAsync(c->pairs[pair], (size_t)c->Hp * 2, rows,
                              (size_t)c->H * 2, (size_t)c->H * 2, n,
                              hipMemcpyHostToDevice, c->stream));
+    c->n_h2d_rows++;
     SYNC_TRY(c);
     return 0;
 }
@@ -1147,6 +1166,7 @@ int llm_hidden_download(llm_ctx_t* c, uint32_t pair, int16_t* rows,
     HIP_TRY(hipMemcpy2DAsync(rows, (size_t)c->H * 2, c->pairs[pair],
                              (size_t)c->Hp * 2, (size_t)c->H * 2, n,
                              hipMemcpyDeviceToHost, c->stream));
+    c->n_d2h_rows++;
     SYNC_TRY(c);
     return 0;
 }
@@ -1317,6 +1337,7 @@ int llm_kv_read(llm_ctx_t* c, uint32_t layer, uint32_t h, uint32_t pos0,
     HIP_TRY(hipSetDevice(c->device));
     FLUSH_TRY(c);
     SYNC_TRY(c);
+    c->n_kv_moves++;
     return kv_transfer(c, layer, h, pos0, n, k, v, false);
 }
 
@@ -1327,6 +1348,7 @@ int llm_kv_write(llm_ctx_t* c, uint32_t layer, uint32_t h, uint32_t pos0,
     HIP_TRY(hipSetDevice(c->device));
     FLUSH_TRY(c);
     SYNC_TRY(c);
+    c->n_kv_moves++;
     return kv_transfer(c, layer, h, pos0, n, const_cast<int16_t*>(k),
                        const_cast<int16_t*>(v), true);
 }
@@ -1522,20 +1544,57 @@ double ms_since(std::chrono::steady_clock::time_point t) {
                std::chrono::steady_clock::now() - t).count();
 }
 
-// One materialised forward of `rows` rows at `position` through layers
-// [0, layer_count): embedding rows into pair 1, Task 18 (1 -> 0) and 19
-// (0 -> 1) per layer, Task 20 (1 -> 0) when `final_norm`
-// (run_composed_decoder_stack, host/host_qwen_8x64.cpp:1258-1445).
-int run_stack(llm_ctx_t* c, const int16_t* embedding, const uint32_t* tokens,
-              uint32_t rows, uint32_t position, uint32_t layer_count,
-              bool final_norm, uint32_t* tasks) {
-    std::vector<int16_t> hidden((size_t)rows * c->H);
-    for (uint32_t r = 0; r < rows; r++)
-        std::memcpy(&hidden[(size_t)r * c->H], embedding + (size_t)tokens[r] * c->H,
-                    (size_t)c->H * 2);
-    int rc = llm_hidden_upload(c, 1, hidden.data(), rows);
-    if (rc) return rc;
+// Stream events of the request loop: at least n of them.
+int gen_events(llm_ctx* c, size_t n) {
+    while (c->gen_events.size() < n) {
+        hipEvent_t e;
+        HIP_TRY(hipEventCreate(&e));
+        c->gen_events.push_back(e);
+    }
+    return 0;
+}
+
+float event_ms(hipEvent_t a, hipEvent_t b) {
+    float ms = 0;
+    return hipEventElapsedTime(&ms, a, b) == hipSuccess ? ms : 0.0f;
+}
+
+void emit(llm_ctx* c, const std::string& line) {
+    if (c->log_fn) c->log_fn(line.c_str(), c->log_user);
+}
+
+std::string fmt_ms(double v) {
+    char b[32];
+    std::snprintf(b, sizeof b, "%.6f", v);
+    return b;
+}
+
+// One forward of `rows` rows at `position` through layers [0, layer_count)
+// (run_composed_decoder_stack, host/host_qwen_8x64.cpp:1258-1445): the
+// rows (pinned host memory) into pair 1 by an asynchronous copy, Task 18
+// (1 -> 0) and 19 (0 -> 1) per layer, Task 20 (1 -> 0) when `final_norm`.
+// Nothing is waited for, unless a line sink is set: then the forward is
+// bracketed by stream events per task, synchronised, and reported as the
+// reference reports its coarse tasks (COARSE_TASK_PROGRESS per task, then
+// one COARSE_TASK_PREFILL_BLOCK or COARSE_TASK_STACK line).
+int run_stack(llm_ctx_t* c, const int16_t* rows_host, uint32_t rows, uint32_t position,
+              uint32_t layer_count, bool final_norm, bool prompt_block,
+              uint32_t* tasks) {
+    if (int rc = ds_flush(c)) return rc;  // pending tasks may read pair 1
+    const bool prof = c->log_fn != nullptr;
+    const uint32_t ntask = 2 * layer_count + (final_norm ? 1u : 0u);
+    if (prof) {
+        if (int rc = gen_events(c, 2 + ntask)) return rc;
+        HIP_TRY(hipEventRecord(c->gen_events[0], c->stream));
+    }
+    const auto host0 = std::chrono::steady_clock::now();
+    invalidate_pair(c, 1);
+    HIP_TRY(hipMemcpy2DAsync(c->pairs[1], (size_t)c->Hp * 2, rows_host, (size_t)c->H * 2,
+                             (size_t)c->H * 2, rows, hipMemcpyHostToDevice, c->stream));
+    c->n_h2d_rows++;
+    if (prof) HIP_TRY(hipEventRecord(c->gen_events[1], c->stream));
     llm_status_t st;
+    uint32_t done = 0;
     auto task = [&](uint32_t op, uint32_t layer, uint32_t in, uint32_t out) {
         const int r = llm_task(c, op, layer, rows, position, 0, in, out, &st);
         if (r < 0) return r;
@@ -1544,14 +1603,83 @@ int run_stack(llm_ctx_t* c, const int16_t* embedding, const uint32_t* tokens,
                                          std::to_string(op) + " code " +
                                          std::to_string(st.code));
         (*tasks)++;
+        if (prof) {
+            if (int rc = ds_flush(c)) return rc;
+            HIP_TRY(hipEventRecord(c->gen_events[2 + done], c->stream));
+        }
+        done++;
         return 0;
     };
+    int rc;
     for (uint32_t layer = 0; layer < layer_count; layer++) {
         if ((rc = task(LLM_OP_ATTENTION_SUBLAYER, layer, 1, 0))) return rc;
         if ((rc = task(LLM_OP_FFN_SUBLAYER, layer, 0, 1))) return rc;
     }
     if (final_norm && (rc = task(LLM_OP_FINAL_NORM, 0, 1, 0))) return rc;
-    return llm_sync(c);
+    if (!prof) return 0;
+    SYNC_TRY(c);
+    const double host_ms = ms_since(host0);
+    double phase_ms[3] = {0, 0, 0};  // attention, FFN, final norm
+    for (uint32_t k = 0; k < ntask; k++) {
+        const bool fin = final_norm && k + 1 == ntask;
+        const uint32_t ph = fin ? 2 : k % 2;
+        const double ms = event_ms(c->gen_events[1 + k], c->gen_events[2 + k]);
+        phase_ms[ph] += ms;
+        static const char* names[3] = {"attention", "ffn", "final_norm"};
+        static const uint32_t ops[3] = {LLM_OP_ATTENTION_SUBLAYER, LLM_OP_FFN_SUBLAYER,
+                                        LLM_OP_FINAL_NORM};
+        emit(c, "COARSE_TASK_PROGRESS completed=" + std::to_string(k + 1) +
+                    " total=" + std::to_string(ntask) + " op=" + std::to_string(ops[ph]) +
+                    " phase=" + names[ph] + " layer=" + std::to_string(fin ? 0 : k / 2) +
+                    " position=" + std::to_string(position) +
+                    " query_tokens=" + std::to_string(rows) + " controller_ms=" + fmt_ms(ms));
+    }
+    const double input_ms = event_ms(c->gen_events[0], c->gen_events[1]);
+    const double active_ms = event_ms(c->gen_events[1], c->gen_events[1 + ntask]);
+    std::string line =
+        std::string(prompt_block ? "COARSE_TASK_PREFILL_BLOCK" : "COARSE_TASK_STACK") +
+        " layers=" + std::to_string(layer_count) + " tasks=" + std::to_string(ntask);
+    if (prompt_block)
+        line += " position_begin=" + std::to_string(position) +
+                " query_tokens=" + std::to_string(rows) +
+                " position_end=" + std::to_string(position + rows - 1);
+    else
+        line += " position=" + std::to_string(position);
+    line += " event_timing_domain=hip_stream_event attention_controller_ms=" +
+            fmt_ms(phase_ms[0]) + " ffn_controller_ms=" + fmt_ms(phase_ms[1]) +
+            " final_norm_controller_ms=" + fmt_ms(phase_ms[2]) +
+            " kernel_active_ms=" + fmt_ms(active_ms) + " input_migration_ms=" +
+            fmt_ms(input_ms) +
+            " auxiliary_migration_ms=0 status_kernel_ms=0 status_migration_ms=0"
+            " output_migration_ms=0 profiled_sequence_ms=" +
+            fmt_ms(input_ms + active_ms) + " host_elapsed_ms=" + fmt_ms(host_ms);
+    if (prompt_block) line += std::string(" output_materialized=") + (final_norm ? "1" : "0");
+    line += " intermediate_host_copy=0";
+    if (prompt_block) line += " kv_cache_owner=device";
+    emit(c, line);
+    return 0;
+}
+
+// The LM-head argmax of rows [row0, row0 + rows) of `pair` enqueued, its
+// keys copied into pinned host memory; the caller synchronises.
+int ensure_keys_host(llm_ctx_t* c) {
+    if (!c->keys_host &&
+        hipHostMalloc((void**)&c->keys_host, 8 * sizeof(unsigned long long),
+                      hipHostMallocDefault) != hipSuccess)
+        return fail(LLM_E_NOMEM, "hipHostMalloc failed");
+    return 0;
+}
+
+int enqueue_argmax(llm_ctx_t* c, uint32_t pair, uint32_t row0, uint32_t rows) {
+    if (int rc = ds_flush(c)) return rc;
+    HIP_TRY(hipMemsetAsync(c->lm_keys, 0, 8 * sizeof(unsigned long long), c->stream));
+    HIP_TRY(llm::launch_lm_argmax(c->lm.d, c->lm.steps, c->lm_vocab,
+                                  c->pairs[pair] + (size_t)row0 * c->Hp, c->Hp, rows,
+                                  c->lm.L, c->lm_keys, c->stream));
+    HIP_TRY(hipMemcpyAsync(c->keys_host, c->lm_keys, rows * sizeof(unsigned long long),
+                           hipMemcpyDeviceToHost, c->stream));
+    c->n_argmax++;
+    return 0;
 }
 
 }  // namespace
@@ -1592,17 +1720,12 @@ int llm_lm_head_argmax(llm_ctx_t* c, uint32_t pair, uint32_t row0, uint32_t rows
     if (!c->lm_vocab) return fail(LLM_E_STATE, "LM head not loaded");
     HIP_TRY(hipSetDevice(c->device));
     FLUSH_TRY(c);
-    HIP_TRY(hipMemsetAsync(c->lm_keys, 0, 8 * sizeof(unsigned long long), c->stream));
-    HIP_TRY(llm::launch_lm_argmax(c->lm.d, c->lm.steps, c->lm_vocab,
-                                  c->pairs[pair] + (size_t)row0 * c->Hp, c->Hp, rows,
-                                  c->lm.L, c->lm_keys, c->stream));
-    unsigned long long keys[8];
-    HIP_TRY(hipMemcpyAsync(keys, c->lm_keys, rows * sizeof(unsigned long long),
-                           hipMemcpyDeviceToHost, c->stream));
+    if (int rc = ensure_keys_host(c)) return rc;
+    if (int rc = enqueue_argmax(c, pair, row0, rows)) return rc;
     SYNC_TRY(c);
     for (uint32_t r = 0; r < rows; r++) {
-        tokens[r] = key_token(keys[r]);
-        if (scores) scores[r] = key_score(keys[r]);
+        tokens[r] = key_token(c->keys_host[r]);
+        if (scores) scores[r] = key_score(c->keys_host[r]);
     }
     return 0;
 }
@@ -1621,49 +1744,133 @@ int llm_generate(llm_ctx_t* c, const int16_t* embedding, uint32_t vocab,
         return fail(LLM_E_ARG, "sequence exceeds max_seq_len");
     for (uint32_t t = 0; t < n_prompt; t++)
         if (prompt[t] >= vocab) return fail(LLM_E_ARG, "prompt token outside the vocabulary");
+    HIP_TRY(hipSetDevice(c->device));
+    FLUSH_TRY(c);
     llm_generate_stats_t local{};
     llm_generate_stats_t& S = stats ? *stats : local;
     S = llm_generate_stats_t{};
     S.prompt_tokens = n_prompt;
     S.generated_tokens = max_new_tokens;
     const auto begin = std::chrono::steady_clock::now();
+    // Embedding rows of the whole request in pinned memory (the prompt's
+    // now, each sampled token's when it is known): every forward's rows
+    // travel by an asynchronous copy, and nothing waits between forwards
+    // but the argmax read-back each sampled token needs.
+    const size_t need = (size_t)n_prompt + max_new_tokens;
+    if (c->stage_rows < need) {
+        if (c->stage) (void)hipHostFree(c->stage);
+        c->stage = nullptr;
+        c->stage_rows = 0;
+        if (hipHostMalloc((void**)&c->stage, need * c->H * sizeof(int16_t),
+                          hipHostMallocDefault) != hipSuccess)
+            return fail(LLM_E_NOMEM, "hipHostMalloc failed");
+        c->stage_rows = need;
+    }
+    if (int rc = ensure_keys_host(c)) return rc;
+    if (int rc = gen_events(c, 2 + 2 * (size_t)layer_count + 1 + 5)) return rc;
+    const size_t ne = c->gen_events.size();
+    hipEvent_t ev_p0 = c->gen_events[ne - 5], ev_p1 = c->gen_events[ne - 4],
+               ev_a = c->gen_events[ne - 3], ev_b = c->gen_events[ne - 2],
+               ev_l = c->gen_events[ne - 1];
+    for (uint32_t t = 0; t < n_prompt; t++)
+        std::memcpy(c->stage + (size_t)t * c->H, embedding + (size_t)prompt[t] * c->H,
+                    (size_t)c->H * 2);
+    const uint64_t h2d0 = c->n_h2d_rows, d2h0 = c->n_d2h_rows, kv0 = c->n_kv_moves,
+                   am0 = c->n_argmax;
     uint32_t last_row = 0;
     int rc;
     // prompt blocks (host/host_qwen_8x64.cpp:9016-9060, :7840-7884)
+    HIP_TRY(hipEventRecord(ev_p0, c->stream));
     for (uint32_t b0 = 0; b0 < n_prompt; b0 += block_size) {
         const uint32_t rows = std::min(block_size, n_prompt - b0);
         const bool final_block = b0 + rows == n_prompt;
-        const auto t = std::chrono::steady_clock::now();
-        if ((rc = run_stack(c, embedding, prompt + b0, rows, b0, layer_count,
-                            final_block, &S.coarse_task_count)))
+        if ((rc = run_stack(c, c->stage + (size_t)b0 * c->H, rows, b0, layer_count,
+                            final_block, true, &S.coarse_task_count)))
             return rc;
-        S.prompt_forward_ms += ms_since(t);
         S.prompt_forward_passes++;
         if (final_block) S.output_materializations++;
         else S.released_prompt_blocks++;
         last_row = rows - 1;
     }
-    // sampled tokens (host/host_qwen_8x64.cpp:9091-9136)
+    HIP_TRY(hipEventRecord(ev_p1, c->stream));
+    if (max_new_tokens == 0) {
+        SYNC_TRY(c);
+        S.prompt_forward_ms = event_ms(ev_p0, ev_p1);
+    }
+    // sampled tokens (host/host_qwen_8x64.cpp:9091-9136); times from stream
+    // events: a forward from before its rows' copy to after its last task,
+    // the LM head from there to its keys' copy
+    auto gen0 = std::chrono::steady_clock::now();
     uint32_t token = 0;
     for (uint32_t step = 0; step < max_new_tokens; step++) {
-        const auto t = std::chrono::steady_clock::now();
-        if ((rc = llm_lm_head_argmax(c, 0, last_row, 1, &token, nullptr))) return rc;
-        S.lm_head_ms += ms_since(t);
+        if ((rc = enqueue_argmax(c, 0, last_row, 1))) return rc;
+        HIP_TRY(hipEventRecord(ev_l, c->stream));
+        SYNC_TRY(c);
+        token = key_token(c->keys_host[0]);
+        if (step == 0) {
+            S.prompt_forward_ms = event_ms(ev_p0, ev_p1);
+            S.lm_head_ms += event_ms(ev_p1, ev_l);
+            S.time_to_first_token_ms = ms_since(begin);
+            gen0 = std::chrono::steady_clock::now();  // the generated forwards from here
+        } else {
+            S.generated_forward_ms += event_ms(ev_a, ev_b);
+            S.lm_head_ms += event_ms(ev_b, ev_l);
+        }
         out_tokens[step] = token;
-        if (step == 0) S.time_to_first_token_ms = ms_since(begin);
         if (step + 1 < max_new_tokens) {
             if (token >= vocab) return fail(LLM_E_STATE, "sampled token outside the embedding");
-            const auto f = std::chrono::steady_clock::now();
-            if ((rc = run_stack(c, embedding, &token, 1, n_prompt + step, layer_count,
-                                true, &S.coarse_task_count)))
+            int16_t* row = c->stage + ((size_t)n_prompt + step) * c->H;
+            std::memcpy(row, embedding + (size_t)token * c->H, (size_t)c->H * 2);
+            HIP_TRY(hipEventRecord(ev_a, c->stream));
+            if ((rc = run_stack(c, row, 1, n_prompt + step, layer_count, true, false,
+                                &S.coarse_task_count)))
                 return rc;
-            S.generated_forward_ms += ms_since(f);
+            HIP_TRY(hipEventRecord(ev_b, c->stream));
             S.generated_forward_passes++;
             S.output_materializations++;
             last_row = 0;
         }
     }
+    S.generated_wall_ms = max_new_tokens > 1 ? ms_since(gen0) : 0.0;
     S.total_ms = ms_since(begin);
+    S.input_migrations = (uint32_t)(c->n_h2d_rows - h2d0);
+    S.output_migrations = (uint32_t)(c->n_d2h_rows - d2h0);
+    S.kv_migrations = (uint32_t)(c->n_kv_moves - kv0);
+    S.argmax_readbacks = (uint32_t)(c->n_argmax - am0);
+    if (c->log_fn) {
+        const double mean_ms =
+            S.generated_forward_passes ? S.generated_forward_ms / S.generated_forward_passes : 0;
+        const double dec = S.generated_forward_ms > 0
+                               ? 1000.0 * S.generated_forward_passes / S.generated_forward_ms : 0;
+        const double pre = S.prompt_forward_ms > 0 ? 1000.0 * n_prompt / S.prompt_forward_ms : 0;
+        emit(c, "QWEN_8X64_E2E_PROFILE prompt_tokens=" + std::to_string(n_prompt) +
+                    " generated_tokens=" + std::to_string(max_new_tokens) +
+                    " prompt_forward_passes=" + std::to_string(S.prompt_forward_passes) +
+                    " generated_forward_passes=" + std::to_string(S.generated_forward_passes) +
+                    " prefill_mode=coarse_block prefill_block_size=" +
+                    std::to_string(block_size) + " prompt_forward_ms=" +
+                    fmt_ms(S.prompt_forward_ms) + " prefill_token_s=" + fmt_ms(pre) +
+                    " time_to_first_token_ms=" + fmt_ms(S.time_to_first_token_ms) +
+                    " generated_forward_ms=" + fmt_ms(S.generated_forward_ms) +
+                    " mean_inter_token_ms=" + fmt_ms(mean_ms) + " decode_token_s=" +
+                    fmt_ms(dec) + " lm_head_host_ms=" + fmt_ms(S.lm_head_ms) +
+                    " total_host_elapsed_ms=" + fmt_ms(S.total_ms) +
+                    " event_timing_domain=hip_stream_event coarse_task_count=" +
+                    std::to_string(S.coarse_task_count) +
+                    " output_materializations=" + std::to_string(S.output_materializations) +
+                    " released_prompt_blocks=" + std::to_string(S.released_prompt_blocks) +
+                    " input_migrations=" + std::to_string(S.input_migrations) +
+                    " output_migrations=" + std::to_string(S.output_migrations) +
+                    " kv_migrations=" + std::to_string(S.kv_migrations) +
+                    " intermediate_host_copy=0 kv_cache_owner=device PASS");
+    }
+    return 0;
+}
+
+int llm_set_log(llm_ctx_t* c, llm_log_fn fn, void* user) {
+    if (!c) return fail(LLM_E_ARG, "null context");
+    c->log_fn = fn;
+    c->log_user = user;
     return 0;
 }
 

@@ -33,7 +33,7 @@ EXPORTS = (
     "llm_event_record", "llm_event_elapsed_ms", "llm_exp_tables",
     "llm_kernel_timing", "llm_kernel_stats", "llm_bench_copy",
     "llm_bench_projection", "llm_load_lm_head", "llm_lm_head_argmax",
-    "llm_generate", "llm_lm_head_argmax_static",
+    "llm_generate", "llm_lm_head_argmax_static", "llm_set_log",
 )
 KERNELS = ("rmsnorm", "qkv", "rope", "attention", "oproj", "gateup", "down",
            "attn_sublayer", "decode_stack")
@@ -73,7 +73,11 @@ class GenerateStats(ctypes.Structure):
         "output_materializations", "released_prompt_blocks", "reserved0")] + [
             (n, ctypes.c_double) for n in (
                 "prompt_forward_ms", "time_to_first_token_ms",
-                "generated_forward_ms", "lm_head_ms", "total_ms")]
+                "generated_forward_ms", "lm_head_ms", "total_ms",
+                "generated_wall_ms")] + [
+            (n, ctypes.c_uint32) for n in (
+                "input_migrations", "output_migrations", "kv_migrations",
+                "argmax_readbacks")]
 
     def as_dict(self):
         return {n: getattr(self, n) for n, _ in self._fields_ if n != "reserved0"}
@@ -81,6 +85,10 @@ class GenerateStats(ctypes.Structure):
 
 class AccelError(RuntimeError):
     pass
+
+
+# void (*)(const char* line, void* user)
+LOG_FN = ctypes.CFUNCTYPE(None, ctypes.c_char_p, ctypes.c_void_p)
 
 
 def load_library(path=LIB_PATH):
@@ -138,6 +146,7 @@ def load_library(path=LIB_PATH):
                                         ctypes.POINTER(GenerateStats)]),
         "llm_lm_head_argmax_static": (ctypes.c_int, [vp, _u32, _u32, vp, _u32,
                                                      _u32, vp, vp, vp]),
+        "llm_set_log": (ctypes.c_int, [vp, LOG_FN, vp]),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)
@@ -271,15 +280,26 @@ class Accelerator:
                                              scores), "llm_lm_head_argmax")
         return list(toks), list(scores)
 
-    def generate(self, embedding, prompt, block_size, layer_count, max_new_tokens):
+    def generate(self, embedding, prompt, block_size, layer_count, max_new_tokens,
+                 log=None):
+        """llm_generate; `log`, a list, receives the report lines (the
+        forwards are then synchronised one by one)."""
         embedding = np.ascontiguousarray(embedding, np.int16)
         prompt_arr = (ctypes.c_uint32 * len(prompt))(*prompt)
         out = (ctypes.c_uint32 * max(max_new_tokens, 1))()
         st = GenerateStats()
-        self._check(lib().llm_generate(self._ctx, _p16(embedding), embedding.shape[0],
-                                       prompt_arr, len(prompt), block_size,
-                                       layer_count, max_new_tokens, out,
-                                       ctypes.byref(st)), "llm_generate")
+        sink = None
+        if log is not None:
+            sink = LOG_FN(lambda line, _user: log.append(line.decode()))
+            self._check(lib().llm_set_log(self._ctx, sink, None), "llm_set_log")
+        try:
+            self._check(lib().llm_generate(self._ctx, _p16(embedding), embedding.shape[0],
+                                           prompt_arr, len(prompt), block_size,
+                                           layer_count, max_new_tokens, out,
+                                           ctypes.byref(st)), "llm_generate")
+        finally:
+            if sink is not None:
+                lib().llm_set_log(self._ctx, LOG_FN(), None)
         return list(out)[:max_new_tokens], st.as_dict()
 
     # --- tasks ------------------------------------------------------------

@@ -107,6 +107,95 @@ def test_generate_matches_oracle_replay():
     assert st["prompt_forward_passes"] == 2 and st["released_prompt_blocks"] == 1
     assert st["generated_forward_passes"] == G - 1
     assert st["output_materializations"] == G
+    # residency: one hidden-row upload per forward, no hidden-row download,
+    # no KV transfer, one 8-byte key read-back per sampled token
+    assert st["input_migrations"] == 2 + (G - 1)
+    assert st["output_migrations"] == 0 and st["kv_migrations"] == 0
+    assert st["argmax_readbacks"] == G
+    assert st["prompt_forward_ms"] > 0 and st["generated_forward_ms"] > 0
+
+
+def _kv(line):
+    head, *fields = line.split()
+    return head, dict(f.split("=", 1) for f in fields if "=" in f)
+
+
+def test_generate_report_lines_and_residency_contract():
+    """The report lines of the reference's coarse-task generate mode
+    (host/host_qwen_8x64.cpp:1342-1352, :7684-7711, :7885-7909, :9264-9336)
+    and its residency contract (tests/test_coarse_task_residency_contract.sh
+    :63-80): Task 18 output consumed in HBM by Task 19, one input migration
+    per block, the final output materialised only when asked, no KV
+    migration.  Tokens are the same with the line sink (synchronised
+    forwards) as without it."""
+    import llm_accel
+    spec = workloads.CONFIG_A
+    layers = 2
+    synth = workloads.SyntheticModel(spec, layers=layers)
+    emb = synth.embedding()
+    prompt = [int(t) for t in synth.tokens(21)]
+    G, B = 5, 8
+    log = []
+    with llm_accel.Accelerator(accel_shape(spec, layers=layers, max_seq=64)) as a:
+        a.load_model(synth)
+        a.load_lm_head(emb)
+        _say("case generate report lines P21/G5 B8")
+        toks_plain, st_plain = a.generate(emb, prompt, B, layers, G)
+        a.kv_clear()
+        toks, st = a.generate(emb, prompt, B, layers, G, log=log)
+        a.kv_clear()
+        toks_again, _ = a.generate(emb, prompt, B, layers, G)
+    assert toks == toks_plain == toks_again
+    blocks = 3
+    ntask = 2 * layers
+    parsed = [_kv(line) for line in log]
+    heads = [h for h, _ in parsed]
+    # per prompt block: its tasks' progress lines, then the block line
+    n_progress = blocks * ntask + 1 + (G - 1) * (ntask + 1)
+    assert heads.count("COARSE_TASK_PROGRESS") == n_progress
+    assert heads.count("COARSE_TASK_PREFILL_BLOCK") == blocks
+    assert heads.count("COARSE_TASK_STACK") == G - 1
+    assert heads[-1] == "QWEN_8X64_E2E_PROFILE" and log[-1].endswith(" PASS")
+    pre = [f for h, f in parsed if h == "COARSE_TASK_PREFILL_BLOCK"]
+    assert [int(f["position_begin"]) for f in pre] == [0, 8, 16]
+    assert [int(f["query_tokens"]) for f in pre] == [8, 8, 5]
+    assert [int(f["position_end"]) for f in pre] == [7, 15, 20]
+    assert [f["output_materialized"] for f in pre] == ["0", "0", "1"]
+    assert [int(f["tasks"]) for f in pre] == [ntask, ntask, ntask + 1]
+    for f in pre:
+        assert f["intermediate_host_copy"] == "0" and f["kv_cache_owner"] == "device"
+        assert float(f["kernel_active_ms"]) > 0
+        assert float(f["input_migration_ms"]) >= 0
+        assert float(f["output_migration_ms"]) == 0
+    stack = [f for h, f in parsed if h == "COARSE_TASK_STACK"]
+    assert [int(f["position"]) for f in stack] == [21 + i for i in range(G - 1)]
+    assert all(int(f["tasks"]) == ntask + 1 for f in stack)
+    prog = [f for h, f in parsed if h == "COARSE_TASK_PROGRESS"]
+    # the first block: T18/T19 per layer, in order
+    first = prog[:ntask]
+    assert [int(f["completed"]) for f in first] == list(range(1, ntask + 1))
+    assert all(int(f["total"]) == ntask for f in first)
+    assert [f["phase"] for f in first] == ["attention", "ffn"] * layers
+    assert [int(f["op"]) for f in first] == [18, 19] * layers
+    assert [int(f["layer"]) for f in first] == [l for l in range(layers) for _ in (0, 1)]
+    assert prog[2 * ntask + ntask]["phase"] == "final_norm"
+    _, prof = parsed[-1]
+    assert int(prof["prompt_tokens"]) == 21 and int(prof["generated_tokens"]) == G
+    assert int(prof["prompt_forward_passes"]) == blocks
+    assert int(prof["generated_forward_passes"]) == G - 1
+    assert prof["prefill_mode"] == "coarse_block" and int(prof["prefill_block_size"]) == B
+    assert int(prof["coarse_task_count"]) == st["coarse_task_count"]
+    assert int(prof["released_prompt_blocks"]) == blocks - 1
+    assert int(prof["input_migrations"]) == blocks + G - 1
+    assert int(prof["output_migrations"]) == 0 and int(prof["kv_migrations"]) == 0
+    assert prof["intermediate_host_copy"] == "0" and prof["kv_cache_owner"] == "device"
+    assert float(prof["decode_token_s"]) > 0
+    for key in ("prompt_forward_ms", "prefill_token_s", "time_to_first_token_ms",
+                "generated_forward_ms", "mean_inter_token_ms", "lm_head_host_ms",
+                "total_host_elapsed_ms"):
+        assert float(prof[key]) >= 0, key
+    assert st["input_migrations"] == blocks + G - 1
+    assert st["output_migrations"] == 0 and st["kv_migrations"] == 0
 
 
 @pytest.fixture(scope="module")
