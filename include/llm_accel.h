@@ -133,6 +133,21 @@ int llm_load_projection(llm_ctx_t* ctx, uint32_t layer, uint32_t proj,
  * covering every layer's 16x16 tiles. */
 int llm_load_packed_shards(llm_ctx_t* ctx, const int16_t* const shards[16],
                            uint64_t shard_words);
+/* A packed Fix16 checkpoint directory (model_data_t::load,
+ * host/host_qwen_8x64.cpp:736-840): layer_weights_shard00..15.fix16.bin
+ * (the llm_load_packed_shards layout, weight_shard_words 64-byte words
+ * each for the context's num_layers), norm_weights.fix16.bin
+ * ((2L+1)*hidden int16), token_embedding.fix16.bin (vocab*hidden int16,
+ * read into `embedding`, host memory of the caller, when not NULL) and,
+ * unless LLM_CKPT_TIE_EMBEDDINGS (the embedding is then the LM head),
+ * lm_head.fix16.bin into the LM head when present.  Every file must have
+ * exactly its expected size ("<what> size mismatch: <path> expected=N
+ * actual=M", LLM_E_ARG; sizes are all checked before anything loads);
+ * with LLM_CKPT_REQUIRE_LM_HEAD a missing, untied LM head is an error. */
+#define LLM_CKPT_TIE_EMBEDDINGS 1u
+#define LLM_CKPT_REQUIRE_LM_HEAD 2u
+int llm_load_checkpoint_dir(llm_ctx_t* ctx, const char* dir, uint32_t flags,
+                            int16_t* embedding);
 /* Norm table, [(2*num_layers + 1)][hidden] Q8.8: rows 2l (attention),
  * 2l+1 (FFN), 2L (final) (include/control_cache_8x64.hpp:111-123). */
 int llm_load_norms(llm_ctx_t* ctx, const int16_t* norms);

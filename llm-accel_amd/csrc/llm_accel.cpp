@@ -1132,6 +1132,114 @@ int llm_load_packed_shards(llm_ctx_t* c, const int16_t* const shards[16],
     return 0;
 }
 
+// Bytes of the file at `path`, or -1 when it cannot be opened.
+static long long file_bytes(const std::string& path) {
+    FILE* f = std::fopen(path.c_str(), "rb");
+    if (!f) return -1;
+    long long n = -1;
+    if (std::fseek(f, 0, SEEK_END) == 0) n = std::ftell(f);
+    std::fclose(f);
+    return n;
+}
+
+// The whole file into dst, which must be exactly `bytes` long
+// (load_exact_file, host/host_qwen_8x64.cpp:736-763).
+static int load_exact(const std::string& path, void* dst, size_t bytes, const char* what) {
+    const long long actual = file_bytes(path);
+    if (actual != (long long)bytes)
+        return fail(LLM_E_ARG, std::string(what) + " size mismatch: " + path +
+                                   " expected=" + std::to_string(bytes) +
+                                   " actual=" + std::to_string(actual < 0 ? 0 : actual));
+    FILE* f = std::fopen(path.c_str(), "rb");
+    if (!f) return fail(LLM_E_ARG, "failed to read " + path);
+    const size_t got = std::fread(dst, 1, bytes, f);
+    std::fclose(f);
+    if (got != bytes) return fail(LLM_E_ARG, "failed to read " + path);
+    return 0;
+}
+
+int llm_load_checkpoint_dir(llm_ctx_t* c, const char* dir, uint32_t flags,
+                            int16_t* embedding) {
+    if (!c || !dir) return fail(LLM_E_ARG, "null argument");
+    if (flags & ~(uint32_t)(LLM_CKPT_TIE_EMBEDDINGS | LLM_CKPT_REQUIRE_LM_HEAD))
+        return fail(LLM_E_ARG, "unknown checkpoint flags");
+    const std::string d(dir);
+    const size_t vocab = c->s.vocab_size, emb_vals = vocab * c->H;
+    const size_t norm_vals = (size_t)(2 * c->L + 1) * c->H;
+    // weight_shard_words (host/host_qwen_8x64.cpp:165-187): 16x16 tiles of
+    // every projection of every layer, two tiles per 64-byte word
+    uint64_t layer_tiles = 0;
+    for (uint32_t p = 0; p < 7; p++) {
+        const uint32_t K = p == LLM_PROJ_DOWN ? c->I : c->H;
+        const uint32_t N = (p == LLM_PROJ_K || p == LLM_PROJ_V) ? c->Ckv
+                         : (p == LLM_PROJ_GATE || p == LLM_PROJ_UP) ? c->I : c->H;
+        layer_tiles += cdiv(N, 16) * cdiv(K, 16);
+    }
+    const uint64_t shard_words = cdiv((uint64_t)c->L * layer_tiles, 2);
+    const bool tie = flags & LLM_CKPT_TIE_EMBEDDINGS;
+    // every size first, in the reference's order (embedding, norms, shards,
+    // LM head), so that a bad directory loads nothing
+    std::vector<std::string> shard_paths(16);
+    for (int i = 0; i < 16; i++) {
+        char name[64];
+        std::snprintf(name, sizeof name, "/layer_weights_shard%02d.fix16.bin", i);
+        shard_paths[i] = d + name;
+    }
+    const std::string emb_path = d + "/token_embedding.fix16.bin";
+    const std::string norm_path = d + "/norm_weights.fix16.bin";
+    const std::string lm_path = d + "/lm_head.fix16.bin";
+    auto check = [&](const std::string& path, size_t bytes, const char* what) {
+        const long long actual = file_bytes(path);
+        if (actual == (long long)bytes) return 0;
+        return fail(LLM_E_ARG, std::string(what) + " size mismatch: " + path +
+                                   " expected=" + std::to_string(bytes) +
+                                   " actual=" + std::to_string(actual < 0 ? 0 : actual));
+    };
+    int rc;
+    if ((rc = check(emb_path, emb_vals * 2, "embedding"))) return rc;
+    if ((rc = check(norm_path, norm_vals * 2, "norm weights"))) return rc;
+    for (int i = 0; i < 16; i++)
+        if ((rc = check(shard_paths[i], shard_words * 64, "weight shard"))) return rc;
+    const bool have_lm = !tie && file_bytes(lm_path) >= 0;
+    if (have_lm && (rc = check(lm_path, emb_vals * 2, "LM head"))) return rc;
+    if (!tie && !have_lm && (flags & LLM_CKPT_REQUIRE_LM_HEAD))
+        return fail(LLM_E_ARG, "generate mode requires lm_head.fix16.bin or tied embeddings");
+    HIP_TRY(hipSetDevice(c->device));
+    FLUSH_TRY(c);
+    {
+        std::vector<int16_t> norms(norm_vals);
+        if ((rc = load_exact(norm_path, norms.data(), norm_vals * 2, "norm weights")) ||
+            (rc = llm_load_norms(c, norms.data())))
+            return rc;
+    }
+    {
+        std::vector<std::vector<int16_t>> shards(16);
+        const int16_t* ptrs[16];
+        for (int i = 0; i < 16; i++) {
+            shards[i].resize((size_t)shard_words * 32);
+            if ((rc = load_exact(shard_paths[i], shards[i].data(), shard_words * 64,
+                                 "weight shard")))
+                return rc;
+            ptrs[i] = shards[i].data();
+        }
+        if ((rc = llm_load_packed_shards(c, ptrs, shard_words))) return rc;
+    }
+    std::vector<int16_t> own;
+    int16_t* emb = embedding;
+    if (!emb && tie) {
+        own.resize(emb_vals);
+        emb = own.data();
+    }
+    if (emb && (rc = load_exact(emb_path, emb, emb_vals * 2, "embedding"))) return rc;
+    if (tie) return llm_load_lm_head(c, emb, (uint32_t)vocab);
+    if (have_lm) {
+        std::vector<int16_t> lm(emb_vals);
+        if ((rc = load_exact(lm_path, lm.data(), emb_vals * 2, "LM head"))) return rc;
+        return llm_load_lm_head(c, lm.data(), (uint32_t)vocab);
+    }
+    return 0;
+}
+
 int llm_load_norms(llm_ctx_t* c, const int16_t* norms) {
     if (!c || !norms) return fail(LLM_E_ARG, "null argument");
     HIP_TRY(hipSetDevice(c->device));

@@ -34,7 +34,10 @@ EXPORTS = (
     "llm_kernel_timing", "llm_kernel_stats", "llm_bench_copy",
     "llm_bench_projection", "llm_load_lm_head", "llm_lm_head_argmax",
     "llm_generate", "llm_lm_head_argmax_static", "llm_set_log",
+    "llm_load_checkpoint_dir",
 )
+CKPT_TIE_EMBEDDINGS = 1
+CKPT_REQUIRE_LM_HEAD = 2
 KERNELS = ("rmsnorm", "qkv", "rope", "attention", "oproj", "gateup", "down",
            "attn_sublayer", "decode_stack")
 
@@ -147,6 +150,7 @@ def load_library(path=LIB_PATH):
         "llm_lm_head_argmax_static": (ctypes.c_int, [vp, _u32, _u32, vp, _u32,
                                                      _u32, vp, vp, vp]),
         "llm_set_log": (ctypes.c_int, [vp, LOG_FN, vp]),
+        "llm_load_checkpoint_dir": (ctypes.c_int, [vp, ctypes.c_char_p, _u32, _i16p]),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)
@@ -268,6 +272,20 @@ class Accelerator:
         return port0, port1
 
     # --- LM head and generation ------------------------------------------
+    def load_checkpoint_dir(self, path, tie_embeddings=False, require_lm_head=False,
+                            want_embedding=True):
+        """llm_load_checkpoint_dir; returns the token embedding [vocab][hidden]
+        (or None when not wanted)."""
+        emb = None
+        if want_embedding:
+            emb = np.zeros((self.shape.vocab_size, self.shape.hidden_size), np.int16)
+        flags = (CKPT_TIE_EMBEDDINGS if tie_embeddings else 0) | \
+                (CKPT_REQUIRE_LM_HEAD if require_lm_head else 0)
+        self._check(lib().llm_load_checkpoint_dir(
+            self._ctx, os.fsencode(path), flags,
+            _p16(emb) if emb is not None else None), "llm_load_checkpoint_dir")
+        return emb
+
     def load_lm_head(self, table):
         table = np.ascontiguousarray(table, np.int16)
         self._check(lib().llm_load_lm_head(self._ctx, _p16(table), table.shape[0]),

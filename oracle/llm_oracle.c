@@ -50,6 +50,14 @@ static inline int16_t sat16(int64_t v) {
 /* golden_weight_t(golden_fm_t x): Q8.8 -> Q4.12, exact shift, saturating
  * at +-8 (host:3251-3252, :3706-3708). */
 static inline int32_t fm_to_wt(int16_t x) { return sat16((int32_t)x * 16); }
+/* One attention product term: a Q8.8 value times golden_weight_t of a
+ * Q8.8 value, AP_RND-narrowed to Q16.16 (host:3251-3256 for QK, the raw
+ * payload PV of :3706-3712): the term every QK and raw-payload PV bank
+ * adds. */
+static inline int32_t fm_wt_term(int16_t a, int16_t b) {
+    return (int32_t)rnd64((int64_t)a * fm_to_wt(b), 4);
+}
+int32_t orc_fm_wt_term(int16_t a, int16_t b) { return fm_wt_term(a, b); }
 /* golden_clamp (host:523-535) on raw Q8.8. */
 static inline int16_t clamp16(int16_t v, int16_t lo, int16_t hi) {
     return v < lo ? lo : (v > hi ? hi : v);
@@ -296,8 +304,7 @@ void orc_qk_scores(const int16_t* q, uint32_t G, uint32_t d,
         for (uint32_t p = 0; p < n; p++) {
             int32_t banks[4] = {0, 0, 0, 0};
             for (uint32_t e = 0; e < d; e++) {
-                int32_t w = fm_to_wt(k[(size_t)p * d + e]);
-                int32_t prod = (int32_t)rnd64((int64_t)q[r * d + e] * w, 4);
+                int32_t prod = fm_wt_term(q[r * d + e], k[(size_t)p * d + e]);
                 banks[e & 3] = sat32((int64_t)banks[e & 3] + prod);
             }
             int32_t total = sat32((int64_t)banks[0] + banks[1] +
@@ -360,12 +367,12 @@ void orc_attention(const int16_t* q, uint32_t G, uint32_t d,
             for (uint32_t e = 0; e < d; e++) {
                 int32_t banks[4] = {0, 0, 0, 0};
                 for (uint32_t p = 0; p < tl; p++) {
-                    int32_t w = fm_to_wt(v[(size_t)(tb + p) * d + e]);
-                    int64_t pw = (int64_t)prob[r * tl + p] * w;
+                    const int16_t vv = v[(size_t)(tb + p) * d + e];
                     /* raw payload / legacy: Q8.8 x Q4.12 (20 fb);
                      * direct: Q2.14 x Q4.12 (26 fb) -> Q16.16 */
-                    int32_t prod = (int32_t)(semantics == 1 ? rnd64(pw, 10)
-                                                            : rnd64(pw, 4));
+                    int32_t prod = semantics == 1
+                        ? (int32_t)rnd64((int64_t)prob[r * tl + p] * fm_to_wt(vv), 10)
+                        : fm_wt_term(prob[r * tl + p], vv);
                     banks[p & 3] = sat32((int64_t)banks[p & 3] + prod);
                 }
                 int32_t total = sat32((int64_t)banks[0] + banks[1] +
@@ -373,7 +380,7 @@ void orc_attention(const int16_t* q, uint32_t G, uint32_t d,
                 if (semantics == 0) /* x accum(fm(1/64)) = raw 4<<8 */
                     total = sat32(rnd64((int64_t)total * 1024, 16));
                 int16_t tv = sat16(rnd64(total, 8));
-                acc[r * d + e] = sat32((int64_t)acc[r * d + e] + ((int32_t)tv << 8));
+                acc[r * d + e] = sat32((int64_t)acc[r * d + e] + (int64_t)tv * 256);
             }
         }
     }

@@ -89,6 +89,8 @@ int16_t orc_rsqrt(int32_t v);          /* golden_rsqrt host:621-656   */
 int16_t orc_silu(int16_t x);           /* golden_silu  host:658-668   */
 int16_t orc_quantize_fix16(double v);  /* quantize_fix16 host:496-505 */
 int16_t orc_inv_sum(int32_t sum);      /* fm(accum(1)/max(sum,2^-12)) */
+/* rnd(a * golden_weight_t(b), 4): one QK / raw-payload PV product term */
+int32_t orc_fm_wt_term(int16_t a, int16_t b);
 
 /* ---- vector / matrix ops -------------------------------------------- */
 /* golden_projection (host:3105-3142); w row-major [out_dim][in_dim]. */

@@ -65,6 +65,7 @@ def _load():
         "orc_silu": (ctypes.c_int16, [ctypes.c_int16]),
         "orc_quantize_fix16": (ctypes.c_int16, [ctypes.c_double]),
         "orc_inv_sum": (ctypes.c_int16, [ctypes.c_int32]),
+        "orc_fm_wt_term": (ctypes.c_int32, [ctypes.c_int16, ctypes.c_int16]),
         "orc_projection": (None, [_i16p, _u32, _u32, _i16p, _u32, _i16p]),
         "orc_residual": (None, [_i16p, _i16p, ctypes.c_size_t, _i16p]),
         "orc_rmsnorm": (None, [_i16p, _u32, _u32, _i16p, _i16p]),
