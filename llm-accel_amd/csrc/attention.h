@@ -31,6 +31,7 @@ struct AttnArgs {
     int32_t* s_tsum;      // [8][kv_heads][max_tiles][group]
     int16_t* s_tval;      // [8][kv_heads][max_tiles][group][head_dim]
     uint32_t grid_rows, grid_tiles;  // tile path: rows and tiles of the launch
+    uint32_t use_gqa;     // long contexts take the GQA tile path when it applies
     uint32_t* counters;   // zero between launches: chunked path [8][kv_heads];
                           // tile path kCounterStride words apart, per (row,
                           // query head) 1 + tile_groups(max_tiles) of them
@@ -57,6 +58,12 @@ constexpr size_t counter_words(uint32_t num_heads, uint32_t tiles) {
 
 // Tiles per split-path workgroup: at most kMaxChunkTiles.
 constexpr uint32_t kMaxChunkTiles = 8;
+
+// Long contexts with the query heads of a GQA group sharing each K / V
+// page (attention_gqa.hip): head_dim 64 or 128, at most 8 query heads per
+// KV head, at most 1024 tiles.
+bool attention_gqa_ok(const AttnArgs& a, uint32_t rows);
+hipError_t launch_attention_gqa(const AttnArgs& a, uint32_t rows, hipStream_t st);
 
 // chunks = max over active rows of ceil(tiles / chunk_tiles); 1 selects
 // the fused single-workgroup path.

@@ -1417,6 +1417,8 @@ template <int D>
 static hipError_t launch_d(const AttnArgs& a, uint32_t rows, uint32_t kv_heads,
                            uint32_t chunks, hipStream_t st) {
     const uint32_t tiles = (a.pos0 + rows + TILE - 1) / TILE;
+    if (tiles > kSplitHeadMaxTiles && a.use_gqa && attention_gqa_ok(a, rows))
+        return launch_attention_gqa(a, rows, st);
     if (D % 32 == 0 && tiles > kSplitHeadMaxTiles) {
         constexpr int DT = D % 32 == 0 ? D : 32;
         AttnArgs g = a;

@@ -133,6 +133,11 @@ struct llm_ctx {
     uint32_t* sync = nullptr;
     uint32_t* host_abort = nullptr;
     bool fused = true;                 // LLM_ACCEL_FUSED=0 disables it
+    bool gqa = true;                   // GQA tile path; LLM_ACCEL_GQA=0 disables it
+    // contexts of at least this many tiles take the GQA tile path (shorter
+    // ones run faster with a workgroup per query head and tile);
+    // LLM_ACCEL_GQA_MIN_TILES overrides it
+    uint32_t gqa_min_tiles = 96;
     uint32_t sync_qkv[32] = {};        // QKV arrivals per line so far, mod 2^32
     uint32_t sync_attn = 0;            // attention arrivals per line, mod 2^32
     // bound of one wait (100 MHz ticks); LLM_ACCEL_WAIT_LIMIT overrides it
@@ -523,6 +528,7 @@ int enqueue_attention_sublayer(llm_ctx* c, uint32_t layer, uint32_t R,
     at.out = c->attn;
     at.ldo = c->Hp;
     at.chunk_tiles = c->chunk_tiles;
+    at.use_gqa = c->gqa && (uint32_t)cdiv(pos + R, llm::kTile) >= c->gqa_min_tiles ? 1u : 0u;
     at.max_tiles = c->tiles;
     at.s_scores = c->s_scores;
     at.s_tmax = c->s_tmax;
@@ -960,6 +966,9 @@ int llm_ctx_create(const llm_shape_t* shape, int device, uint32_t num_pairs,
         return cleanup(fail(LLM_E_NOMEM, "hipHostMalloc failed"));
     *c->host_abort = 0;
     if (const char* e = std::getenv("LLM_ACCEL_FUSED")) c->fused = std::strcmp(e, "0") != 0;
+    if (const char* e = std::getenv("LLM_ACCEL_GQA")) c->gqa = std::strcmp(e, "0") != 0;
+    if (const char* e = std::getenv("LLM_ACCEL_GQA_MIN_TILES"))
+        c->gqa_min_tiles = (uint32_t)std::strtoul(e, nullptr, 10);
     if (hipDeviceGetAttribute(&c->cus, hipDeviceAttributeMultiprocessorCount, c->device) !=
         hipSuccess)
         return cleanup(fail(LLM_E_HIP, "device attribute query failed"));

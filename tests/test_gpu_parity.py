@@ -379,6 +379,74 @@ def test_accumulator_saturation_over_long_context():
     assert first_mismatch(got, want) is None
 
 
+@pytest.mark.parametrize("n,period", [(16384, 1), (16384, 10), (4096, 3)])
+def test_running_max_rises_often(n, period):
+    """K rows of tile j are a fixed +-8 raw pattern times 1 + j // period:
+    for query heads whose score along the pattern is positive the tile
+    maxima rise every `period` tiles (257 rises at period 1 -- the tile-by-
+    tile recurrence -- and about 26 at period 10, each a separate run of
+    the parallel one), up to K values past the Q4.12 bound (the saturation
+    correction); decode row and KV against the oracle."""
+    import llm_accel
+    spec = workloads.CONFIG_B
+    synth = workloads.SyntheticModel(spec, layers=1)
+    om = oracle_from_synthetic(synth, oracle_shape(spec, layers=1, max_seq=n + 64))
+    kc, vc = om.new_kv()
+    rng = np.random.default_rng(9000 + period)
+    x = synth.hidden_rows(1, seed_offset=51)
+    with llm_accel.Accelerator(accel_shape(spec, layers=1, max_seq=n + 64)) as a:
+        a.load_model(synth)
+        for h in range(spec.kv_heads):
+            u = rng.choice(np.array([-8, 8], np.int16), spec.head_dim)
+            step = 1 + (np.arange(n) // 64) // period
+            k = np.clip(step[:, None].astype(np.int64) * u[None, :], -32768, 32767)
+            k = k.astype(np.int16)
+            _, v = synth.kv_rows(n, seed_offset=60 + h)
+            kc[0, h, :n], vc[0, h, :n] = k, v
+            a.kv_write(0, h, 0, k, v)
+        a.upload(2, x)
+        _say(f"case running max rises n={n} period={period}")
+        rc, _ = a.task(18, 0, 1, n, 2, 0)
+        assert rc == 0
+        got = a.download(0, 1)
+        kv_got = [a.kv_read(0, h, n, 1) for h in range(spec.kv_heads)]
+    code, want, _ = om.task((kc, vc), 18, 0, x, n)
+    assert code == 0
+    err = first_mismatch(got, want)
+    assert err is None, err
+    for h in range(spec.kv_heads):
+        assert first_mismatch(kv_got[h][0], kc[0, h, n:n + 1]) is None
+        assert first_mismatch(kv_got[h][1], vc[0, h, n:n + 1]) is None
+
+
+@pytest.fixture
+def gqa_everywhere(monkeypatch):
+    """Contexts of 5 tiles and more take the GQA tile path (by default it
+    starts at 96 tiles, where it overtakes the per-head path)."""
+    monkeypatch.setenv("LLM_ACCEL_GQA_MIN_TILES", "5")
+
+
+@pytest.mark.parametrize("cfg,n,rows", [("B", 1020, 8), ("A", 317, 5), ("B", 319, 1),
+                                         ("A", 382, 1), ("B", 255, 2)])
+def test_gqa_path_block_across_tile_boundary(gqa_everywhere, cfg, n, rows):
+    """The GQA tile path (head_dim 128 and 64) on blocks that straddle a
+    tile boundary after a preloaded context."""
+    test_block_across_tile_boundary_late_context(cfg, n, rows)
+
+
+@pytest.mark.parametrize("cfg,n", [("B", 700), ("A", 700)])
+def test_gqa_path_saturation(gqa_everywhere, cfg, n):
+    test_saturation_only_outside_first_word(cfg, n)
+
+
+def test_gqa_path_saturating_kv(gqa_everywhere):
+    test_saturating_kv_takes_exact_path(700)
+
+
+def test_gqa_path_running_max_rises(gqa_everywhere):
+    test_running_max_rises_often(4096, 3)
+
+
 def test_norm_cache_invalidation():
     # T18 writes pair 0 and derives its FFN norm; uploading new rows into
     # pair 0 before T19 must discard that copy.  T19 into pair 1 derives the
