@@ -50,6 +50,12 @@ def parse():
                     help="configs[3] decode context sweep (extra field)")
     ap.add_argument("--full", action=argparse.BooleanOptionalAction, default=True,
                     help="configs[2] request loop (extra field)")
+    ap.add_argument("--part", choices=("all", "configs1", "sweep", "configs4"),
+                    default="all",
+                    help="run one part alone and print its figures (for profiling); "
+                         "the default runs every part and prints the headline line")
+    ap.add_argument("--sweep-n", type=int, nargs="*", default=[128, 1024, 4096, 16384],
+                    help="context lengths of the configs[3] sweep")
     return ap.parse_args()
 
 
@@ -141,7 +147,8 @@ def load_copies(acc, synth, copies):
                                    synth.norms()[2:3]]))
 
 
-def context_sweep(llm_accel, workloads, spec, synth, copies=4):
+def context_sweep(llm_accel, workloads, spec, synth, copies=4,
+                  lengths=(128, 1024, 4096, 16384)):
     """one layer, K/V preloaded with seeded Q8.8
     N(0, 0.3) to n positions, one decode forward (T18/T19/T20) at position
     n.  The context holds `copies` copies of the layer, each with its own
@@ -149,7 +156,7 @@ def context_sweep(llm_accel, workloads, spec, synth, copies=4):
     finds its weights and K/V evicted by the others (4 x (154 MB + K/V) >
     the 256 MB Infinity Cache) without a flush kernel's dirty lines being
     written back during it; median of 8 forwards after 4 warm-up ones."""
-    nmax = 16384
+    nmax = max(lengths)
     shape = llm_accel.Shape(spec.vocab, spec.hidden, spec.inter, copies, spec.heads,
                             spec.kv_heads, nmax + 64, 1e6)
     out = {}
@@ -160,7 +167,7 @@ def context_sweep(llm_accel, workloads, spec, synth, copies=4):
             for c in range(copies):
                 a.kv_write(c, h, 0, k, v)
         a.upload(3, synth.hidden_rows(1))
-        for n in (128, 1024, 4096, 16384):
+        for n in lengths:
             times = []
             for rep in range(12):
                 layer = rep % copies
@@ -253,6 +260,17 @@ def main():
     spec = workloads.CONFIG_B
     C = args.copies
     synth = workloads.SyntheticModel(spec, layers=1)
+    if args.part == "sweep":
+        print(json.dumps({"part": "sweep", "decode_forward_us_by_context":
+                          context_sweep(llm_accel, workloads, spec, synth,
+                                        lengths=tuple(args.sweep_n))}), flush=True)
+        return
+    if args.part == "configs4":
+        tables = workloads.SyntheticModel(workloads.with_layers(spec, 0))
+        c4 = request_loop(llm_accel, workloads, spec, 36, 1024, 128, tables.embedding(),
+                          tables.lm_head(), warmup=args.warmup, runs=args.steps)
+        print(json.dumps({"part": "configs4", "configs[4]": c4}), flush=True)
+        return
     shape = llm_accel.Shape(spec.vocab, spec.hidden, spec.inter, C, spec.heads,
                             spec.kv_heads, 64, 1e6)
     acc = llm_accel.Accelerator(shape, num_pairs=4)
@@ -329,7 +347,14 @@ def main():
     copy_ms = acc.bench_copy(copy_bytes, 20)
     copy_gbs = 2 * copy_bytes / copy_ms / 1e6
     acc.close()
-    sweep = context_sweep(llm_accel, workloads, spec, synth) if args.sweep else None
+    if args.part == "configs1":
+        print(json.dumps({"part": "configs1", "decode_forward_us": dec_us, "p8_block_us": p8_us,
+                          "kernel_us_decode": {k: round(v[1], 3) for k, v in kdec.items()},
+                          "kernel_us_p8": {k: round(v[1], 3) for k, v in kp8.items()},
+                          "gateup_launch_us": gu_us}), flush=True)
+        return
+    sweep = (context_sweep(llm_accel, workloads, spec, synth, lengths=tuple(args.sweep_n))
+             if args.sweep else None)
     # seeded embedding table and LM head [151936][2048], shared by the
     # request loops
     tables = workloads.SyntheticModel(workloads.with_layers(spec, 0))

@@ -13,8 +13,8 @@
 //       running max after the tile (the maximum of the tile maxima up to
 //       it), their sum and the rounded PV value of every element; the V row
 //       is appended;
-//   (3) scan: one workgroup per (row, query head) runs the per-tile
-//       rounding recurrence.  The running max rises at a few tiles only
+//   (3) scan: one workgroup per (row, query head, 32 elements) runs the
+//       per-tile rounding recurrence.  The running max rises at a few tiles only
 //       ("events"); between two events the recurrence only adds exact
 //       int32 terms, so each such run is summed in parallel and the
 //       sequential part is one step per event, taken only when no partial
@@ -38,6 +38,7 @@ constexpr uint32_t GNT = 256;    // threads per workgroup
 constexpr uint32_t GMAXG = 8;    // query heads per KV head
 constexpr uint32_t GMAXT = 1024; // tiles per context (scan)
 constexpr uint32_t GSLOTS = 32;  // runs the scan sums in parallel (more: tile by tile)
+constexpr uint32_t GSE = 32;     // elements per scan workgroup
 
 // Block rows [r0, r0 + nrow) of a row's block that fall in `tile`.
 struct GqaRows {
@@ -369,7 +370,7 @@ struct __attribute__((aligned(16))) GqaScanSmem {
     int32_t ts[GMAXT];          // tile sums
     int16_t run[GMAXT];         // run of each tile (0: before the first event)
     int16_t ev[GMAXT];          // tile of event k (run k + 1 starts there)
-    int32_t rsum[GSLOTS][128];  // per run, per element: sum of the tile values
+    int32_t rsum[GSLOTS][GSE];  // per run, per element: sum of the tile values
     int32_t rts[GSLOTS];        // per run: sum of the tile sums
     int32_t rlen[GSLOTS];       // per run: tiles
     int64_t old[GSLOTS];        // per run: the rescale factor of its event, << 2
@@ -425,16 +426,18 @@ __device__ __forceinline__ int32_t sum_tiles_seq(const GqaScanSmem& sm, uint32_t
 template <int D>
 __global__ __launch_bounds__(GNT) void attention_gqa_scan_kernel(AttnArgs a) {
     static_assert(D == 64 || D == 128, "GQA tile path: head_dim 64 or 128");
-    constexpr uint32_t C8 = D / 8, NSL = GNT / C8;  // element octets, tile slices
-    constexpr int TVB = 24;                         // tile-value loads in flight per thread
+    constexpr uint32_t ES = D / GSE;                // workgroups per (row, head)
+    constexpr uint32_t C8 = GSE / 8, NSL = GNT / C8;  // element octets, tile slices
+    constexpr int TVB = 8;                          // tile-value loads in flight per thread
     __shared__ GqaScanSmem sm;
-    const uint32_t t = blockIdx.x / a.num_heads, g = blockIdx.x % a.num_heads;
+    const uint32_t es = blockIdx.x % ES, tg = blockIdx.x / ES;
+    const uint32_t t = tg / a.num_heads, g = tg % a.num_heads;
     if (t >= a.grid_rows) return;
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t n = a.pos0 + t + 1, G = a.group, h = g / G, gi = g % G;
     const uint32_t ntiles = (n + TILE - 1) / TILE;  // <= GMAXT (the launcher's check)
     const size_t rh = (size_t)t * a.num_kv_heads + h;
-    const size_t tv_base = (rh * a.max_tiles * G + gi) * D;  // + j G D + e
+    const size_t tv_base = (rh * a.max_tiles * G + gi) * D + GSE * es;  // + j G D + e
     // ---- every load that does not depend on another is issued first: tile
     // maxima and sums, the exp table, this thread's first tile values ----
     int32_t tmr[GMAXT / GNT], tsr[GMAXT / GNT];
@@ -465,7 +468,7 @@ __global__ __launch_bounds__(GNT) void attention_gqa_scan_kernel(AttnArgs a) {
     }
     if (tid < 257) *(v4u*)(sm.e14 + 8 * tid) = exr;
     if (tid == 0) *(v4u*)(sm.e14 + 8 * 256) = exr2;
-    for (uint32_t i = tid; i < GSLOTS * 128; i += GNT) (&sm.rsum[0][0])[i] = 0;
+    for (uint32_t i = tid; i < GSLOTS * GSE; i += GNT) (&sm.rsum[0][0])[i] = 0;
     if (tid < GSLOTS) sm.rts[tid] = sm.rlen[tid] = 0;
     lds_barrier();
     // ---- events (wavefront 0): tiles whose maximum exceeds every earlier
@@ -558,9 +561,9 @@ __global__ __launch_bounds__(GNT) void attention_gqa_scan_kernel(AttnArgs a) {
             sm.old[tid] = (int64_t)prob(sm.e14, mprev - sm.tm[sm.ev[tid - 1]]) << 2;
         }
         lds_barrier();
-        // ---- the sum of the probabilities, once per head (lane 0 of the
-        // last wavefront, beside the elements' chains) ----
-        if (tid == GNT - 64) {
+        // ---- the sum of the probabilities, once per workgroup (lane 0 of
+        // the second wavefront, beside the elements' chains) ----
+        if (tid == 64) {
             int32_t sum = 0, m = INT16_MIN;
             for (uint32_t r = 0; r <= nev; r++) {
                 const uint32_t a0 = r == 0 ? 0 : (uint32_t)sm.ev[r - 1];
@@ -576,14 +579,14 @@ __global__ __launch_bounds__(GNT) void attention_gqa_scan_kernel(AttnArgs a) {
             }
             sm.sum = sum;
         }
-    } else if (tid == GNT - 64) {
+    } else if (tid == 64) {
         sm.sum = sum_tiles_seq(sm, 0, ntiles, INT16_MIN, 0);
     }
     // ---- the accumulator, one element per thread: one step per run when
     // no partial sum of the run can reach the int32 bounds (tile values
     // << 8 are within 2^23 in magnitude), else the run tile by tile ----
     int32_t acc = 0;
-    if (tid < D) {
+    if (tid < GSE) {
         const size_t tv0 = tv_base + tid;
         if (!parallel) {
             acc = acc_tiles_seq(a, sm, tv0, G, D, 0, ntiles, INT16_MIN, 0);
@@ -604,8 +607,8 @@ __global__ __launch_bounds__(GNT) void attention_gqa_scan_kernel(AttnArgs a) {
         }
     }
     lds_barrier();  // the sum
-    if (tid < D)
-        a.out[(size_t)t * a.ldo + (size_t)g * D + tid] =
+    if (tid < GSE)
+        a.out[(size_t)t * a.ldo + (size_t)g * D + GSE * es + tid] =
             fx_sat16(fx_rnd((int64_t)acc * fx_inv_sum(sm.sum), 16));
 }
 
@@ -621,7 +624,7 @@ hipError_t launch_gqa_d(const AttnArgs& a, uint32_t rows, uint32_t tiles, hipStr
     attention_gqa_pv_kernel<D><<<grid, GNT, 0, st>>>(g);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
-    attention_gqa_scan_kernel<D><<<rows * a.num_heads, GNT, 0, st>>>(g);
+    attention_gqa_scan_kernel<D><<<rows * a.num_heads * (D / GSE), GNT, 0, st>>>(g);
     return hipGetLastError();
 }
 

@@ -137,7 +137,7 @@ struct llm_ctx {
     // contexts of at least this many tiles take the GQA tile path (shorter
     // ones run faster with a workgroup per query head and tile);
     // LLM_ACCEL_GQA_MIN_TILES overrides it
-    uint32_t gqa_min_tiles = 96;
+    uint32_t gqa_min_tiles = 64;
     uint32_t sync_qkv[32] = {};        // QKV arrivals per line so far, mod 2^32
     uint32_t sync_attn = 0;            // attention arrivals per line, mod 2^32
     // bound of one wait (100 MHz ticks); LLM_ACCEL_WAIT_LIMIT overrides it

@@ -422,7 +422,7 @@ def test_running_max_rises_often(n, period):
 @pytest.fixture
 def gqa_everywhere(monkeypatch):
     """Contexts of 5 tiles and more take the GQA tile path (by default it
-    starts at 96 tiles, where it overtakes the per-head path)."""
+    starts at 64 tiles, where it overtakes the per-head path)."""
     monkeypatch.setenv("LLM_ACCEL_GQA_MIN_TILES", "5")
 
 
