@@ -9,6 +9,27 @@
 // __threadfence() would instead write back and invalidate the whole L2 of
 // the XCD for every workgroup, which dominates when hundreds of workgroups
 // publish.
+//
+// Why relaxed atomics suffice (an argument at the level of the gfx9 ISA,
+// not of the C++ memory model):
+//   - producer: every value is a relaxed agent-scope atomic store
+//     (global_store ... sc1).  s_waitcnt vmcnt(0) returns only when the
+//     memory system has acknowledged each of the wavefront's stores, i.e.
+//     when each is performed at the coherence point; __syncthreads() then
+//     puts every wavefront of the workgroup past its own wait before one
+//     thread issues the counter's atomic add.  The add is therefore issued
+//     after the values are globally visible at the coherence point;
+//   - consumer: the counter is polled with relaxed agent-scope atomic
+//     loads (sc1: read at the coherence point, not from a stale L2 line).
+//     The value loads are issued only after the poll's result has decided a
+//     branch; the hardware issues a wavefront's memory instructions in
+//     order and does not execute past an unresolved branch, and both kinds
+//     of load are served by the same coherence point, so they see the
+//     values written before the counter reached its target.
+// The release / acquire formulation would make the compiler surround each
+// counter atomic with write-back / invalidation of the XCD's whole L2
+// (agent scope spans XCDs whose L2s are not coherent with each other),
+// which is the per-workgroup cost this scheme avoids.
 #pragma once
 
 #include <hip/hip_runtime.h>
