@@ -228,3 +228,61 @@ def test_kat2_kat3_generated_tokens(qwen3b_reference_model, layers, kat):
         toks, st = a.generate(m.embedding(), k["prompt"], 8, layers, 2)
     assert toks == k["generated"]
     assert st["coarse_task_count"] == 2 * layers + 1 + (2 * layers + 1)
+
+
+def _kat_final_rows(m, layers):
+    """The prompt (tokens 0..7, one block) through `layers` layers and Task
+    20 on the GPU, and the same steps in the oracle: both [8][H] rows."""
+    import llm_accel
+    s = orc.profile("qwen2.5-3b")
+    shape = llm_accel.Shape(s.vocab_size, s.hidden_size, s.intermediate_size,
+                            s.num_layers, s.num_heads, s.num_kv_heads, 64, 1e6)
+    emb = m.embedding()
+    h = emb[0:8].copy()
+    with llm_accel.Accelerator(shape) as a:
+        for layer in range(layers):
+            for p in range(7):
+                a.load_projection(layer, p, m.weight(layer, p))
+        a.load_norms(m.norms())
+        a.upload(1, h)
+        for layer in range(layers):
+            a.task(18, layer, 8, 0, 1, 0)
+            a.task(19, layer, 8, 0, 0, 1)
+        a.task(20, 0, 8, 0, 1, 0)
+        got = a.download(0, 8)
+    kv = m.new_kv()
+    cur = h
+    for layer in range(layers):
+        _, cur, _ = m.task(kv, 18, layer, cur, 0)
+        _, cur, _ = m.task(kv, 19, layer, cur, 0)
+    _, want, _ = m.task(kv, 20, 0, cur, 0)
+    return got, want
+
+
+@pytest.mark.parametrize("layers", [1, 2])
+def test_kat2_kat3_final_hidden_rows_match_oracle(qwen3b_reference_model, layers):
+    """The final-normed prompt rows of the reference's random Qwen2.5-3B
+    model (1 and 2 layers): GPU and oracle bit for bit, and their FNV-1a-64
+    checksums (host:8542-8549) equal."""
+    _say(f"case KAT final hidden rows, {layers} layer(s)")
+    got, want = _kat_final_rows(qwen3b_reference_model, layers)
+    assert np.array_equal(got, want)
+    assert [orc.checksum(got[p]) for p in range(8)] == [orc.checksum(want[p]) for p in range(8)]
+
+
+@pytest.mark.xfail(strict=True, reason="parity unpinned: the reference's hls::exp<16,8> "
+                   "(SiLU, host/host_qwen_8x64.cpp:578-586) is not floor(e^x*256) at every "
+                   "entry, so the post-FFN rows differ from the reference's in low bits")
+@pytest.mark.parametrize("layers,kat", [(1, "kat2_qwen3b_l1"), (2, "kat3_qwen3b_l2")])
+def test_kat2_kat3_final_hidden_checksums_on_gpu(qwen3b_reference_model, layers, kat):
+    """results/qwen3b-e2e-20260820/host.evidence.log:40-47 (1 layer, 8
+    positions) and results/qwen3b-e2e-l2-20260821/host.evidence.log:49
+    (2 layers, position 7)."""
+    got, _ = _kat_final_rows(qwen3b_reference_model, layers)
+    k = KAT[kat]
+    if layers == 1:
+        want = [int(x, 16) for x in k["final_hidden_checksums"]]
+        assert [orc.checksum(got[p]) for p in range(8)] == want
+    else:
+        assert orc.checksum(got[7]) == int(k["final_hidden_checksum_pos7"], 16)
+
