@@ -15,7 +15,8 @@ stream-event times (the loop waits only for each token's argmax keys).
 Extras: configs[1] (one layer, P8/G2: an 8-row prefill block and a decode
 forward at position 8, over `--copies` weight copies so that the streamed
 working set exceeds the 256 MB Infinity Cache), per-kernel times, the
-configs[3] context sweep and the configs[2] request (2 layers, P16/G8).
+configs[3] context sweep, the configs[2] request (2 layers, P16/G8) and
+the operator-level commands (ops 1-15, 17) on one layer.
 
 Prints one JSON line.
 """
@@ -50,7 +51,7 @@ def parse():
                     help="configs[3] decode context sweep (extra field)")
     ap.add_argument("--full", action=argparse.BooleanOptionalAction, default=True,
                     help="configs[2] request loop (extra field)")
-    ap.add_argument("--part", choices=("all", "configs1", "sweep", "configs4"),
+    ap.add_argument("--part", choices=("all", "configs1", "sweep", "configs4", "ops"),
                     default="all",
                     help="run one part alone and print its figures (for profiling); "
                          "the default runs every part and prints the headline line")
@@ -248,6 +249,61 @@ def request_loop(llm_accel, workloads, spec, layers, prompt_len, gen, emb, lm_he
     }
 
 
+def operator_timings(llm_accel, workloads, spec, synth, iters=50):
+    """Operator-level commands (llm_op, ops 1-15 and 17) on one
+    Qwen2.5-3B-shaped layer with a 2048-position cache: mean µs per command
+    from stream events around `iters` back-to-back commands on the
+    context's own ports, and the algorithmic bytes / µs of each."""
+    shape = llm_accel.Shape(spec.vocab, spec.hidden, spec.inter, 1, spec.heads,
+                            spec.kv_heads, 2048, 1e6)
+    acc = llm_accel.Accelerator(shape)
+    acc.load_model(synth)
+    rng = np.random.default_rng(11)
+    n_ctx = 2048
+    for h in range(spec.kv_heads):
+        k, v = synth.kv_rows(n_ctx, seed_offset=20 + h)
+        acc.kv_write(0, h, 0, k, v)
+    _, port_n = acc.port(llm_accel.PORT_IN)
+    for p in (llm_accel.PORT_IN, llm_accel.PORT_AUX):
+        acc.port_write(p, rng.integers(-600, 600, port_n).astype(np.int16))
+    H, I, C, D = spec.hidden, spec.inter, spec.kv_channels, spec.head_dim
+    G, HK = spec.heads // spec.kv_heads, spec.kv_heads
+    O = llm_accel
+    cases = [  # name, (op, token_count, position, tile_len), algorithmic bytes
+        ("q_proj_r1", (O.OP_Q_PROJECTION, 1, 0, 0), 2 * H * H),
+        ("q_proj_r8", (O.OP_Q_PROJECTION, 8, 0, 0), 2 * H * H),
+        ("k_proj_r8", (O.OP_K_PROJECTION, 8, 0, 0), 2 * C * H),
+        ("gate_proj_r1", (O.OP_FFN_GATE, 1, 0, 0), 2 * I * H),
+        ("gate_proj_r8", (O.OP_FFN_GATE, 8, 0, 0), 2 * I * H),
+        ("down_proj_r1", (O.OP_FFN_DOWN, 1, 0, 0), 2 * H * I),
+        ("down_proj_r8", (O.OP_FFN_DOWN, 8, 0, 0), 2 * H * I),
+        ("rmsnorm_r8", (O.OP_RMSNORM, 8, 0, 0), 2 * 2 * 8 * H),
+        ("silu_mul_r8", (O.OP_SILU_MUL, 8, 0, 0), 3 * 2 * 8 * I),
+        ("residual_r8", (O.OP_RESIDUAL_ADD, 8, 0, 0), 3 * 2 * 8 * H),
+        ("attn_qk_t64", (O.OP_ATTN_QK, G, 0, 64), 2 * HK * (64 * D + G * D + G * 64)),
+        ("attn_pv_t64", (O.OP_ATTN_PV, G, 0, 64), 2 * HK * (64 * D + G * 64 + G * D)),
+        ("softmax_t64", (O.OP_SOFTMAX, G, 0, 64), 2 * 2 * HK * G * 64),
+        ("attn_flash_n1024", (O.OP_ATTN_FLASH, G, 1023, 0), 2 * 2 * HK * 1024 * D),
+        ("attn_flash_n2048", (O.OP_ATTN_FLASH, G, 2047, 0), 2 * 2 * HK * 2048 * D),
+        ("decode_smoke_n2048", (O.OP_DECODE_SMOKE, G, 2047, 1), 2 * 2 * HK * 2048 * D),
+        ("prefill_block_t8_n1024", (O.OP_ATTN_PREFILL_BLOCK, 8, 1016, 0),
+         2 * 2 * HK * 1024 * D),
+    ]
+    out = {}
+    for name, (op, t, pos, tl), nbytes in cases:
+        for _ in range(3):
+            acc.op(op, 0, t, pos, tl, sync=False)
+        acc.sync()
+        acc.record(0)
+        for _ in range(iters):
+            acc.op(op, 0, t, pos, tl, sync=False)
+        acc.record(1)
+        us = acc.elapsed_ms(0, 1) * 1e3 / iters
+        out[name] = {"us": round(us, 3), "algorithmic_gbs": round(nbytes / (us * 1e-6) / 1e9, 1)}
+    acc.close()
+    return out
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -264,6 +320,10 @@ def main():
         print(json.dumps({"part": "sweep", "decode_forward_us_by_context":
                           context_sweep(llm_accel, workloads, spec, synth,
                                         lengths=tuple(args.sweep_n))}), flush=True)
+        return
+    if args.part == "ops":
+        print(json.dumps({"part": "ops", "operators": operator_timings(
+            llm_accel, workloads, spec, synth)}), flush=True)
         return
     if args.part == "configs4":
         tables = workloads.SyntheticModel(workloads.with_layers(spec, 0))
@@ -355,6 +415,7 @@ def main():
         return
     sweep = (context_sweep(llm_accel, workloads, spec, synth, lengths=tuple(args.sweep_n))
              if args.sweep else None)
+    ops = operator_timings(llm_accel, workloads, spec, synth)
     # seeded embedding table and LM head [151936][2048], shared by the
     # request loops
     tables = workloads.SyntheticModel(workloads.with_layers(spec, 0))
@@ -414,6 +475,7 @@ def main():
         "copy_kernel_gbs": copy_gbs,
         "decode_forward_us_by_context": sweep,
         "configs[2]": c2,
+        "operators": ops,
         "roofline": {
             "kernel": "proj_kernel<1,*,EPI_SILU> (gate|up + SiLU*up, decode row)",
             "bound": "hbm",

@@ -36,13 +36,30 @@
 extern "C" {
 #endif
 
-/* Operator ids (include/control_cache_8x64.hpp:253-276).  Only the
- * resident-layer image's operators run here; ids 1..15 and 17 return
+/* Operator ids (include/control_cache_8x64.hpp:253-276).  llm_task() is
+ * the resident-layer image: ids 1..15 and 17 return
  * LLM_STATUS_BAD_OPERATOR exactly as that image does
- * (kernel/control_cache_8x64.cpp:6483-6494). */
+ * (kernel/control_cache_8x64.cpp:6483-6494); llm_op() runs them as the
+ * controller's full image does. */
 enum {
     LLM_OP_NOP = 0,
+    LLM_OP_Q_PROJECTION = 1,       /* operator-level (llm_op)          */
+    LLM_OP_K_PROJECTION = 2,
+    LLM_OP_V_PROJECTION = 3,
+    LLM_OP_O_PROJECTION = 4,
+    LLM_OP_FFN_GATE = 5,
+    LLM_OP_FFN_UP = 6,
+    LLM_OP_FFN_DOWN = 7,
+    LLM_OP_RMSNORM = 8,
+    LLM_OP_SILU_MUL = 9,
+    LLM_OP_RESIDUAL_ADD = 10,
+    LLM_OP_ATTN_QK = 11,
+    LLM_OP_ATTN_PV = 12,
+    LLM_OP_SOFTMAX = 13,
+    LLM_OP_ATTN_FLASH = 14,
+    LLM_OP_DECODE_SMOKE = 15,
     LLM_OP_DECODER_LAYER = 16,     /* attention + FFN sublayers        */
+    LLM_OP_ATTN_PREFILL_BLOCK = 17, /* operator-level (llm_op)         */
     LLM_OP_ATTENTION_SUBLAYER = 18, /* Task 18                         */
     LLM_OP_FFN_SUBLAYER = 19,       /* Task 19                         */
     LLM_OP_FINAL_NORM = 20          /* Task 20                         */
@@ -175,6 +192,55 @@ int llm_hidden_download_ports(llm_ctx_t* ctx, uint32_t pair, int16_t* port0,
 int llm_task(llm_ctx_t* ctx, uint32_t op, uint32_t layer,
              uint32_t token_count, uint32_t position, uint32_t tile_len,
              uint32_t in_pair, uint32_t out_pair, llm_status_t* status);
+
+/* Operator-level commands: the per-operator scheduler of the
+ * controller's full image (kernel/control_cache_8x64.cpp:6497-7500) as the
+ * reference host drives it through run_feature, run_attention and
+ * run_prefill_attention_block (host/host_qwen_8x64.cpp:1088-1133,
+ * :1556-1675).  Replaces launch() of those host paths (:2500-2757) with
+ * ops 1..15 and 17; ops 16 and 18..20 are llm_task()'s (LLM_E_ARG here).
+ *
+ * in, aux and out are device memory, each holding what the reference's
+ * two ports of that name hold (input_port0/1, aux_port0/1,
+ * output_port0/1), concatenated and tight (rows not padded to 64-byte
+ * words); NULL selects the context's own port buffer (llm_port()).  With
+ * H = hidden, I = intermediate, C = num_kv_heads * head_dim, G = query
+ * heads per KV head, d = head_dim, T = token_count, and [a][b] row-major
+ * int16 Q8.8:
+ *   1-3, 5, 6 (Q, K, V, gate, up projection of `layer`): in [T][H] ->
+ *        out [T][H | C | C | I | I];
+ *   4 (O): in [T][H] -> out [T][H];   7 (down): in [T][I] -> out [T][H];
+ *   8 RMSNORM: in [T][H], aux [1][H] gains -> out [T][H];
+ *   9 SILU_MUL: in gate [T][I], aux up [T][I] -> out [T][I];
+ *   10 RESIDUAL_ADD: in [T][H], aux [T][H] -> out [T][H];
+ *   11 ATTN_QK (1 <= tile_len <= 64): in q [Hkv][G][d], aux K panels
+ *        [Hkv][tile_len][d] -> out scores [Hkv][G][64] (0 past tile_len);
+ *   12 ATTN_PV: in probabilities [Hkv][G][64] (Q8.8, first tile_len
+ *        used), aux V panels [Hkv][tile_len][d] -> out [Hkv][G][d];
+ *   13 SOFTMAX: in [Hkv][G][64] -> out [Hkv][G][tile_len];
+ *   14 ATTN_FLASH (T = G): in q [Hkv][G][d] -> out [Hkv][G][d], attention
+ *        over cache positions [0, position] of `layer`;
+ *   15 DECODE_SMOKE (T = G): as 14 after writing aux = K [Hkv][d] then
+ *        V [Hkv][d] as cache position `position`;
+ *   17 ATTN_PREFILL_BLOCK (1 <= T <= 8): in q [Hkv][T][G][d] -> out the
+ *        same shape; token t attends to cache positions [0, position + t].
+ * Returns the reference status code (also in *status, with the
+ * controller's counters); work is enqueued on the context stream and not
+ * waited for (llm_sync()).  tile_len != 0 on a projection is the FPGA
+ * MM wave-profile encoding and returns LLM_E_ARG. */
+enum { LLM_PORT_IN = 0, LLM_PORT_AUX = 1, LLM_PORT_OUT = 2 };
+int llm_op(llm_ctx_t* ctx, uint32_t op, uint32_t layer, uint32_t token_count,
+           uint32_t position, uint32_t tile_len, const int16_t* in,
+           const int16_t* aux, int16_t* out, llm_status_t* status);
+/* The context's port buffer `port` (device memory of *elems int16,
+ * enough for every operator's tensor); allocated on first use.  Replaces
+ * the reference host's six data buffers data_words_ (two per port name,
+ * host/host_qwen_8x64.cpp:3060, packed by :2062-2123). */
+int llm_port(llm_ctx_t* ctx, uint32_t port, void** dev, size_t* elems);
+/* Synchronous host copies into / out of a port buffer (the migrations
+ * around launch(), host/host_qwen_8x64.cpp:2500-2757). */
+int llm_port_write(llm_ctx_t* ctx, uint32_t port, const int16_t* host, size_t elems);
+int llm_port_read(llm_ctx_t* ctx, uint32_t port, int16_t* host, size_t elems);
 
 /* KV cache rows of one layer and KV head, positions [pos0, pos0 + n):
  * k / v are [n][head_dim] Q8.8 (K stored after RoPE, V raw). */

@@ -26,6 +26,7 @@
 #include "decode_stack.h"
 #include "fixed_point.h"
 #include "kernels.h"
+#include "ops.h"
 
 namespace {
 
@@ -162,6 +163,12 @@ struct llm_ctx {
     struct FinalCache { int pair = -1, src = -1; uint32_t rows = 0; };
     FinalCache final_cache;
     int16_t* xn_final = nullptr;        // [8][Hp]
+    // Operator-level commands (llm_op): the context's own in / aux / out
+    // port buffers and the 8-row projection staging, allocated on first use.
+    bool ports_ready = false;
+    int16_t* ports[3] = {nullptr, nullptr, nullptr};
+    size_t port_n = 0;                  // elements per port
+    int16_t* op_stage = nullptr;        // [8][max(Hp, Ip)]
     // partial sums / arrival counters of the split matrix-core projection
     int32_t* mf_part = nullptr;
     uint32_t* mf_count = nullptr;
@@ -1395,6 +1402,249 @@ int llm_task(llm_ctx_t* c, uint32_t op, uint32_t layer, uint32_t token_count,
     // The resident-layer image carries no per-operator scheduler
     // (kernel/control_cache_8x64.cpp:6483-6494).
     return reject(LLM_STATUS_BAD_OPERATOR);
+}
+
+}  // extern "C"
+
+namespace {
+
+// ---------------------------------------------------------------------
+// Operator-level commands: the per-operator scheduler of the controller's
+// full image (kernel/control_cache_8x64.cpp:6497-7500), driven by the
+// reference host's run_feature / run_attention /
+// run_prefill_attention_block (host/host_qwen_8x64.cpp:1088-1133,
+// :1556-1675).
+// ---------------------------------------------------------------------
+
+// One port holds the largest tensor an operator exchanges: 8 feature rows
+// of the hidden or intermediate width, every KV head's K / V panel of 64
+// positions, or 64 scores per query head.
+int ensure_ports(llm_ctx* c) {
+    if (c->ports_ready) return 0;
+    const size_t n = std::max({(size_t)8 * c->Hp, (size_t)8 * c->Ip, (size_t)64 * c->Hq,
+                               (size_t)64 * c->Ckv});
+    for (int i = 0; i < 3; i++)
+        if (!c->ports[i])
+            if (int rc = dev_alloc(c, (void**)&c->ports[i], n * 2)) return rc;
+    if (!c->op_stage)
+        if (int rc = dev_alloc(c, (void**)&c->op_stage,
+                               (size_t)8 * std::max(c->Hp, c->Ip) * 2))
+            return rc;
+    c->port_n = n;
+    c->ports_ready = true;
+    return 0;
+}
+
+// The controller's status counters for an operator-level command
+// (kernel/control_cache_8x64.cpp:6715-6723, :6825-6832, :7110-7113,
+// :7163-7169, :7251-7258, :7339-7342, :7489-7495): two 8x64 cores, waves
+// of 128 outputs, 32 packets per MM task, 16-lane vector packets, PV waves
+// of 64 head elements.
+void fill_op_counters(const llm_ctx* c, uint32_t op, uint32_t T, uint32_t pos,
+                      uint32_t tile_len, llm_status_t* st) {
+    const uint32_t pv_waves = (uint32_t)cdiv(c->d, 64);
+    auto mm = [&](uint32_t waves, uint32_t tasks) {
+        st->output_waves = waves;
+        st->mm_tasks = tasks;
+        st->completed_packets = tasks * 32;
+    };
+    if (op >= 1 && op <= 7) {
+        const uint32_t out_dim = (op == 2 || op == 3) ? c->Ckv
+                               : (op == 5 || op == 6) ? c->I : c->H;
+        const uint32_t w = (uint32_t)cdiv(out_dim, 128);
+        mm(w, 2 * w);
+    } else if (op >= 8 && op <= 10) {
+        const uint32_t blocks = (uint32_t)cdiv(op == 9 ? c->I : c->H, 16);
+        const uint32_t c0 = std::min(T, 4u), c1 = T > 4 ? T - 4 : 0;
+        st->vector_tasks = (c0 > 0) + (c1 > 0);
+        st->completed_packets = (c0 + c1) * blocks;
+    } else if (op == 11) {
+        mm(1, 2);
+    } else if (op == 12) {
+        mm(pv_waves, 2 * pv_waves);
+    } else if (op == 13) {
+        st->vector_tasks = 2;
+        st->completed_packets = 2 * c->G * (uint32_t)cdiv(tile_len, 16);
+    } else if (op == 14 || op == 15) {
+        mm(pv_waves, 2 * (uint32_t)cdiv(pos + 1, 64) * (1 + pv_waves));
+    } else if (op == 17) {
+        mm(pv_waves, 2 * (uint32_t)cdiv(pos + T, 64) * c->G * (1 + pv_waves));
+    }
+}
+
+// One projection (0 = Q .. 6 = down) of `T` rows without epilogue.  Q, K
+// and V are row ranges of the stored Q | K | V matrix.  The rows are
+// staged into 8 rows padded to whole k-steps: the projection kernels read
+// whole k-steps, and the matrix-core kernel all 8 rows (rows past T only
+// reach outputs that are not stored).
+int enqueue_op_projection(llm_ctx* c, uint32_t layer, uint32_t proj, uint32_t T,
+                          const int16_t* in, int16_t* out) {
+    static const int mat_of[7] = {M_QKV, M_QKV, M_QKV, M_O, M_GATE, M_UP, M_DOWN};
+    const Matrix& m = c->mat(layer, mat_of[proj]);
+    const uint32_t row0 = proj == 1 ? c->H : proj == 2 ? c->H + c->Ckv : 0;
+    const uint32_t n = proj == 0 ? c->H : (proj <= 2 ? c->Ckv : m.n);
+    if (T == 0) return 0;
+    HIP_TRY(hipMemcpy2DAsync(c->op_stage, (size_t)m.k_pad * 2, in, (size_t)m.k * 2,
+                             (size_t)m.k * 2, T, hipMemcpyDeviceToDevice, c->stream));
+    llm::ProjArgs a{};
+    a.w0 = m.d + (size_t)row0 * m.k_pad;
+    a.steps = m.steps;
+    a.x = c->op_stage;
+    a.ldx = m.k_pad;
+    a.out = out;
+    a.ldo = n;
+    a.n = n;
+    a.rows = T;
+    // the matrix-core records cover 16 outputs each
+    if (row0 % llm::kMfRows == 0) {
+        set_mf(a, m);
+        if (a.mf0) {
+            a.mf0 += (size_t)(row0 / llm::kMfRows) * m.kq * llm::kMfRecord;
+            a.ms0 += (size_t)2 * row0;
+            a.nc = (uint32_t)cdiv(n, llm::kMfRows);
+        }
+    }
+    HIP_TRY(llm::launch_proj(a, llm::EPI_STORE, m.L, (uint32_t)cdiv(n, 4), c->stream));
+    return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int llm_port(llm_ctx_t* c, uint32_t port, void** dev, size_t* elems) {
+    if (!c || port > LLM_PORT_OUT) return fail(LLM_E_ARG, "bad port arguments");
+    HIP_TRY(hipSetDevice(c->device));
+    if (int rc = ensure_ports(c)) return rc;
+    if (dev) *dev = c->ports[port];
+    if (elems) *elems = c->port_n;
+    return 0;
+}
+
+int llm_port_write(llm_ctx_t* c, uint32_t port, const int16_t* host, size_t elems) {
+    if (!c || port > LLM_PORT_OUT || (!host && elems)) return fail(LLM_E_ARG, "bad port arguments");
+    HIP_TRY(hipSetDevice(c->device));
+    if (int rc = ensure_ports(c)) return rc;
+    if (elems > c->port_n) return fail(LLM_E_ARG, "port write exceeds the port");
+    FLUSH_TRY(c);
+    if (elems)
+        HIP_TRY(hipMemcpyAsync(c->ports[port], host, elems * 2, hipMemcpyHostToDevice,
+                               c->stream));
+    SYNC_TRY(c);
+    return 0;
+}
+
+int llm_port_read(llm_ctx_t* c, uint32_t port, int16_t* host, size_t elems) {
+    if (!c || port > LLM_PORT_OUT || (!host && elems)) return fail(LLM_E_ARG, "bad port arguments");
+    HIP_TRY(hipSetDevice(c->device));
+    if (int rc = ensure_ports(c)) return rc;
+    if (elems > c->port_n) return fail(LLM_E_ARG, "port read exceeds the port");
+    FLUSH_TRY(c);
+    if (elems)
+        HIP_TRY(hipMemcpyAsync(host, c->ports[port], elems * 2, hipMemcpyDeviceToHost,
+                               c->stream));
+    SYNC_TRY(c);
+    return 0;
+}
+
+int llm_op(llm_ctx_t* c, uint32_t op, uint32_t layer, uint32_t token_count,
+           uint32_t position, uint32_t tile_len, const int16_t* in,
+           const int16_t* aux, int16_t* out, llm_status_t* status) {
+    llm_status_t local;
+    llm_status_t* st = status ? status : &local;
+    std::memset(st, 0, sizeof(*st));
+    if (!c) return fail(LLM_E_ARG, "null context");
+    // argument decoding and the checks shared by every operator
+    // (kernel/control_cache_8x64.cpp:5882-5957)
+    if (tile_len != 0) token_count &= 0xffffu;
+    st->op = LLM_OP_NOP;
+    st->token_count = token_count;
+    st->last_task = 1;
+    auto reject = [&](uint32_t code) {
+        st->code = code;
+        return (int)code;
+    };
+    if (token_count > 8) return reject(LLM_STATUS_BAD_TOKEN_COUNT);
+    st->op = op;
+    if (op > LLM_OP_FINAL_NORM) return reject(LLM_STATUS_BAD_OPERATOR);
+    if (op == LLM_OP_NOP) return LLM_STATUS_OK;
+    if (op == LLM_OP_DECODER_LAYER || op >= LLM_OP_ATTENTION_SUBLAYER) {
+        st->op = LLM_OP_NOP;
+        return fail(LLM_E_ARG, "operator " + std::to_string(op) +
+                                   " is a resident-layer task: use llm_task");
+    }
+    if (layer >= c->L) return reject(LLM_STATUS_BAD_LAYER);
+    const uint32_t T = token_count, G = c->G, D = c->d;
+    // per-operator checks in the controller's order (:6497-6531,
+    // :6729-6750, :7018-7027)
+    if (op == LLM_OP_ATTN_PREFILL_BLOCK) {
+        if (T == 0) return reject(LLM_STATUS_BAD_TOKEN_COUNT);
+        if (position >= c->max_seq || position + T > c->max_seq)
+            return reject(LLM_STATUS_BAD_POSITION);
+    } else if (op == LLM_OP_ATTN_FLASH || op == LLM_OP_DECODE_SMOKE) {
+        if (T != G) return reject(LLM_STATUS_BAD_TOKEN_COUNT);
+        if (position >= c->max_seq) return reject(LLM_STATUS_BAD_POSITION);
+        if (tile_len > 64) return reject(LLM_STATUS_BAD_TILE_LENGTH);
+    } else if (op >= LLM_OP_ATTN_QK && op <= LLM_OP_SOFTMAX) {
+        if (tile_len == 0 || tile_len > 64) return reject(LLM_STATUS_BAD_TILE_LENGTH);
+    } else if (op <= LLM_OP_FFN_DOWN && tile_len != 0) {
+        // run_mm_wave_profile's encoding (host/host_qwen_8x64.cpp:1495-1554)
+        st->op = LLM_OP_NOP;
+        return fail(LLM_E_ARG, "the MM wave-profile encoding (tile_len != 0 on a "
+                               "projection) selects FPGA cores and stream stages; "
+                               "it is not supported");
+    }
+    HIP_TRY(hipSetDevice(c->device));
+    if (int rc = ensure_ports(c)) return rc;
+    FLUSH_TRY(c);
+    if (!in) in = c->ports[LLM_PORT_IN];
+    if (!aux) aux = c->ports[LLM_PORT_AUX];
+    if (!out) out = c->ports[LLM_PORT_OUT];
+    hipStream_t s = c->stream;
+    const size_t layer_off = (size_t)layer * c->Hkv * c->tiles * llm::kTile * D;
+    if (op <= LLM_OP_FFN_DOWN) {
+        if (!c->loaded[layer * 7 + op - 1])
+            return fail(LLM_E_STATE, "layer " + std::to_string(layer) + " projection " +
+                                         std::to_string(op - 1) + " not loaded");
+        if (int rc = enqueue_op_projection(c, layer, op - 1, T, in, out)) return rc;
+    } else if (op == LLM_OP_RMSNORM) {
+        if (T) HIP_TRY(llm::launch_rmsnorm(in, c->H, aux, c->H, out, c->H, T,
+                                           c->const_gain, s));
+    } else if (op == LLM_OP_SILU_MUL) {
+        HIP_TRY(llm::launch_op_silu_mul(in, aux, T * c->I, c->exp8, out, s));
+    } else if (op == LLM_OP_RESIDUAL_ADD) {
+        HIP_TRY(llm::launch_op_residual(in, aux, T * c->H, out, s));
+    } else if (op == LLM_OP_ATTN_QK) {
+        HIP_TRY(llm::launch_op_qk(in, aux, c->Hkv, G, D, tile_len, c->qk_scale, out, s));
+    } else if (op == LLM_OP_ATTN_PV) {
+        HIP_TRY(llm::launch_op_pv(in, aux, c->Hkv, G, D, tile_len, out, s));
+    } else if (op == LLM_OP_SOFTMAX) {
+        HIP_TRY(llm::launch_op_softmax(in, c->Hkv * G, tile_len, c->exp8, out, s));
+    } else {
+        const bool block = op == LLM_OP_ATTN_PREFILL_BLOCK;
+        if (op == LLM_OP_DECODE_SMOKE)  // aux = K rows, then V rows, of every KV head
+            HIP_TRY(llm::launch_op_kv_append(c->kcache + layer_off, c->vcache + layer_off,
+                                             c->tiles, c->Hkv, D, position, aux,
+                                             aux + (size_t)c->Hkv * D, s));
+        llm::OpFlashArgs fa{};
+        fa.q = in;
+        fa.kcache = c->kcache + layer_off;
+        fa.vcache = c->vcache + layer_off;
+        fa.tiles = c->tiles;
+        fa.kv_heads = c->Hkv;
+        fa.tokens = block ? T : 1;
+        fa.group = G;
+        fa.head_dim = D;
+        fa.pos0 = position;
+        fa.qk_scale = c->qk_scale;
+        fa.exp8 = c->exp8;
+        fa.exp14 = c->exp14;
+        fa.legacy = block ? 0 : 1;
+        fa.out = out;
+        HIP_TRY(llm::launch_op_flash(fa, s));
+    }
+    fill_op_counters(c, op, T, position, tile_len, st);
+    return LLM_STATUS_OK;
 }
 
 }  // extern "C"

@@ -16,6 +16,14 @@ LIB_PATH = os.path.join(_HERE, "libllm_accel.so")
 
 OP_NOP, OP_DECODER_LAYER = 0, 16
 OP_ATTENTION, OP_FFN, OP_FINAL_NORM = 18, 19, 20
+# Operator-level ids (include/control_cache_8x64.hpp:253-276), run by op().
+(OP_Q_PROJECTION, OP_K_PROJECTION, OP_V_PROJECTION, OP_O_PROJECTION,
+ OP_FFN_GATE, OP_FFN_UP, OP_FFN_DOWN, OP_RMSNORM, OP_SILU_MUL,
+ OP_RESIDUAL_ADD, OP_ATTN_QK, OP_ATTN_PV, OP_SOFTMAX, OP_ATTN_FLASH,
+ OP_DECODE_SMOKE) = range(1, 16)
+OP_ATTN_PREFILL_BLOCK = 17
+PORT_IN, PORT_AUX, PORT_OUT = 0, 1, 2
+ATTENTION_TILE = 64
 STATUS_OK, BAD_OPERATOR, BAD_TOKEN_COUNT = 0, 1, 2
 BAD_TILE_LENGTH, BAD_POSITION, BAD_LAYER = 3, 4, 5
 PROJ_Q, PROJ_K, PROJ_V, PROJ_O, PROJ_GATE, PROJ_UP, PROJ_DOWN = range(7)
@@ -34,7 +42,8 @@ EXPORTS = (
     "llm_kernel_timing", "llm_kernel_stats", "llm_bench_copy",
     "llm_bench_projection", "llm_load_lm_head", "llm_lm_head_argmax",
     "llm_generate", "llm_lm_head_argmax_static", "llm_set_log",
-    "llm_load_checkpoint_dir",
+    "llm_load_checkpoint_dir", "llm_op", "llm_port", "llm_port_write",
+    "llm_port_read",
 )
 CKPT_TIE_EMBEDDINGS = 1
 CKPT_REQUIRE_LM_HEAD = 2
@@ -151,6 +160,12 @@ def load_library(path=LIB_PATH):
                                                      _u32, vp, vp, vp]),
         "llm_set_log": (ctypes.c_int, [vp, LOG_FN, vp]),
         "llm_load_checkpoint_dir": (ctypes.c_int, [vp, ctypes.c_char_p, _u32, _i16p]),
+        "llm_op": (ctypes.c_int, [vp, _u32, _u32, _u32, _u32, _u32, vp, vp, vp,
+                                  ctypes.POINTER(Status)]),
+        "llm_port": (ctypes.c_int, [vp, _u32, ctypes.POINTER(vp),
+                                    ctypes.POINTER(ctypes.c_size_t)]),
+        "llm_port_write": (ctypes.c_int, [vp, _u32, _i16p, ctypes.c_size_t]),
+        "llm_port_read": (ctypes.c_int, [vp, _u32, _i16p, ctypes.c_size_t]),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)
@@ -328,6 +343,122 @@ class Accelerator:
                             tile_len, in_pair, out_pair, ctypes.byref(st))
         self._check(rc, "llm_task")
         return rc, st
+
+    # --- operator-level commands ---------------------------------------
+    def port(self, port):
+        """(device address, elements) of the context's port buffer."""
+        dev = ctypes.c_void_p()
+        n = ctypes.c_size_t()
+        self._check(lib().llm_port(self._ctx, port, ctypes.byref(dev),
+                                   ctypes.byref(n)), "llm_port")
+        return dev.value, n.value
+
+    def port_write(self, port, a):
+        a = np.ascontiguousarray(a, np.int16).reshape(-1)
+        self._check(lib().llm_port_write(self._ctx, port, _p16(a), a.size),
+                    "llm_port_write")
+
+    def port_read(self, port, n):
+        out = np.zeros(n, np.int16)
+        self._check(lib().llm_port_read(self._ctx, port, _p16(out), n),
+                    "llm_port_read")
+        return out
+
+    def op(self, op, layer=0, token_count=0, position=0, tile_len=0,
+           lhs=None, rhs=None, out_elems=0, in_ptr=None, aux_ptr=None,
+           out_ptr=None, sync=True):
+        """One operator-level command (llm_op).  lhs / rhs go to the
+        context's in / aux ports (or device pointers in_ptr / aux_ptr /
+        out_ptr are used as given); returns (out_elems values of the out
+        port, Status).  A status code != 0 is returned, not raised.  With
+        sync=False the work is only enqueued (and nothing is read back)."""
+        if lhs is not None:
+            self.port_write(PORT_IN, lhs)
+        if rhs is not None:
+            self.port_write(PORT_AUX, rhs)
+        st = Status()
+        rc = lib().llm_op(self._ctx, op, layer, token_count, position, tile_len,
+                          in_ptr, aux_ptr, out_ptr, ctypes.byref(st))
+        self._check(rc, "llm_op")
+        if not sync:
+            return None, st
+        self.sync()
+        out = self.port_read(PORT_OUT, out_elems) if out_elems else None
+        return out, st
+
+    def _checked(self, op, st):
+        if st.code != STATUS_OK:
+            raise AccelError(f"controller status failure: op {op} code {st.code}")
+
+    def run_feature(self, op, lhs, rhs=None, layer=0, position=0):
+        """run_feature (host/host_qwen_8x64.cpp:1088-1133): projections,
+        RMSNorm (rhs = one row of gains), SiLU*up (rhs = up), residual add
+        (rhs = the residual rows); lhs [rows][in_dim] -> [rows][out_dim]."""
+        sh = self.shape
+        h, i, c = sh.hidden_size, sh.intermediate_size, sh.kv_channels
+        in_dim = i if op in (OP_FFN_DOWN, OP_SILU_MUL) else h
+        out_dim = {OP_K_PROJECTION: c, OP_V_PROJECTION: c, OP_FFN_GATE: i,
+                   OP_FFN_UP: i, OP_SILU_MUL: i}.get(op, h)
+        lhs = np.ascontiguousarray(lhs, np.int16)
+        if lhs.ndim != 2 or not 0 < lhs.shape[0] <= 8 or lhs.shape[1] != in_dim:
+            raise AccelError("feature operator input shape mismatch")
+        needs_rhs = op in (OP_RMSNORM, OP_SILU_MUL, OP_RESIDUAL_ADD)
+        if needs_rhs:
+            rows = 1 if op == OP_RMSNORM else lhs.shape[0]
+            if rhs is None or np.shape(rhs) != (rows, in_dim):
+                raise AccelError("feature operator RHS shape mismatch")
+        out, st = self.op(op, layer, lhs.shape[0], position, 0, lhs,
+                          rhs if needs_rhs else None, lhs.shape[0] * out_dim)
+        self._checked(op, st)
+        return out.reshape(lhs.shape[0], out_dim)
+
+    def run_attention(self, op, inputs, aux=None, position=0, tile_len=None,
+                      layer=0):
+        """run_attention (host/host_qwen_8x64.cpp:1556-1645) over every KV
+        head at once: inputs [kv_heads][G][cols] (port k = KV head k).
+        aux: K or V panels [kv_heads][tile_len][d] (QK, PV), (k, v) rows
+        [kv_heads][d] each (DECODE_SMOKE), None (SOFTMAX, ATTN_FLASH).
+        Returns ([kv_heads][G][out_cols], Status)."""
+        sh = self.shape
+        g, d, hk = sh.num_heads // sh.num_kv_heads, sh.head_dim, sh.num_kv_heads
+        src = d if op in (OP_ATTN_QK, OP_ATTN_FLASH, OP_DECODE_SMOKE) else ATTENTION_TILE
+        inputs = np.ascontiguousarray(inputs, np.int16)
+        if tile_len is None:
+            tile_len = 1 if op in (OP_ATTN_FLASH, OP_DECODE_SMOKE) else ATTENTION_TILE
+        if inputs.shape != (hk, g, src) or not 0 < tile_len <= ATTENTION_TILE:
+            raise AccelError("attention source shape mismatch")
+        if op == OP_DECODE_SMOKE:
+            k, v = aux
+            rhs = np.concatenate([np.asarray(k, np.int16).reshape(-1),
+                                  np.asarray(v, np.int16).reshape(-1)])
+            if rhs.size != 2 * hk * d:
+                raise AccelError("decode smoke KV shape mismatch")
+        elif op in (OP_ATTN_QK, OP_ATTN_PV):
+            rhs = np.ascontiguousarray(aux, np.int16)
+            if rhs.shape != (hk, tile_len, d):
+                raise AccelError("attention panel shape mismatch")
+        else:
+            rhs = None
+        cols = {OP_ATTN_QK: ATTENTION_TILE, OP_SOFTMAX: tile_len}.get(op, d)
+        out, st = self.op(op, layer, g, position, tile_len, inputs, rhs,
+                          hk * g * cols)
+        self._checked(op, st)
+        return out.reshape(hk, g, cols), st
+
+    def run_prefill_attention_block(self, queries, position, token_count,
+                                    layer=0):
+        """run_prefill_attention_block (host/host_qwen_8x64.cpp:1647-1675):
+        queries [kv_heads][token_count][G][d] -> the same shape."""
+        sh = self.shape
+        g, d, hk = sh.num_heads // sh.num_kv_heads, sh.head_dim, sh.num_kv_heads
+        q = np.ascontiguousarray(queries, np.int16)
+        if (not 0 < token_count <= 8 or position + token_count > sh.max_seq_len
+                or q.shape != (hk, token_count, g, d)):
+            raise AccelError("prefill attention block shape mismatch")
+        out, st = self.op(OP_ATTN_PREFILL_BLOCK, layer, token_count, position, 0,
+                          q, None, q.size)
+        self._checked(OP_ATTN_PREFILL_BLOCK, st)
+        return out.reshape(q.shape), st
 
     # --- KV cache -------------------------------------------------------
     def kv_read(self, layer, kv_head, pos0, n):

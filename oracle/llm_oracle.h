@@ -125,6 +125,15 @@ void orc_attention(const int16_t* q, uint32_t G, uint32_t d,
 void orc_qk_scores(const int16_t* q, uint32_t G, uint32_t d,
                    const int16_t* k, uint32_t n, int16_t* scores);
 
+/* ATTN_PV of one group over one tile: golden_attention_mm(p, v, d, false)
+ * (host:3219-3278).  p [G][ldp] Q8.8 (first n used), v [n][d], out [G][d]. */
+void orc_attention_pv(const int16_t* p, uint32_t G, uint32_t ldp,
+                      const int16_t* v, uint32_t n, uint32_t d, int16_t* out);
+/* SOFTMAX rows (kernel/compute_stream.cpp:388-478): x [rows][ldx], first
+ * n of each row, out [rows][n]. */
+void orc_softmax_rows(const int16_t* x, uint32_t rows, uint32_t ldx,
+                      uint32_t n, int16_t* out);
+
 /* ---- model ---------------------------------------------------------- */
 typedef struct orc_model orc_model_t;
 

@@ -75,6 +75,9 @@ def _load():
         "orc_attention": (None, [_i16p, _u32, _u32, _i16p, _i16p, _u32,
                                  ctypes.c_int, _i16p]),
         "orc_qk_scores": (None, [_i16p, _u32, _u32, _i16p, _u32, _i16p]),
+        "orc_attention_pv": (None, [_i16p, _u32, _u32, _i16p, _u32, _u32,
+                                    _i16p]),
+        "orc_softmax_rows": (None, [_i16p, _u32, _u32, _u32, _i16p]),
         "orc_model_create": (ctypes.c_void_p,
                              [ctypes.POINTER(Shape), _u32, ctypes.c_int]),
         "orc_model_destroy": (None, [ctypes.c_void_p]),
@@ -201,6 +204,24 @@ def attention(q, k, v, semantics=SEM_RAW_PAYLOAD):
     out = np.zeros((g, d), np.int16)
     lib.orc_attention(p16(q), g, d, p16(k), p16(v), k.shape[0], semantics,
                       p16(out))
+    return out
+
+
+def attention_pv(p, v):
+    """ATTN_PV: p [G][>= n] Q8.8 probabilities, v [n][d]."""
+    p = np.ascontiguousarray(p, np.int16)
+    v = np.ascontiguousarray(v, np.int16)
+    n, d = v.shape
+    out = np.zeros((p.shape[0], d), np.int16)
+    lib.orc_attention_pv(p16(p), p.shape[0], p.shape[1], p16(v), n, d, p16(out))
+    return out
+
+
+def softmax_rows(x, n):
+    """SOFTMAX over the first n elements of each row of x."""
+    x = np.ascontiguousarray(x, np.int16)
+    out = np.zeros((x.shape[0], n), np.int16)
+    lib.orc_softmax_rows(p16(x), x.shape[0], x.shape[1], n, p16(out))
     return out
 
 

@@ -219,23 +219,128 @@ def test_single_position_attention_is_saturated_v():
         assert np.array_equal(out, np.repeat(want, 8, axis=0))
 
 
+@pytest.mark.parametrize("semantics", [orc.SEM_RAW_PAYLOAD, orc.SEM_LEGACY_Q8_8])
 @pytest.mark.parametrize("n", [1, 5, 64, 65, 200])
-def test_uniform_scores_give_rounded_mean(n):
+def test_uniform_scores_give_rounded_mean(n, semantics):
     """q = 0 makes every score 0, every probability 1.0 and every rescale
     factor 1.0 after the first tile, so the output is a closed form in the
     per-tile sums of V: floor(sum_t sat16(sum_tile v) * inv / 256 + 1/2)
-    with inv = floor(256 / n + 1/2)."""
+    with inv = floor(256 / n + 1/2).  Both probability formats (Q2.14 with
+    the PV result scaled by 1/64, Q8.8 unscaled) reach the same form."""
     rng = np.random.default_rng(n)
     d = 64
     q = np.zeros((2, d), np.int16)
     k = rng.integers(-3000, 3000, (n, d), dtype=np.int16)
     v = rng.integers(-60, 60, (n, d), dtype=np.int16)
-    out = orc.attention(q, k, v)
+    out = orc.attention(q, k, v, semantics)
     inv = math.floor(Fraction(256, n) + Fraction(1, 2))
     tiles = [v[t:t + 64].astype(np.int64).sum(axis=0) for t in range(0, n, 64)]
     acc = sum(np.clip(t, -32768, 32767) for t in tiles) * 256
     want = np.floor((acc * inv) / 65536 + 0.5).astype(np.int64)
     assert np.array_equal(out[0], want) and np.array_equal(out[1], want)
+
+
+def test_legacy_single_position_is_saturated_v():
+    # Q8.8 probabilities: exp(0) = 1.0 is raw 256, the sum 1.0, and the
+    # unscaled PV of 256 x Q4.12(v) returns v clamped to [-8, 8].
+    rng = np.random.default_rng(6)
+    q = rng.integers(-4000, 4000, (8, 128), dtype=np.int16)
+    k = rng.integers(-4000, 4000, (1, 128), dtype=np.int16)
+    v = rng.integers(-6000, 6000, (1, 128), dtype=np.int16)
+    out = orc.attention(q, k, v, orc.SEM_LEGACY_Q8_8)
+    assert np.array_equal(out, np.repeat(np.clip(v, -2048, 2048), 8, axis=0))
+
+
+def test_legacy_one_tile_composes_scores_exp8_pv_and_inverse():
+    """Within one tile the Q8.8 recurrence starts from sum 0 and acc 0, so
+    the output is fm(256 * PV(p, v) * inv(sum p)) with p = exp8(s - max):
+    checks that the legacy path uses the Q8.8 table and no 1/64 scale,
+    from the separately pinned scores, table, PV and inverse."""
+    rng = np.random.default_rng(17)
+    n, d = 37, 64
+    q = rng.integers(-900, 900, (4, d), dtype=np.int16)
+    k = rng.integers(-900, 900, (n, d), dtype=np.int16)
+    v = rng.integers(-700, 700, (n, d), dtype=np.int16)
+    s = orc.qk_scores(q, k).astype(np.int64)
+    p = np.array([[orc.lib.orc_exp_q8_8(int(np.clip(x - row.max(), -32768, 32767)))
+                   for x in row] for row in s], np.int16)
+    pv = orc.attention_pv(p, v).astype(np.int64)
+    inv = np.array([orc.lib.orc_inv_sum(int(r.astype(np.int64).sum()) * 256) for r in p],
+                   np.int64)
+    want = np.clip(np.floor((pv * 256 * inv[:, None]) / 65536 + 0.5), -32768, 32767)
+    assert np.array_equal(orc.attention(q, k, v, orc.SEM_LEGACY_Q8_8), want)
+    # the production format differs (Q2.14 probabilities)
+    assert not np.array_equal(orc.attention(q, k, v), want)
+
+
+# ---- ATTN_PV and SOFTMAX operators ----------------------------------------------
+def test_attention_pv_one_hot_selects_the_saturated_v_row():
+    # p = 1.0 (raw 256) at position j: 256 x Q4.12(v) / 256 = v clamped to
+    # [-8, 8]; columns past n are ignored.
+    rng = np.random.default_rng(3)
+    n, d = 13, 128
+    v = rng.integers(-3000, 3000, (n, d), dtype=np.int16)
+    p = np.zeros((8, 64), np.int16)
+    p[:, n:] = 32767
+    sel = rng.integers(0, n, 8)
+    p[np.arange(8), sel] = 256
+    out = orc.attention_pv(p, v)
+    assert np.array_equal(out, np.clip(v[sel], -2048, 2048))
+
+
+def test_attention_pv_is_a_sum_over_positions():
+    # Two selected positions add (small values: no rounding, no saturation);
+    # a transposed operand or a dropped bank fails this.
+    rng = np.random.default_rng(4)
+    n, d = 64, 64
+    v = rng.integers(-500, 500, (n, d), dtype=np.int16)
+    p = np.zeros((3, 64), np.int16)
+    pairs = [(0, 5), (6, 63), (33, 34)]
+    for r, (a, b) in enumerate(pairs):
+        p[r, a] = p[r, b] = 256
+    out = orc.attention_pv(p, v)
+    for r, (a, b) in enumerate(pairs):
+        assert np.array_equal(out[r], v[a].astype(np.int32) + v[b])
+    # p = 0.5 (raw 128): half of the row, rounded half up
+    p2 = np.zeros((1, 64), np.int16)
+    p2[0, 9] = 128
+    assert np.array_equal(orc.attention_pv(p2, v)[0],
+                          np.floor(v[9] / 2 + 0.5).astype(np.int64))
+
+
+@pytest.mark.parametrize("n", [1, 2, 4, 13, 64])
+def test_softmax_of_equal_values_is_the_reciprocal(n):
+    # every exp is 1.0 (raw 256), the sum is n, the result recip(n) (the
+    # pinned Newton reciprocal); columns past n are ignored
+    x = np.full((2, 64), -700, np.int16)
+    x[:, n:] = 30000
+    out = orc.softmax_rows(x, n)
+    want = orc.lib.orc_recip(256 * n) if 256 * n <= 32767 else orc.lib.orc_recip(32767)
+    assert out.shape == (2, n) and np.all(out == want)
+    if n in (1, 2, 4):
+        assert want == 256 // n
+
+
+def test_softmax_dominant_entry_and_normalisation():
+    rng = np.random.default_rng(8)
+    # one entry 8 or more above the rest: exp(-8) is raw 0, the row is one-hot
+    x = rng.integers(-3000, -2000, (4, 64)).astype(np.int16)
+    x[np.arange(4), [0, 7, 31, 63]] = 0
+    out = orc.softmax_rows(x, 64)
+    assert np.array_equal(out, np.eye(64, dtype=np.int16)[[0, 7, 31, 63]] * 256)
+    # general rows: fm(e * recip(sum e)) with e from the pinned Q8.8 table
+    # and the pinned Newton reciprocal (three steps from a power-of-two
+    # seed: not the exact 1 / sum, so the rows need not sum to 1.0)
+    x = rng.integers(-1500, 1500, (6, 64)).astype(np.int16)
+    for n in (5, 40, 64):
+        out = orc.softmax_rows(x, n)
+        for r in range(6):
+            e = np.array([orc.lib.orc_exp_q8_8(int(np.clip(int(a) - int(x[r, :n].max()),
+                                                            -32768, 32767)))
+                          for a in x[r, :n]], np.int64)
+            inv = orc.lib.orc_recip(int(min(e.sum(), 32767)))
+            assert np.array_equal(out[r], np.floor(e * inv / 256 + 0.5).astype(np.int64))
+            assert out[r].argmax() == x[r, :n].argmax()
 
 
 def test_attention_tiles_anchor_at_zero_and_prefix_invariance():
