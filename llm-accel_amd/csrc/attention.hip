@@ -1058,17 +1058,27 @@ __host__ __device__ inline uint32_t tile_grid(uint32_t rows, uint32_t tiles, uin
     return 8 * group * ((rows * tiles * kv_heads + 7) / 8);
 }
 
-template <int D>
-__global__ __launch_bounds__(D * 2) void attention_tile_scores_kernel(AttnArgs a) {
+// Counters of the one-launch tile path: per (row, query head) one line per
+// group of kArriveGroup tiles, counting the tiles whose maximum has been
+// published (at most 64 tiles: 4 lines).
+constexpr uint32_t kTileFusedMaxTiles = 4 * kArriveGroup;
+__device__ __forceinline__ uint32_t* tile_max_counter(const AttnArgs& a, uint32_t t,
+                                                      uint32_t g) {
+    return a.tmax_count + ((size_t)t * a.num_heads + g) * 4 * kCounterStride;
+}
+
+// Phase 1 of the tile path for a workgroup inside the row's context: the
+// tile's scores and their maximum; FUSED keeps the scores in LDS (lsc, lmt)
+// and publishes the maximum with a device-coherent store.
+template <int D, bool FUSED>
+__device__ __forceinline__ void tile_scores_phase(const AttnArgs& a, const TileWg& wg,
+                                                  TileScoresSmem<D>& sm, int16_t* lsc,
+                                                  int32_t* lmt) {
     static_assert(D % 32 == 0, "tile path: head_dim a multiple of 32");
     constexpr uint32_t NTH = D * 2;
     constexpr int NK = (8 * (D / 2) + NTH - 1) / NTH;  // block K items per thread
-    __shared__ TileScoresSmem<D> sm;
-    const TileWg wg = tile_wg(a);
-    if (!wg.valid) return;  // padding
     const uint32_t t = wg.t, g = wg.g, tile = wg.tile, tid = threadIdx.x;
     const uint32_t n = a.pos0 + t + 1, own = n - 1;
-    if (tile * TILE >= n) return;  // beyond this row's context
     const uint32_t lane = tid & 63, w = tid >> 6;
     const uint32_t G = a.group, h = g / G, gi = g % G;
     const int64_t scale = (int64_t)a.qk_scale << 8;
@@ -1170,13 +1180,30 @@ __global__ __launch_bounds__(D * 2) void attention_tile_scores_kernel(AttnArgs a
         ts = fx_sat32(fx_rnd((int64_t)ts * scale, 16));
         const int32_t s = valid ? fx_sat16(fx_rnd(ts, 8)) : INT16_MIN;
         const size_t base = (((size_t)t * a.num_kv_heads + h) * a.max_tiles + tile) * G + gi;
-        a.s_scores[base * TILE + lane] = (int16_t)s;
         const int32_t mx = wave_max(s);
-        if (lane == 0) a.s_tmax[base] = (int16_t)mx;
+        if (FUSED) {
+            lsc[lane] = (int16_t)s;
+            if (lane == 0) {
+                *lmt = mx;
+                st_coherent(&a.s_tmax32[base], mx);
+            }
+        } else {
+            a.s_scores[base * TILE + lane] = (int16_t)s;
+            if (lane == 0) a.s_tmax[base] = (int16_t)mx;
+        }
     }
     if (gi == 0 && own / TILE == tile && tid < D / 8)  // this row's K into the cache
         *(v4u*)(a.kcache + page_off<D>(a, h, tile) + (own % TILE) * D + 8 * tid) =
             *(const v4u*)(sm.kv[t] + 8 * tid);
+}
+
+template <int D>
+__global__ __launch_bounds__(D * 2) void attention_tile_scores_kernel(AttnArgs a) {
+    __shared__ TileScoresSmem<D> sm;
+    const TileWg wg = tile_wg(a);
+    if (!wg.valid) return;                             // padding
+    if (wg.tile * TILE >= a.pos0 + wg.t + 1) return;   // beyond this row's context
+    tile_scores_phase<D, false>(a, wg, sm, nullptr, nullptr);
 }
 
 // The wavefront's V^T slice of `tile` alone (see slice_load).
@@ -1189,19 +1216,24 @@ __device__ __forceinline__ void slice_load_v(const AttnArgs& a, uint32_t h, uint
     for (int c = 0; c < 4; c++) R.v[c] = *(const v4u*)(vp + 512 * c);
 }
 
-template <int D>
-__global__ __launch_bounds__(D * 2) void attention_tile_pv_kernel(AttnArgs a) {
+// Phase 2 of the tile path for a workgroup inside the row's context: the
+// tile's probabilities under the running max, their sum, its PV values,
+// and the recurrence on the last tile of the (row, query head) to arrive.
+// Non-FUSED: the scores and maxima come from the scores launch.  FUSED:
+// this workgroup's scores are lsc / lmt, the other tiles' maxima are
+// published during this launch: wait() (after this phase's own loads are
+// issued) returns once they all are, or false when the wait gave up.
+template <int D, bool FUSED, typename Wait>
+__device__ __forceinline__ void tile_pv_phase(const AttnArgs& a, const TileWg& wg,
+                                              TilePvSmem<D>& sm, const int16_t* lsc,
+                                              const int32_t* lmt, Wait&& wait) {
     static_assert(D % 32 == 0, "tile path: head_dim a multiple of 32");
     constexpr uint32_t NTH = D * 2;
     constexpr int NE = (257 + NTH - 1) / NTH;    // exp table pieces per thread
     constexpr int NV = (8 * D + NTH - 1) / NTH;  // block V elements per thread
     constexpr int NM = 4;                        // tile maxima per lane (tiles < 256)
-    __shared__ TilePvSmem<D> sm;
-    const TileWg wg = tile_wg(a);
-    if (!wg.valid) return;  // padding
     const uint32_t t = wg.t, g = wg.g, tile = wg.tile, tid = threadIdx.x;
     const uint32_t n = a.pos0 + t + 1, own = n - 1;
-    if (tile * TILE >= n) return;  // beyond this row's context
     const uint32_t ntiles = (n + TILE - 1) / TILE;
     const uint32_t lane = tid & 63, w = tid >> 6;
     const uint32_t G = a.group, h = g / G, gi = g % G;
@@ -1225,22 +1257,32 @@ __global__ __launch_bounds__(D * 2) void attention_tile_pv_kernel(AttnArgs a) {
         vx[u] = a.qkv[(size_t)(tr.r0 + i / D) * a.ldqkv +
                       (size_t)(a.num_heads + a.num_kv_heads) * D + (size_t)h * D + i % D];
     }
-    const int32_t sc = a.s_scores[base * TILE + lane];
-    const int32_t mt = a.s_tmax[base];
-    // maxima of the tiles before this one (this lane's share)
-    int32_t mprev = INT16_MIN;
+    int32_t sc = 0, mt = 0, mprev = INT16_MIN;  // mprev: maxima of the earlier tiles
+    if (!FUSED) {
+        sc = a.s_scores[base * TILE + lane];
+        mt = a.s_tmax[base];
 #pragma unroll
-    for (int u = 0; u < NM; u++) {
-        const uint32_t j = lane + 64 * u;
-        const int32_t v = a.s_tmax[(rh * a.max_tiles + (j < tile ? j : 0)) * G + gi];
-        mprev = j < tile && v > mprev ? v : mprev;
-    }
-    for (uint32_t j = lane + 64 * NM; j < tile; j += 64) {  // contexts beyond 256 tiles
-        const int32_t v = a.s_tmax[(rh * a.max_tiles + j) * G + gi];
-        mprev = v > mprev ? v : mprev;
+        for (int u = 0; u < NM; u++) {  // this lane's share
+            const uint32_t j = lane + 64 * u;
+            const int32_t v = a.s_tmax[(rh * a.max_tiles + (j < tile ? j : 0)) * G + gi];
+            mprev = j < tile && v > mprev ? v : mprev;
+        }
+        for (uint32_t j = lane + 64 * NM; j < tile; j += 64) {  // contexts beyond 256 tiles
+            const int32_t v = a.s_tmax[(rh * a.max_tiles + j) * G + gi];
+            mprev = v > mprev ? v : mprev;
+        }
     }
     SplitRegs regs;
     slice_load_v<D>(a, h, tile, w, lane, regs);
+    if (FUSED) {
+        if (!wait()) return;
+        sc = lsc[lane];
+        mt = *lmt;
+        for (uint32_t j = lane; j < tile; j += 64) {  // tile < kTileFusedMaxTiles
+            const int32_t v = ld_coherent(&a.s_tmax32[(rh * a.max_tiles + j) * G + gi]);
+            mprev = v > mprev ? v : mprev;
+        }
+    }
 #pragma unroll
     for (int u = 0; u < NE; u++) {
         const uint32_t c = tid + NTH * u;
@@ -1321,6 +1363,10 @@ __global__ __launch_bounds__(D * 2) void attention_tile_pv_kernel(AttnArgs a) {
                                     ? ntiles - grp * kArriveGroup : kArriveGroup;
         if (!arrive_last(top + (1 + grp) * kCounterStride, in_grp, &sm.last)) return;
         if (!arrive_last(top, tile_groups(ntiles), &sm.last)) return;
+        // every workgroup of this (row, query head) has passed its wait for
+        // the maxima: their counters start the next launch at zero
+        if (FUSED && tid < tile_groups(ntiles))
+            st_coherent(tile_max_counter(a, t, g) + tid * kCounterStride, 0u);
     }
     // A tile whose maximum does not raise the running max has factor
     // exp(0) = 1.0 (rnd(v * 2^16, 16) = v): sum and acc take saturating
@@ -1346,7 +1392,7 @@ __global__ __launch_bounds__(D * 2) void attention_tile_pv_kernel(AttnArgs a) {
         pc.tsv = 0;
         if (tid < nj) {
             const size_t b = (rh * a.max_tiles + j0 + tid) * G + gi;
-            pc.tm = a.s_tmax[b];
+            pc.tm = FUSED ? ld_coherent(&a.s_tmax32[b]) : (int32_t)a.s_tmax[b];
             pc.tsv = ld_coherent(&a.s_tsum[b]);
         }
     };
@@ -1414,6 +1460,63 @@ __global__ __launch_bounds__(D * 2) void attention_tile_pv_kernel(AttnArgs a) {
 }
 
 template <int D>
+__global__ __launch_bounds__(D * 2) void attention_tile_pv_kernel(AttnArgs a) {
+    __shared__ TilePvSmem<D> sm;
+    const TileWg wg = tile_wg(a);
+    if (!wg.valid) return;                             // padding
+    if (wg.tile * TILE >= a.pos0 + wg.t + 1) return;   // beyond this row's context
+    tile_pv_phase<D, false>(a, wg, sm, nullptr, nullptr, [] { return true; });
+}
+
+// The tile path in one launch (contexts of at most kTileFusedMaxTiles
+// tiles; launched only when every workgroup of the grid fits on the device
+// at once, so that the workgroups a tile waits for are all running): the
+// scores phase, one arrival per tile after its maximum is published, the V
+// loads of the PV phase issued, then a bounded wait for every tile's
+// maximum of the (row, query head), and the PV phase.
+template <int D>
+__global__ __launch_bounds__(D * 2) void attention_tile_fused_kernel(AttnArgs a) {
+    __shared__ union {
+        TileScoresSmem<D> s;
+        TilePvSmem<D> p;
+    } sm;
+    __shared__ int16_t lsc[TILE];
+    __shared__ int32_t lmt;
+    __shared__ uint32_t flag;
+    const TileWg wg = tile_wg(a);
+    if (!wg.valid) return;                        // padding
+    const uint32_t n = a.pos0 + wg.t + 1;
+    if (wg.tile * TILE >= n) return;              // beyond this row's context
+    tile_scores_phase<D, true>(a, wg, sm.s, lsc, &lmt);
+    const uint32_t ntiles = (n + TILE - 1) / TILE;
+    uint32_t* maxc = tile_max_counter(a, wg.t, wg.g);
+    arrive(maxc + (wg.tile / kArriveGroup) * kCounterStride);  // also ends phase 1's LDS use
+    tile_pv_phase<D, true>(a, wg, sm.p, lsc, &lmt, [&] {
+        return wait_counts(
+            maxc, kCounterStride, tile_groups(ntiles),
+            [&](uint32_t l) {
+                return ntiles - l * kArriveGroup < kArriveGroup ? ntiles - l * kArriveGroup
+                                                                : kArriveGroup;
+            },
+            a.wait_limit, a.abort, a.host_abort, &flag);
+    });
+}
+
+// Workgroups of the one-launch tile path the device holds at once.
+template <int D>
+uint32_t tile_fused_capacity(uint32_t cus) {
+    static int per_cu = -1;
+    if (per_cu < 0) {
+        int nb = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                &nb, reinterpret_cast<const void*>(&attention_tile_fused_kernel<D>), 2 * D, 0) !=
+            hipSuccess)
+            nb = 0;
+        per_cu = nb;
+    }
+    return (uint32_t)per_cu * cus;
+}
+template <int D>
 static hipError_t launch_d(const AttnArgs& a, uint32_t rows, uint32_t kv_heads,
                            uint32_t chunks, hipStream_t st) {
     const uint32_t tiles = (a.pos0 + rows + TILE - 1) / TILE;
@@ -1425,6 +1528,11 @@ static hipError_t launch_d(const AttnArgs& a, uint32_t rows, uint32_t kv_heads,
         g.grid_rows = rows;
         g.grid_tiles = tiles;
         const uint32_t grid = tile_grid(rows, tiles, a.num_kv_heads, a.group);
+        if (a.tile_fused && a.tmax_count && tiles <= kTileFusedMaxTiles &&
+            grid <= tile_fused_capacity<DT>(a.cus)) {
+            attention_tile_fused_kernel<DT><<<grid, 2 * D, 0, st>>>(g);
+            return hipGetLastError();
+        }
         attention_tile_scores_kernel<DT><<<grid, 2 * D, 0, st>>>(g);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;

@@ -60,7 +60,13 @@ struct ProjArgs {
     // chunk to arrive (mf_count) finishes it.
     int32_t* mf_part;
     uint32_t* mf_count;
+    // 12-bit copies of w0 / w1 ("p12", see proj_p12_kernel), for matrices
+    // whose weights all lie in [-2048, 2047]; null when absent.
+    const uint8_t* p0;
+    const uint8_t* p1;
 };
+// Bytes of the p12 copy per 4-row block and k-step.
+constexpr uint32_t kP12Step = 768;
 
 // Matrix-core layout: record (c, q) of 2048 bytes holds outputs 16c..16c+15
 // and inputs 64q..64q+63: bytes [0, 1024) the high bytes w >> 8, bytes
@@ -105,6 +111,9 @@ MfSplit mf_split(uint32_t nc, uint32_t kq);
 // int32 words of partial sums per (chunk, part) record.
 constexpr uint32_t mf_part_words(uint32_t nm) { return nm * 2 * 256 + 32; }
 bool proj_uses_mfma(const ProjArgs& a, int epi);
+// Single rows read the p12 copy when every matrix of the launch has one
+// (and a wavefront's share of K fits the kernel).
+bool proj_uses_p12(const ProjArgs& a);
 hipError_t launch_proj(const ProjArgs& a, int epi, int L, uint32_t blocks,
                        hipStream_t st);
 // RMSNorm of `rows` rows; const_gain > 0 selects the elementwise kernel

@@ -274,6 +274,126 @@ __global__ __launch_bounds__(64 * WPB) void proj_kernel(ProjArgs a) {
 }
 
 // ---------------------------------------------------------------------
+// Projection over 12-bit weights ("p12"), for matrices whose weights all
+// lie in [-2048, 2047]: w + 2048 = 256 h + l with l a byte and h a nibble,
+// so that sum_k w x = 256 sum h x + sum l x - 2048 sum x, every term an
+// exact integer (the same sums as the 16-bit kernel, 3/4 of its bytes).
+// Per 4-row block and k-step 768 bytes: the l bytes of lane (i, j) (row i,
+// columns 8j..8j+7) at 8 (16 i + j), then its h nibbles as one word at
+// 512 + 4 (16 i + j), column 2m in bits 4m..4m+3 and column 2m + 1 in bits
+// 16 + 4m..16 + 4m + 3, so that (word >> 4m) & 0x000F000F is the int16
+// pair of columns (2m, 2m + 1).  A wavefront holds at most SPW k-steps,
+// all loaded before the first product; partial sums stay in int32
+// (SPW <= 32: |sum l x| <= 8 SPW 255 2^15 < 2^31).
+// ---------------------------------------------------------------------
+template <int RT, int EPI, int WPB, int SPW>
+__global__ __launch_bounds__(64 * WPB) void proj_p12_kernel(ProjArgs a) {
+    static_assert(SPW <= 32, "int32 partial sums");
+    static_assert(EPI == EPI_SILU || EPI == EPI_RESID, "the FFN epilogues only");
+    constexpr int NM = EPI == EPI_SILU ? 2 : 1;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int i = lane >> 4, j = lane & 15;
+    const uint32_t b = blockIdx.x;
+    const int et = threadIdx.x;
+    const uint32_t en = b * 4 + et / RT, er = et % RT;
+    const bool eout = et < 4 * RT && er < a.rows && en < a.n;
+    EpiIn ei{0, 0, 0};
+    if (eout) ei = epi_fetch<EPI>(a, er, en);
+    const uint32_t fn = b * 4 + (et >> 3), fr = et & 7;
+    const bool efill = EPI == EPI_RESID && a.final_out && et < 32 && fr >= a.rows && fn < a.n;
+    int16_t fill = 0;
+    if (efill) fill = a.res[(size_t)fr * a.ldr + fn];
+    const uint32_t S = a.steps;
+    const uint32_t s0 = wave * S / WPB, s1 = (wave + 1) * S / WPB;
+    const uint32_t cnt = s1 - s0;  // <= SPW (the launcher's choice)
+
+    const uint8_t* wp[NM];
+    wp[0] = a.p0 + (size_t)(b * S + s0) * 768;
+    if (NM == 2) wp[NM - 1] = a.p1 + (size_t)(b * S + s0) * 768;
+    const int16_t* xp = a.x + (size_t)s0 * 128 + j * 8;
+    uint2 lo[SPW][NM];
+    uint32_t hi[SPW][NM];
+    uint4 xv[SPW][RT];
+#pragma unroll
+    for (int u = 0; u < SPW; u++) {
+        const uint32_t du = cnt == 0 ? 0 : ((uint32_t)u < cnt ? u : cnt - 1);
+#pragma unroll
+        for (int m = 0; m < NM; m++) {
+            lo[u][m] = *(const uint2*)(wp[m] + (size_t)du * 768 + 8 * lane);
+            hi[u][m] = *(const uint32_t*)(wp[m] + (size_t)du * 768 + 512 + 4 * lane);
+        }
+#pragma unroll
+        for (int r = 0; r < RT; r++) xv[u][r] = *(const uint4*)(xp + (size_t)r * a.ldx + du * 128);
+    }
+    int32_t pl[NM][RT], ph[NM][RT], sx[RT];
+#pragma unroll
+    for (int r = 0; r < RT; r++) {
+        sx[r] = 0;
+#pragma unroll
+        for (int m = 0; m < NM; m++) pl[m][r] = 0, ph[m][r] = 0;
+    }
+    // steps past the wavefront's last carry zero activations (no branch
+    // between a load and its use)
+#pragma unroll
+    for (int u = 0; u < SPW; u++) {
+        const uint32_t keep = lane_mask((uint32_t)u < cnt);
+#pragma unroll
+        for (int r = 0; r < RT; r++) {
+            const uint4 x = and4(xv[u][r], keep);
+            sx[r] = dot2(0x00010001u, x.x, sx[r]);
+            sx[r] = dot2(0x00010001u, x.y, sx[r]);
+            sx[r] = dot2(0x00010001u, x.z, sx[r]);
+            sx[r] = dot2(0x00010001u, x.w, sx[r]);
+#pragma unroll
+            for (int m = 0; m < NM; m++) {
+                const uint2 l8 = lo[u][m];
+                const uint32_t h4 = hi[u][m];
+                int32_t p = pl[m][r], q = ph[m][r];
+                p = dot2(__builtin_amdgcn_perm(0u, l8.x, 0x0c010c00u), x.x, p);
+                p = dot2(__builtin_amdgcn_perm(0u, l8.x, 0x0c030c02u), x.y, p);
+                p = dot2(__builtin_amdgcn_perm(0u, l8.y, 0x0c010c00u), x.z, p);
+                p = dot2(__builtin_amdgcn_perm(0u, l8.y, 0x0c030c02u), x.w, p);
+                q = dot2(h4 & 0x000f000fu, x.x, q);
+                q = dot2((h4 >> 4) & 0x000f000fu, x.y, q);
+                q = dot2((h4 >> 8) & 0x000f000fu, x.z, q);
+                q = dot2((h4 >> 12) & 0x000f000fu, x.w, q);
+                pl[m][r] = p;
+                ph[m][r] = q;
+            }
+        }
+    }
+    int64_t acc[NM][RT];
+#pragma unroll
+    for (int m = 0; m < NM; m++)
+#pragma unroll
+        for (int r = 0; r < RT; r++) {
+            acc[m][r] = 256 * (int64_t)ph[m][r] + pl[m][r] - 2048 * (int64_t)sx[r];
+#pragma unroll
+            for (int off = 8; off > 0; off >>= 1) acc[m][r] += __shfl_xor(acc[m][r], off, 64);
+        }
+    __shared__ int64_t red[WPB][NM][4][RT];
+    if (j == 0) {
+#pragma unroll
+        for (int m = 0; m < NM; m++)
+#pragma unroll
+            for (int r = 0; r < RT; r++) red[wave][m][i][r] = acc[m][r];
+    }
+    __syncthreads();
+    if (eout) {
+        const int ii = et / RT;
+        int64_t tot[NM];
+#pragma unroll
+        for (int m = 0; m < NM; m++) {
+            tot[m] = 0;
+#pragma unroll
+            for (int w = 0; w < WPB; w++) tot[m] += red[w][m][ii][er];
+        }
+        proj_out<EPI>(a, er, en, tot[0], tot[NM - 1], ei, a.exp8);
+    }
+    if (efill) a.final_out[(size_t)fr * a.ldn + fn] = fill;
+}
+
+// ---------------------------------------------------------------------
 // Projection on the matrix cores, for blocks of several rows.
 //
 // int16 operands are split into bytes, w = 256 a + b + 128 and
@@ -691,9 +811,33 @@ static hipError_t launch_proj_rt(const ProjArgs& a, int L, uint32_t blocks,
     return launch_proj_w<RT, EPI, LLM_PROJ_WPB>(a, L, blocks, st);
 }
 
+// The p12 kernel (FFN epilogues, one row): gate|up with 8 wavefronts
+// per block, the down projection with 16 (as the 16-bit kernel's long
+// reductions), every wavefront's steps loaded at once; proj_uses_p12
+// bounds the steps per wavefront by 8.
+template <int RT, int EPI, int W>
+static hipError_t launch_p12_w(const ProjArgs& a, uint32_t blocks, hipStream_t st) {
+    const uint32_t spw = (a.steps + W - 1) / W;
+    // the smallest variant that holds the steps (registers decide how many
+    // 16-wavefront blocks a compute unit holds)
+    if (spw <= 2) proj_p12_kernel<RT, EPI, W, 2><<<blocks, 64 * W, 0, st>>>(a);
+    else if (spw <= 4) proj_p12_kernel<RT, EPI, W, 4><<<blocks, 64 * W, 0, st>>>(a);
+    else if (spw <= 6) proj_p12_kernel<RT, EPI, W, 6><<<blocks, 64 * W, 0, st>>>(a);
+    else proj_p12_kernel<RT, EPI, W, 8><<<blocks, 64 * W, 0, st>>>(a);
+    return hipGetLastError();
+}
+template <int RT, int EPI>
+static hipError_t launch_p12_rt(const ProjArgs& a, uint32_t blocks, hipStream_t st) {
+    if constexpr (EPI == EPI_SILU) return launch_p12_w<RT, EPI, 8>(a, blocks, st);
+    else return launch_p12_w<RT, EPI, 16>(a, blocks, st);
+}
+
 template <int EPI>
 static hipError_t launch_proj_epi(const ProjArgs& a, int L, uint32_t blocks,
                                   hipStream_t st) {
+    if constexpr (EPI == EPI_SILU || EPI == EPI_RESID) {
+        if (proj_uses_p12(a)) return launch_p12_rt<1, EPI>(a, blocks, st);
+    }
     if (a.rows <= 1) return launch_proj_rt<1, EPI>(a, L, blocks, st);
     if (a.rows <= 2) return launch_proj_rt<2, EPI>(a, L, blocks, st);
     if (a.rows <= 4) return launch_proj_rt<4, EPI>(a, L, blocks, st);
@@ -752,6 +896,14 @@ static hipError_t launch_mfma_epi(const ProjArgs& a, hipStream_t st) {
 
 bool proj_uses_mfma(const ProjArgs& a, int epi) {
     return a.rows >= kMfMinRows && a.mf0 && a.mf_part && a.kq * kMfCols <= 32768;
+}
+
+bool proj_uses_p12(const ProjArgs& a) {
+    // one row (two rows measured slower than the 16-bit kernel: the
+    // unpacking is paid per activation row), at most 8 k-steps per
+    // wavefront: 8 wavefronts for gate|up, 16 else
+    return a.rows == 1 && a.p0 && (a.w1 == nullptr || a.p1) &&
+           a.steps <= (a.w1 ? 8u * 8u : 16u * 8u);
 }
 
 hipError_t launch_proj(const ProjArgs& a, int epi, int L, uint32_t blocks,

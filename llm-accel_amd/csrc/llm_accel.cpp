@@ -75,6 +75,10 @@ struct Matrix {
     int32_t* ctx_part = nullptr;     // the context's split scratch
     uint32_t* ctx_count = nullptr;
     int maxw[3] = {0, 0, 0};  // per stored projection (qkv keeps three)
+    // 12-bit copy (gate, up, down): p12_ok once loaded weights all lie in
+    // [-2048, 2047]
+    uint8_t* p12 = nullptr;
+    bool p12_ok = false;
     int L = 16;               // int32 widening interval in k-steps
     size_t elems() const { return (size_t)n_pad * k_pad; }
 };
@@ -129,6 +133,7 @@ struct llm_ctx {
     int32_t* s_tsum = nullptr;
     int16_t* s_tval = nullptr;
     uint32_t* counters = nullptr;
+    size_t counter_bytes = 0, tmax_count_bytes = 0;
     // fused attention sublayer: arrival counters (growing across launches)
     // and the host-visible word a kernel sets when one of its waits gave up
     uint32_t* sync = nullptr;
@@ -139,6 +144,14 @@ struct llm_ctx {
     // ones run faster with a workgroup per query head and tile);
     // LLM_ACCEL_GQA_MIN_TILES overrides it
     uint32_t gqa_min_tiles = 64;
+    // the tile path (5-64 tiles) in one launch when the grid fits on the
+    // device at once; LLM_ACCEL_TILE_FUSED=0 keeps its two launches
+    bool tile_fused = true;
+    // 12-bit copies of the FFN matrices for single decode rows (weights in
+    // [-2048, 2047]); LLM_ACCEL_P12=0 keeps the 16-bit copies only
+    bool p12 = true;
+    int32_t* s_tmax32 = nullptr;       // tile maxima published in that launch
+    uint32_t* tmax_count = nullptr;    // its arrival counters
     uint32_t sync_qkv[32] = {};        // QKV arrivals per line so far, mod 2^32
     uint32_t sync_attn = 0;            // attention arrivals per line, mod 2^32
     // bound of one wait (100 MHz ticks); LLM_ACCEL_WAIT_LIMIT overrides it
@@ -275,6 +288,9 @@ void harvest_timing(llm_ctx* c) {
 int check_waits(llm_ctx* c) {
     if (!c->host_abort || __atomic_load_n(c->host_abort, __ATOMIC_ACQUIRE) == 0) return 0;
     (void)hipMemsetAsync(c->sync, 0, llm::kSyncWords * 4, c->stream);
+    // counters a workgroup that left a wait early did not reset
+    (void)hipMemsetAsync(c->counters, 0, c->counter_bytes, c->stream);
+    (void)hipMemsetAsync(c->tmax_count, 0, c->tmax_count_bytes, c->stream);
     if (c->ds_sync) (void)hipMemsetAsync(c->ds_sync, 0, llm::kStackSyncWords * 4, c->stream);
     (void)hipStreamSynchronize(c->stream);
     std::fill(std::begin(c->sync_qkv), std::end(c->sync_qkv), 0u);
@@ -355,6 +371,32 @@ int upload_rows(llm_ctx* c, Matrix& m, uint32_t row0, uint32_t rows,
     const size_t off = (size_t)(row0 / 4) * S * 512;
     HIP_TRY(hipMemcpy(m.d + off, buf.data(), buf.size() * sizeof(int16_t),
                       hipMemcpyHostToDevice));
+    if (m.p12) {
+        // the 12-bit copy (layout in kernels.hip, proj_p12_kernel), built
+        // from the 16-bit tiles when every weight of the matrix fits
+        m.p12_ok = false;
+        bool fits = row0 == 0 && rows == m.n;
+        for (size_t q = 0; fits && q < buf.size(); q++) fits = buf[q] >= -2048 && buf[q] <= 2047;
+        if (fits) {
+            const size_t nsteps = (size_t)(rows_pad / 4) * S;
+            std::vector<uint8_t> pk(nsteps * llm::kP12Step, 0);
+            parallel_for((uint32_t)nsteps, [&](uint32_t bs) {
+                const int16_t* t = &buf[(size_t)bs * 512];  // [4 rows][16 lanes][8]
+                uint8_t* o = &pk[(size_t)bs * llm::kP12Step];
+                for (uint32_t ln = 0; ln < 64; ln++) {
+                    uint32_t word = 0;
+                    for (uint32_t e = 0; e < 8; e++) {
+                        const uint32_t u = (uint32_t)(t[ln * 8 + e] + 2048);
+                        o[8 * ln + e] = (uint8_t)(u & 255);
+                        word |= (u >> 8) << ((e & 1) * 16 + (e >> 1) * 4);
+                    }
+                    std::memcpy(o + 512 + 4 * ln, &word, 4);
+                }
+            });
+            HIP_TRY(hipMemcpy(m.p12, pk.data(), pk.size(), hipMemcpyHostToDevice));
+            m.p12_ok = true;
+        }
+    }
     if (m.mf) {
         // byte-plane records of the chunks these rows cover
         if (row0 % llm::kMfRows != 0)
@@ -537,6 +579,13 @@ int enqueue_attention_sublayer(llm_ctx* c, uint32_t layer, uint32_t R,
     at.chunk_tiles = c->chunk_tiles;
     at.use_gqa = c->gqa && (uint32_t)cdiv(pos + R, llm::kTile) >= c->gqa_min_tiles ? 1u : 0u;
     at.max_tiles = c->tiles;
+    at.tile_fused = c->tile_fused ? 1u : 0u;
+    at.s_tmax32 = c->s_tmax32;
+    at.tmax_count = c->tmax_count;
+    at.abort = c->sync + llm::kSyncAbort;
+    at.host_abort = c->host_abort;
+    at.wait_limit = c->wait_limit;
+    at.cus = (uint32_t)c->cus;
     at.s_scores = c->s_scores;
     at.s_tmax = c->s_tmax;
     at.s_tsum = c->s_tsum;
@@ -642,6 +691,10 @@ int enqueue_ffn_sublayer(llm_ctx* c, uint32_t layer, uint32_t R, int in_pair,
     a.rows = R;
     a.exp8 = c->exp8;
     set_mf(a, mg, &mu);
+    if (mg.p12_ok && mu.p12_ok) {
+        a.p0 = mg.p12;
+        a.p1 = mu.p12;
+    }
     {
         TimedScope ts(c, LLM_K_GATEUP);
         HIP_TRY(llm::launch_proj(a, llm::EPI_SILU, std::min(mg.L, mu.L),
@@ -660,6 +713,7 @@ int enqueue_ffn_sublayer(llm_ctx* c, uint32_t layer, uint32_t R, int in_pair,
     dn.n = md.n;
     dn.rows = R;
     set_mf(dn, md);
+    if (md.p12_ok) dn.p0 = md.p12;
     const bool next = c->const_gain > 0 && layer + 1 < c->L;
     if (c->const_gain > 0) {
         dn.ldn = c->Hp;
@@ -878,6 +932,7 @@ int llm_ctx_create(const llm_shape_t* shape, int device, uint32_t num_pairs,
         return cleanup(fail(LLM_E_HIP, "hipStreamCreate failed"));
 
     // weights
+    if (const char* e = std::getenv("LLM_ACCEL_P12")) c->p12 = std::strcmp(e, "0") != 0;
     c->mats.resize((size_t)c->L * M_COUNT);
     c->loaded.assign((size_t)c->L * 7, false);
     size_t total = 0;
@@ -899,9 +954,15 @@ int llm_ctx_create(const llm_shape_t* shape, int device, uint32_t num_pairs,
     if ((rc = dev_alloc(c, (void**)&c->arena, total * sizeof(int16_t))))
         return cleanup(rc);
     size_t off = 0;
-    for (auto& mt : c->mats) {
+    for (int idx = 0; idx < (int)c->mats.size(); idx++) {
+        Matrix& mt = c->mats[idx];
         mt.d = c->arena + off;
         off += mt.elems();
+        // 12-bit copy of the FFN matrices for single decode rows
+        const int kind = idx % M_COUNT;
+        if (c->p12 && (kind == M_GATE || kind == M_UP || kind == M_DOWN))
+            if ((rc = dev_alloc(c, (void**)&mt.p12, mt.elems() / 512 * llm::kP12Step)))
+                return cleanup(rc);
         // byte-plane copy for multi-row blocks on the matrix cores
         mt.nc = (uint32_t)cdiv(mt.n, llm::kMfRows);
         mt.kq = (uint32_t)cdiv(mt.k, llm::kMfCols);
@@ -954,6 +1015,8 @@ int llm_ctx_create(const llm_shape_t* shape, int device, uint32_t num_pairs,
         if ((rc = dev_alloc(c, (void**)&p, (size_t)8 * c->Hp * 2)))
             return cleanup(rc);
     const size_t rht = (size_t)8 * c->Hkv * c->tiles * c->G;  // rows*heads*tiles*group
+    c->counter_bytes = std::max(llm::counter_words(c->Hq, c->tiles), (size_t)8 * c->Hkv) * 4;
+    c->tmax_count_bytes = (size_t)8 * c->Hq * 4 * llm::kCounterStride * 4;
     c->exported.assign(num_pairs, 0);
     if ((rc = dev_alloc(c, (void**)&c->xn_attn, (size_t)8 * c->Hp * 2)) ||
         (rc = dev_alloc(c, (void**)&c->xn_final, (size_t)8 * c->Hp * 2)) ||
@@ -965,8 +1028,9 @@ int llm_ctx_create(const llm_shape_t* shape, int device, uint32_t num_pairs,
         (rc = dev_alloc(c, (void**)&c->s_tmax, rht * 2)) ||
         (rc = dev_alloc(c, (void**)&c->s_tsum, rht * 4)) ||
         (rc = dev_alloc(c, (void**)&c->s_tval, rht * d * 2)) ||
-        (rc = dev_alloc(c, (void**)&c->counters,
-                        std::max(llm::counter_words(c->Hq, c->tiles), (size_t)8 * c->Hkv) * 4)) ||
+        (rc = dev_alloc(c, (void**)&c->counters, c->counter_bytes)) ||
+        (rc = dev_alloc(c, (void**)&c->s_tmax32, rht * 4)) ||
+        (rc = dev_alloc(c, (void**)&c->tmax_count, c->tmax_count_bytes)) ||
         (rc = dev_alloc(c, (void**)&c->sync, (size_t)llm::kSyncWords * 4)))
         return cleanup(rc);
     if (hipHostMalloc((void**)&c->host_abort, 64, hipHostMallocDefault) != hipSuccess)
@@ -974,6 +1038,8 @@ int llm_ctx_create(const llm_shape_t* shape, int device, uint32_t num_pairs,
     *c->host_abort = 0;
     if (const char* e = std::getenv("LLM_ACCEL_FUSED")) c->fused = std::strcmp(e, "0") != 0;
     if (const char* e = std::getenv("LLM_ACCEL_GQA")) c->gqa = std::strcmp(e, "0") != 0;
+    if (const char* e = std::getenv("LLM_ACCEL_TILE_FUSED"))
+        c->tile_fused = std::strcmp(e, "0") != 0;
     if (const char* e = std::getenv("LLM_ACCEL_GQA_MIN_TILES"))
         c->gqa_min_tiles = (uint32_t)std::strtoul(e, nullptr, 10);
     if (hipDeviceGetAttribute(&c->cus, hipDeviceAttributeMultiprocessorCount, c->device) !=
@@ -1824,6 +1890,7 @@ int llm_bench_projection(llm_ctx_t* c, uint32_t kernel, uint32_t rows,
             a.out = c->qkv; a.ldo = c->Nqkv; a.res = c->xn_ffn; a.ldr = c->Hp;
             a.n = m.n; L = m.L; blocks = m.n_pad / 4; epi = llm::EPI_RESID;
             set_mf(a, m);
+            if (m.p12_ok) a.p0 = m.p12;
         } else {
             const Matrix& g = c->mat(layer, M_GATE);
             const Matrix& u = c->mat(layer, M_UP);
@@ -1832,6 +1899,10 @@ int llm_bench_projection(llm_ctx_t* c, uint32_t kernel, uint32_t rows,
             a.exp8 = c->exp8; L = std::min(g.L, u.L); blocks = g.n_pad / 4;
             epi = llm::EPI_SILU;
             set_mf(a, g, &u);
+            if (g.p12_ok && u.p12_ok) {
+                a.p0 = g.p12;
+                a.p1 = u.p12;
+            }
         }
         return llm::launch_proj(a, epi, L, blocks, c->stream);
     };

@@ -238,3 +238,57 @@ def test_fused_long_mixed_sequence(start):
                     assert err is None, f"op {op} layer {layer} at {pos}: {err}"
                     cur = want
                     pin, pout = pout, pin
+
+
+def test_tile_path_wait_timeout_is_reported():
+    """The one-launch tile path (decode row at 5 tiles) with a 0-tick wait
+    bound: the launch ends (every wait is bounded); either every wait was
+    already satisfied at its first poll and the row equals the oracle's, or
+    the next synchronisation reports the time-out and the one after is
+    clean.  An 8-row block that does not wait (2 tiles) then matches the
+    oracle."""
+    import llm_accel
+    spec = workloads.CONFIG_B
+    n = 300
+    synth = workloads.SyntheticModel(spec, seed=workloads.SEED, layers=1)
+    om = oracle_from_synthetic(synth, oracle_shape(spec, layers=1, max_seq=512))
+    kc, vc = om.new_kv()
+    acc = _accel(spec, 1, 512, {"LLM_ACCEL_WAIT_LIMIT": "0"})
+    with acc:
+        acc.load_model(synth)
+        for h in range(spec.kv_heads):
+            k, v = synth.kv_rows(n, seed_offset=80 + h)
+            kc[0, h, :n], vc[0, h, :n] = k, v
+            acc.kv_write(0, h, 0, k, v)
+        x = synth.hidden_rows(1, seed_offset=81)
+        acc.upload(2, x)
+        _say(f"case tile path 0-tick wait bound n={n}")
+        rc, _ = acc.task(18, 0, 1, n, 2, 0)
+        assert rc == 0
+        try:
+            acc.sync()
+            timed_out = False
+        except llm_accel.AccelError as e:
+            assert "timed out" in str(e)
+            timed_out = True
+        acc.sync()  # clean either way
+        if not timed_out:
+            _, want, _ = om.task((kc, vc), 18, 0, x, n)
+            assert first_mismatch(acc.download(0, 1), want) is None
+        else:
+            # the aborted launch may have appended position n on the GPU:
+            # give the oracle the same row
+            for h in range(spec.kv_heads):
+                k, v = acc.kv_read(0, h, n, 1)
+                kc[0, h, n], vc[0, h, n] = k[0], v[0]
+        # an 8-row block at positions 100-107 (split-head path, no waits)
+        h8 = synth.hidden_rows(8, seed_offset=82)
+        acc.upload(3, h8)
+        _say("case 8-row block after the tile-path wait")
+        rc, _ = acc.task(18, 0, 8, 100, 3, 1)
+        assert rc == 0
+        got = acc.download(1, 8)
+    kc2, vc2 = kc.copy(), vc.copy()
+    code, want, _ = om.task((kc2, vc2), 18, 0, h8, 100)
+    assert code == 0
+    assert first_mismatch(got, want) is None

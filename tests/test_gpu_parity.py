@@ -419,6 +419,33 @@ def test_running_max_rises_often(n, period):
         assert first_mismatch(kv_got[h][1], vc[0, h, n:n + 1]) is None
 
 
+@pytest.mark.parametrize("cfg,n,rows", [("B", 1024, 1), ("B", 1150, 2), ("A", 4030, 2),
+                                         ("B", 4031, 1), ("A", 300, 1), ("B", 2047, 2)])
+def test_tile_path_one_launch(cfg, n, rows):
+    """Decode rows at 5-63 tiles take the tile path in one launch (tile
+    maxima exchanged between the workgroups of the launch); up to 63
+    tiles, both head_dims, blocks across a tile boundary."""
+    test_block_across_tile_boundary_late_context(cfg, n, rows)
+
+
+@pytest.fixture
+def tile_two_launches(monkeypatch):
+    """The tile path as two launches (scores, then PV and recurrence)."""
+    monkeypatch.setenv("LLM_ACCEL_TILE_FUSED", "0")
+
+
+@pytest.mark.parametrize("cfg,n,rows", [("B", 1024, 1), ("A", 382, 1), ("B", 255, 2),
+                                         ("A", 4030, 2)])
+def test_tile_path_two_launches(tile_two_launches, cfg, n, rows):
+    test_block_across_tile_boundary_late_context(cfg, n, rows)
+
+
+def test_tile_path_one_launch_running_max_rises(monkeypatch):
+    # every tile raises the running max (the recurrence's rescaling path)
+    monkeypatch.setenv("LLM_ACCEL_GQA_MIN_TILES", "1000")
+    test_running_max_rises_often(2048, 1)
+
+
 @pytest.fixture
 def gqa_everywhere(monkeypatch):
     """Contexts of 5 tiles and more take the GQA tile path (by default it
