@@ -289,7 +289,6 @@ __global__ __launch_bounds__(64 * WPB) void proj_kernel(ProjArgs a) {
 template <int RT, int EPI, int WPB, int SPW>
 __global__ __launch_bounds__(64 * WPB) void proj_p12_kernel(ProjArgs a) {
     static_assert(SPW <= 32, "int32 partial sums");
-    static_assert(EPI == EPI_SILU || EPI == EPI_RESID, "the FFN epilogues only");
     constexpr int NM = EPI == EPI_SILU ? 2 : 1;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int i = lane >> 4, j = lane & 15;
@@ -313,7 +312,7 @@ __global__ __launch_bounds__(64 * WPB) void proj_p12_kernel(ProjArgs a) {
     const int16_t* xp = a.x + (size_t)s0 * 128 + j * 8;
     uint2 lo[SPW][NM];
     uint32_t hi[SPW][NM];
-    uint4 xv[SPW][RT];
+    uint4 xv[SPW][RT], gv[SPW];
 #pragma unroll
     for (int u = 0; u < SPW; u++) {
         const uint32_t du = cnt == 0 ? 0 : ((uint32_t)u < cnt ? u : cnt - 1);
@@ -324,6 +323,8 @@ __global__ __launch_bounds__(64 * WPB) void proj_p12_kernel(ProjArgs a) {
         }
 #pragma unroll
         for (int r = 0; r < RT; r++) xv[u][r] = *(const uint4*)(xp + (size_t)r * a.ldx + du * 128);
+        if (EPI == EPI_STORE_NORM_IN)  // the norm table is padded to whole k-steps
+            gv[u] = *(const uint4*)(a.in_gamma + (s0 + du) * 128 + j * 8);
     }
     int32_t pl[NM][RT], ph[NM][RT], sx[RT];
 #pragma unroll
@@ -339,7 +340,9 @@ __global__ __launch_bounds__(64 * WPB) void proj_p12_kernel(ProjArgs a) {
         const uint32_t keep = lane_mask((uint32_t)u < cnt);
 #pragma unroll
         for (int r = 0; r < RT; r++) {
-            const uint4 x = and4(xv[u][r], keep);
+            const uint4 x = and4(EPI == EPI_STORE_NORM_IN ? norm8(xv[u][r], gv[u], a.in_gain)
+                                                          : xv[u][r],
+                                 keep);
             sx[r] = dot2(0x00010001u, x.x, sx[r]);
             sx[r] = dot2(0x00010001u, x.y, sx[r]);
             sx[r] = dot2(0x00010001u, x.z, sx[r]);
@@ -811,9 +814,9 @@ static hipError_t launch_proj_rt(const ProjArgs& a, int L, uint32_t blocks,
     return launch_proj_w<RT, EPI, LLM_PROJ_WPB>(a, L, blocks, st);
 }
 
-// The p12 kernel (FFN epilogues, one row): gate|up with 8 wavefronts
-// per block, the down projection with 16 (as the 16-bit kernel's long
-// reductions), every wavefront's steps loaded at once; proj_uses_p12
+// The p12 kernel (one row): gate|up with 8 wavefronts per block, long
+// reductions (the down projection) with 16 and the others with 4, as the
+// 16-bit kernel; every wavefront's steps loaded at once; proj_uses_p12
 // bounds the steps per wavefront by 8.
 template <int RT, int EPI, int W>
 static hipError_t launch_p12_w(const ProjArgs& a, uint32_t blocks, hipStream_t st) {
@@ -828,16 +831,18 @@ static hipError_t launch_p12_w(const ProjArgs& a, uint32_t blocks, hipStream_t s
 }
 template <int RT, int EPI>
 static hipError_t launch_p12_rt(const ProjArgs& a, uint32_t blocks, hipStream_t st) {
-    if constexpr (EPI == EPI_SILU) return launch_p12_w<RT, EPI, 8>(a, blocks, st);
-    else return launch_p12_w<RT, EPI, 16>(a, blocks, st);
+    if constexpr (EPI == EPI_SILU) {
+        return launch_p12_w<RT, EPI, LLM_PROJ_WPB_SILU>(a, blocks, st);
+    } else {
+        if (a.steps >= LLM_PROJ_LONG_STEPS) return launch_p12_w<RT, EPI, 16>(a, blocks, st);
+        return launch_p12_w<RT, EPI, LLM_PROJ_WPB>(a, blocks, st);
+    }
 }
 
 template <int EPI>
 static hipError_t launch_proj_epi(const ProjArgs& a, int L, uint32_t blocks,
                                   hipStream_t st) {
-    if constexpr (EPI == EPI_SILU || EPI == EPI_RESID) {
-        if (proj_uses_p12(a)) return launch_p12_rt<1, EPI>(a, blocks, st);
-    }
+    if (proj_uses_p12(a)) return launch_p12_rt<1, EPI>(a, blocks, st);
     if (a.rows <= 1) return launch_proj_rt<1, EPI>(a, L, blocks, st);
     if (a.rows <= 2) return launch_proj_rt<2, EPI>(a, L, blocks, st);
     if (a.rows <= 4) return launch_proj_rt<4, EPI>(a, L, blocks, st);
@@ -901,9 +906,10 @@ bool proj_uses_mfma(const ProjArgs& a, int epi) {
 bool proj_uses_p12(const ProjArgs& a) {
     // one row (two rows measured slower than the 16-bit kernel: the
     // unpacking is paid per activation row), at most 8 k-steps per
-    // wavefront: 8 wavefronts for gate|up, 16 else
-    return a.rows == 1 && a.p0 && (a.w1 == nullptr || a.p1) &&
-           a.steps <= (a.w1 ? 8u * 8u : 16u * 8u);
+    // wavefront with the launcher's wavefronts per block
+    const uint32_t w = a.w1 ? LLM_PROJ_WPB_SILU
+                     : (a.steps >= LLM_PROJ_LONG_STEPS ? 16u : (uint32_t)LLM_PROJ_WPB);
+    return a.rows == 1 && a.p0 && (a.w1 == nullptr || a.p1) && a.steps <= 8 * w;
 }
 
 hipError_t launch_proj(const ProjArgs& a, int epi, int L, uint32_t blocks,

@@ -75,9 +75,10 @@ struct Matrix {
     int32_t* ctx_part = nullptr;     // the context's split scratch
     uint32_t* ctx_count = nullptr;
     int maxw[3] = {0, 0, 0};  // per stored projection (qkv keeps three)
-    // 12-bit copy (gate, up, down): p12_ok once loaded weights all lie in
-    // [-2048, 2047]
+    // 12-bit copy: p12_ok once every stored projection (Q, K, V of the
+    // Q|K|V matrix, else one) is loaded with weights in [-2048, 2047]
     uint8_t* p12 = nullptr;
+    bool p12_fit[3] = {false, true, true};
     bool p12_ok = false;
     int L = 16;               // int32 widening interval in k-steps
     size_t elems() const { return (size_t)n_pad * k_pad; }
@@ -147,8 +148,8 @@ struct llm_ctx {
     // the tile path (5-64 tiles) in one launch when the grid fits on the
     // device at once; LLM_ACCEL_TILE_FUSED=0 keeps its two launches
     bool tile_fused = true;
-    // 12-bit copies of the FFN matrices for single decode rows (weights in
-    // [-2048, 2047]); LLM_ACCEL_P12=0 keeps the 16-bit copies only
+    // 12-bit copies of the weight matrices for single decode rows (weights
+    // in [-2048, 2047]); LLM_ACCEL_P12=0 keeps the 16-bit copies only
     bool p12 = true;
     int32_t* s_tmax32 = nullptr;       // tile maxima published in that launch
     uint32_t* tmax_count = nullptr;    // its arrival counters
@@ -372,11 +373,12 @@ int upload_rows(llm_ctx* c, Matrix& m, uint32_t row0, uint32_t rows,
     HIP_TRY(hipMemcpy(m.d + off, buf.data(), buf.size() * sizeof(int16_t),
                       hipMemcpyHostToDevice));
     if (m.p12) {
-        // the 12-bit copy (layout in kernels.hip, proj_p12_kernel), built
-        // from the 16-bit tiles when every weight of the matrix fits
-        m.p12_ok = false;
-        bool fits = row0 == 0 && rows == m.n;
+        // the 12-bit copy (layout in kernels.hip, proj_p12_kernel) of these
+        // rows, built from the 16-bit tiles when every weight fits
+        bool fits = true;
         for (size_t q = 0; fits && q < buf.size(); q++) fits = buf[q] >= -2048 && buf[q] <= 2047;
+        m.p12_fit[which] = fits;
+        m.p12_ok = m.p12_fit[0] && m.p12_fit[1] && m.p12_fit[2];
         if (fits) {
             const size_t nsteps = (size_t)(rows_pad / 4) * S;
             std::vector<uint8_t> pk(nsteps * llm::kP12Step, 0);
@@ -393,8 +395,8 @@ int upload_rows(llm_ctx* c, Matrix& m, uint32_t row0, uint32_t rows,
                     std::memcpy(o + 512 + 4 * ln, &word, 4);
                 }
             });
-            HIP_TRY(hipMemcpy(m.p12, pk.data(), pk.size(), hipMemcpyHostToDevice));
-            m.p12_ok = true;
+            HIP_TRY(hipMemcpy(m.p12 + (size_t)(row0 / 4) * S * llm::kP12Step, pk.data(),
+                              pk.size(), hipMemcpyHostToDevice));
         }
     }
     if (m.mf) {
@@ -553,6 +555,7 @@ int enqueue_attention_sublayer(llm_ctx* c, uint32_t layer, uint32_t R,
     a.n = mq.n;
     a.rows = R;
     set_mf(a, mq);
+    if (mq.p12_ok) a.p0 = mq.p12;  // single rows outside the fused launch
     if (norm_in) {
         a.in_gamma = c->norms + (size_t)(2 * layer) * c->H;
         a.in_gain = c->const_gain;
@@ -613,6 +616,7 @@ int enqueue_attention_sublayer(llm_ctx* c, uint32_t layer, uint32_t R,
     o.n = mo.n;
     o.rows = R;
     set_mf(o, mo);
+    if (mo.p12_ok) o.p0 = mo.p12;
     if (c->const_gain > 0) {  // FFN norm of this sublayer's output
         o.norm_out = c->xn_ffn;
         o.ldn = c->Hp;
@@ -958,9 +962,9 @@ int llm_ctx_create(const llm_shape_t* shape, int device, uint32_t num_pairs,
         Matrix& mt = c->mats[idx];
         mt.d = c->arena + off;
         off += mt.elems();
-        // 12-bit copy of the FFN matrices for single decode rows
-        const int kind = idx % M_COUNT;
-        if (c->p12 && (kind == M_GATE || kind == M_UP || kind == M_DOWN))
+        // 12-bit copy for single decode rows
+        if (idx % M_COUNT == M_QKV) mt.p12_fit[1] = mt.p12_fit[2] = false;
+        if (c->p12)
             if ((rc = dev_alloc(c, (void**)&mt.p12, mt.elems() / 512 * llm::kP12Step)))
                 return cleanup(rc);
         // byte-plane copy for multi-row blocks on the matrix cores
@@ -1881,6 +1885,7 @@ int llm_bench_projection(llm_ctx_t* c, uint32_t kernel, uint32_t rows,
             a.w0 = m.d; a.steps = m.steps; a.x = c->xn_attn; a.ldx = c->Hp;
             a.out = c->qkv; a.ldo = c->Nqkv; a.n = m.n; L = m.L; blocks = m.n_pad / 4;
             set_mf(a, m);
+            if (m.p12_ok) a.p0 = m.p12;
         } else if (kernel == LLM_K_OPROJ || kernel == LLM_K_DOWN) {
             const Matrix& m = c->mat(layer, kernel == LLM_K_OPROJ ? M_O : M_DOWN);
             a.w0 = m.d; a.steps = m.steps;

@@ -98,3 +98,58 @@ def test_ffn_p12_matches_oracle_and_16bit(cfg, case):
         assert code == 0
         assert first_mismatch(outs["1"][k], want) is None, f"p12 rows={rows}"
         assert first_mismatch(outs["0"][k], want) is None, f"16-bit rows={rows}"
+
+
+@pytest.mark.parametrize("cfg", ["A", "B"])
+@pytest.mark.parametrize("case", ["extremes", "v_outlier", "o_outlier"])
+def test_attention_p12_matches_oracle_and_16bit(cfg, case):
+    """Task 18 of one row at 5 tiles (separate QKV, attention and O
+    launches; the QKV launch normalises its input on load) over Q / K / V / O
+    weights that reach -2048 and 2047; one weight past 12 bits in V (the
+    whole Q|K|V matrix keeps 16 bits) or in O."""
+    spec = workloads.CONFIG_A if cfg == "A" else workloads.CONFIG_B
+    n = 300
+    synth = workloads.SyntheticModel(spec, layers=1)
+    edits = {(0, p): _extremes for p in range(4)}
+    if case == "v_outlier":
+        edits[(0, 2)] = _outlier
+    if case == "o_outlier":
+        edits[(0, 3)] = _outlier
+    model = _Edited(synth, edits)
+    om = oracle_from_synthetic(model, oracle_shape(spec, layers=1, max_seq=n + 8))
+    kc, vc = om.new_kv()
+    pre = [synth.kv_rows(n, seed_offset=90 + h) for h in range(spec.kv_heads)]
+    for h in range(spec.kv_heads):
+        kc[0, h, :n], vc[0, h, :n] = pre[h]
+    x = np.random.default_rng(6).integers(-20000, 20000, (1, spec.hidden)).astype(np.int16)
+    outs = {}
+    for p12 in ("1", "0"):
+        import llm_accel
+        old = {k: os.environ.get(k) for k in ("LLM_ACCEL_P12", "LLM_ACCEL_STACK")}
+        os.environ.update({"LLM_ACCEL_P12": p12, "LLM_ACCEL_STACK": "0"})
+        try:
+            acc = llm_accel.Accelerator(accel_shape(spec, layers=1, max_seq=n + 8))
+        finally:
+            for k, v in old.items():
+                if v is None:
+                    os.environ.pop(k, None)
+                else:
+                    os.environ[k] = v
+        with acc:
+            acc.load_model(model)
+            for h in range(spec.kv_heads):
+                acc.kv_write(0, h, 0, *pre[h])
+            acc.upload(2, x)
+            _say(f"case attention {cfg} {case} p12={p12}")
+            rc, _ = acc.task(18, 0, 1, n, 2, 0)
+            assert rc == 0
+            outs[p12] = (acc.download(0, 1), [acc.kv_read(0, h, n, 1)
+                                              for h in range(spec.kv_heads)])
+    code, want, _ = om.task((kc, vc), 18, 0, x, n)
+    assert code == 0
+    for p12 in ("1", "0"):
+        got, kv = outs[p12]
+        assert first_mismatch(got, want) is None, f"p12={p12}"
+        for h in range(spec.kv_heads):
+            assert np.array_equal(kv[h][0], kc[0, h, n:n + 1])
+            assert np.array_equal(kv[h][1], vc[0, h, n:n + 1])
