@@ -44,12 +44,11 @@ struct AttnArgs {
     int32_t* c_tsum;      // [8][kv_heads][max_chunks][group]
     int32_t* c_sum;       // [8][kv_heads][max_chunks][group][head_dim]
     // tile path in one launch (up to 64 tiles): tile maxima published
-    // during the launch, arrival counters per (row, query head) (4 lines
-    // kCounterStride words apart, zero between launches), the bounded
-    // wait's abort words and limit, and the device's compute units
+    // during the launch (flag | value, zero between launches; the flagged
+    // tile sums use s_tsum), the bounded wait's abort words and limit, and
+    // the device's compute units
     uint32_t tile_fused;
     int32_t* s_tmax32;    // [8][kv_heads][max_tiles][group]
-    uint32_t* tmax_count; // [8][num_heads][4][kCounterStride]
     uint32_t* abort;      // device word set when a wait gave up
     uint32_t* host_abort; // host-visible copy
     uint32_t wait_limit;  // bound of one wait (100 MHz ticks)

@@ -1010,6 +1010,7 @@ struct __attribute__((aligned(16))) TilePvSmem {
     int16_t p[NWH][TILE], cp[NWH][TILE];  // per wavefront: probabilities, c(p)
     int16_t e14[2056];                    // Q2.14 exp table
     uint32_t last;
+    int32_t m0;                           // one-launch path: running max before the tile
     union __attribute__((aligned(16))) {
         int16_t scr[NWH][SLICE_SCRATCH];  // per wavefront: slice transposes
         struct {                          // then the recurrence operands of up
@@ -1058,18 +1059,17 @@ __host__ __device__ inline uint32_t tile_grid(uint32_t rows, uint32_t tiles, uin
     return 8 * group * ((rows * tiles * kv_heads + 7) / 8);
 }
 
-// Counters of the one-launch tile path: per (row, query head) one line per
-// group of kArriveGroup tiles, counting the tiles whose maximum has been
-// published (at most 64 tiles: 4 lines).
-constexpr uint32_t kTileFusedMaxTiles = 4 * kArriveGroup;
-__device__ __forceinline__ uint32_t* tile_max_counter(const AttnArgs& a, uint32_t t,
-                                                      uint32_t g) {
-    return a.tmax_count + ((size_t)t * a.num_heads + g) * 4 * kCounterStride;
-}
+// One-launch tile path: a (row, query head) has at most 64 tiles (one
+// polling lane per tile).  Its tile maxima and tile sums carry a flag bit
+// in the same word (zero between launches: the workgroup that combines the
+// tiles clears them).
+constexpr uint32_t kTileFusedMaxTiles = 64;
+constexpr uint32_t kMaxValid = 0x10000u;     // s_tmax32: flag | (uint16) maximum
+constexpr uint32_t kSumValid = 0x80000000u;  // s_tsum: flag | tile sum (< 2^21)
 
 // Phase 1 of the tile path for a workgroup inside the row's context: the
 // tile's scores and their maximum; FUSED keeps the scores in LDS (lsc, lmt)
-// and publishes the maximum with a device-coherent store.
+// and publishes the flagged maximum with a device-coherent store.
 template <int D, bool FUSED>
 __device__ __forceinline__ void tile_scores_phase(const AttnArgs& a, const TileWg& wg,
                                                   TileScoresSmem<D>& sm, int16_t* lsc,
@@ -1185,7 +1185,7 @@ __device__ __forceinline__ void tile_scores_phase(const AttnArgs& a, const TileW
             lsc[lane] = (int16_t)s;
             if (lane == 0) {
                 *lmt = mx;
-                st_coherent(&a.s_tmax32[base], mx);
+                st_coherent(&a.s_tmax32[base], (int32_t)(kMaxValid | (uint16_t)mx));
             }
         } else {
             a.s_scores[base * TILE + lane] = (int16_t)s;
@@ -1218,15 +1218,17 @@ __device__ __forceinline__ void slice_load_v(const AttnArgs& a, uint32_t h, uint
 
 // Phase 2 of the tile path for a workgroup inside the row's context: the
 // tile's probabilities under the running max, their sum, its PV values,
-// and the recurrence on the last tile of the (row, query head) to arrive.
-// Non-FUSED: the scores and maxima come from the scores launch.  FUSED:
-// this workgroup's scores are lsc / lmt, the other tiles' maxima are
-// published during this launch: wait() (after this phase's own loads are
-// issued) returns once they all are, or false when the wait gave up.
-template <int D, bool FUSED, typename Wait>
+// and the recurrence over the tiles of the (row, query head).  Non-FUSED:
+// the scores and maxima come from the scores launch, the last tile to
+// arrive runs the recurrence.  FUSED: this workgroup's scores are lsc /
+// lmt; after its own loads are issued it polls the flagged maxima of the
+// earlier tiles, publishes its PV values and then its flagged tile sum,
+// and the workgroup of the last tile polls the other tiles' sums and runs
+// the recurrence.
+template <int D, bool FUSED>
 __device__ __forceinline__ void tile_pv_phase(const AttnArgs& a, const TileWg& wg,
                                               TilePvSmem<D>& sm, const int16_t* lsc,
-                                              const int32_t* lmt, Wait&& wait) {
+                                              const int32_t* lmt) {
     static_assert(D % 32 == 0, "tile path: head_dim a multiple of 32");
     constexpr uint32_t NTH = D * 2;
     constexpr int NE = (257 + NTH - 1) / NTH;    // exp table pieces per thread
@@ -1275,12 +1277,17 @@ __device__ __forceinline__ void tile_pv_phase(const AttnArgs& a, const TileWg& w
     SplitRegs regs;
     slice_load_v<D>(a, h, tile, w, lane, regs);
     if (FUSED) {
-        if (!wait()) return;
+        // lane j < tile of wavefront 0 polls tile j's maximum
+        // (tile < kTileFusedMaxTiles); their maximum goes through LDS
+        uint32_t v = 0;
+        if (!poll_flags((const uint32_t*)&a.s_tmax32[rh * a.max_tiles * G + gi], G, tile,
+                        kMaxValid, &v, a.wait_limit, a.abort, a.host_abort, &sm.last))
+            return;
         sc = lsc[lane];
         mt = *lmt;
-        for (uint32_t j = lane; j < tile; j += 64) {  // tile < kTileFusedMaxTiles
-            const int32_t v = ld_coherent(&a.s_tmax32[(rh * a.max_tiles + j) * G + gi]);
-            mprev = v > mprev ? v : mprev;
+        if (w == 0) {
+            const int32_t mx = wave_max(lane < tile ? (int32_t)(int16_t)(v & 0xffffu) : INT16_MIN);
+            if (lane == 0) sm.m0 = mx;
         }
     }
 #pragma unroll
@@ -1295,7 +1302,7 @@ __device__ __forceinline__ void tile_pv_phase(const AttnArgs& a, const TileWg& w
     }
     lds_barrier();
     // ---- probabilities under the running max after this tile ----
-    const int32_t m0 = wave_max(mprev);        // running max before the tile
+    const int32_t m0 = FUSED ? sm.m0 : wave_max(mprev);  // running max before the tile
     const int32_t mn = mt > m0 ? mt : m0;      // and after it
     const bool valid = tile * TILE + lane < n;
     const int32_t pr = valid ? prob(sm.e14, sc - mn) : 0;
@@ -1352,21 +1359,32 @@ __device__ __forceinline__ void tile_pv_phase(const AttnArgs& a, const TileWg& w
         const uint64_t q4 = (uint64_t)((uint16_t)tv | (t1 << 16)) | ((uint64_t)(t2 | (t3 << 16)) << 32);
         if (hh == 0 && (lane & 3) == 0) st_coherent((uint64_t*)&a.s_tval[base * D + e], q4);
     }
-    if (tid == 0) st_coherent(&a.s_tsum[base], tsum);
     if (gi == 0 && own / TILE == tile && tid < D)  // this row's V into the cache
         a.vcache[page_off<D>(a, h, tile) + tid * TILE + paired(own % TILE)] = sm.kv[t][tid];
-    // ---- the last tile of this (row, query head) runs the recurrence ----
-    {
+    if (FUSED) {
+        // the PV values are performed, then the flagged sum is published
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (tid == 0) {
+            st_coherent(&a.s_tsum[base], (int32_t)(kSumValid | (uint32_t)tsum));
+            __builtin_amdgcn_s_waitcnt(0);  // before this workgroup reads it back
+        }
+        if (tile + 1 != ntiles) return;
+        // the last tile's workgroup: every earlier tile's sum is published
+        uint32_t v = 0;
+        if (!poll_flags((const uint32_t*)&a.s_tsum[rh * a.max_tiles * G + gi], G, tile,
+                        kSumValid, &v, a.wait_limit, a.abort, a.host_abort, &sm.last))
+            return;
+    } else {
+        // ---- the last tile of this (row, query head) to arrive runs the
+        // recurrence ----
+        if (tid == 0) st_coherent(&a.s_tsum[base], tsum);
         const uint32_t ng = tile_groups(a.max_tiles), grp = tile / kArriveGroup;
         uint32_t* top = a.counters + ((size_t)t * a.num_heads + g) * (1 + ng) * kCounterStride;
         const uint32_t in_grp = ntiles - grp * kArriveGroup < kArriveGroup
                                     ? ntiles - grp * kArriveGroup : kArriveGroup;
         if (!arrive_last(top + (1 + grp) * kCounterStride, in_grp, &sm.last)) return;
         if (!arrive_last(top, tile_groups(ntiles), &sm.last)) return;
-        // every workgroup of this (row, query head) has passed its wait for
-        // the maxima: their counters start the next launch at zero
-        if (FUSED && tid < tile_groups(ntiles))
-            st_coherent(tile_max_counter(a, t, g) + tid * kCounterStride, 0u);
     }
     // A tile whose maximum does not raise the running max has factor
     // exp(0) = 1.0 (rnd(v * 2^16, 16) = v): sum and acc take saturating
@@ -1392,8 +1410,13 @@ __device__ __forceinline__ void tile_pv_phase(const AttnArgs& a, const TileWg& w
         pc.tsv = 0;
         if (tid < nj) {
             const size_t b = (rh * a.max_tiles + j0 + tid) * G + gi;
-            pc.tm = FUSED ? ld_coherent(&a.s_tmax32[b]) : (int32_t)a.s_tmax[b];
-            pc.tsv = ld_coherent(&a.s_tsum[b]);
+            if (FUSED) {
+                pc.tm = (int16_t)(ld_coherent(&a.s_tmax32[b]) & 0xffff);
+                pc.tsv = (int32_t)((uint32_t)ld_coherent(&a.s_tsum[b]) & ~kSumValid);
+            } else {
+                pc.tm = a.s_tmax[b];
+                pc.tsv = ld_coherent(&a.s_tsum[b]);
+            }
         }
     };
     Piece cur;
@@ -1457,6 +1480,15 @@ __device__ __forceinline__ void tile_pv_phase(const AttnArgs& a, const TileWg& w
     if (tid < D)
         a.out[(size_t)t * a.ldo + (size_t)g * D + tid] =
             fx_sat16(fx_rnd((int64_t)acc * fx_inv_sum(sum), 16));
+    if (FUSED) {
+        // every tile of this (row, query head) has read the maxima and
+        // published its sum: clear the flags for the next launch
+        for (uint32_t j = tid; j < ntiles; j += NTH) {
+            const size_t b = (rh * a.max_tiles + j) * G + gi;
+            st_coherent(&a.s_tmax32[b], 0);
+            st_coherent(&a.s_tsum[b], 0);
+        }
+    }
 }
 
 template <int D>
@@ -1465,15 +1497,15 @@ __global__ __launch_bounds__(D * 2) void attention_tile_pv_kernel(AttnArgs a) {
     const TileWg wg = tile_wg(a);
     if (!wg.valid) return;                             // padding
     if (wg.tile * TILE >= a.pos0 + wg.t + 1) return;   // beyond this row's context
-    tile_pv_phase<D, false>(a, wg, sm, nullptr, nullptr, [] { return true; });
+    tile_pv_phase<D, false>(a, wg, sm, nullptr, nullptr);
 }
 
 // The tile path in one launch (contexts of at most kTileFusedMaxTiles
 // tiles; launched only when every workgroup of the grid fits on the device
 // at once, so that the workgroups a tile waits for are all running): the
-// scores phase, one arrival per tile after its maximum is published, the V
-// loads of the PV phase issued, then a bounded wait for every tile's
-// maximum of the (row, query head), and the PV phase.
+// scores phase, which publishes the tile's flagged maximum, and the PV
+// phase, which waits for the earlier tiles' maxima after issuing its own
+// loads; the last tile's workgroup combines the tiles.
 template <int D>
 __global__ __launch_bounds__(D * 2) void attention_tile_fused_kernel(AttnArgs a) {
     __shared__ union {
@@ -1482,24 +1514,13 @@ __global__ __launch_bounds__(D * 2) void attention_tile_fused_kernel(AttnArgs a)
     } sm;
     __shared__ int16_t lsc[TILE];
     __shared__ int32_t lmt;
-    __shared__ uint32_t flag;
     const TileWg wg = tile_wg(a);
     if (!wg.valid) return;                        // padding
     const uint32_t n = a.pos0 + wg.t + 1;
     if (wg.tile * TILE >= n) return;              // beyond this row's context
     tile_scores_phase<D, true>(a, wg, sm.s, lsc, &lmt);
-    const uint32_t ntiles = (n + TILE - 1) / TILE;
-    uint32_t* maxc = tile_max_counter(a, wg.t, wg.g);
-    arrive(maxc + (wg.tile / kArriveGroup) * kCounterStride);  // also ends phase 1's LDS use
-    tile_pv_phase<D, true>(a, wg, sm.p, lsc, &lmt, [&] {
-        return wait_counts(
-            maxc, kCounterStride, tile_groups(ntiles),
-            [&](uint32_t l) {
-                return ntiles - l * kArriveGroup < kArriveGroup ? ntiles - l * kArriveGroup
-                                                                : kArriveGroup;
-            },
-            a.wait_limit, a.abort, a.host_abort, &flag);
-    });
+    __syncthreads();  // phase 1's LDS use ends
+    tile_pv_phase<D, true>(a, wg, sm.p, lsc, &lmt);
 }
 
 // Workgroups of the one-launch tile path the device holds at once.
@@ -1528,7 +1549,7 @@ static hipError_t launch_d(const AttnArgs& a, uint32_t rows, uint32_t kv_heads,
         g.grid_rows = rows;
         g.grid_tiles = tiles;
         const uint32_t grid = tile_grid(rows, tiles, a.num_kv_heads, a.group);
-        if (a.tile_fused && a.tmax_count && tiles <= kTileFusedMaxTiles &&
+        if (a.tile_fused && a.s_tmax32 && tiles <= kTileFusedMaxTiles &&
             grid <= tile_fused_capacity<DT>(a.cus)) {
             attention_tile_fused_kernel<DT><<<grid, 2 * D, 0, st>>>(g);
             return hipGetLastError();

@@ -131,4 +131,46 @@ __device__ __forceinline__ bool wait_counts(const uint32_t* counter, uint32_t st
     return *lds_flag != 0;
 }
 
+// Waits until each of the n <= 64 words p[l * stride] (l < n) has a bit of
+// `valid` set, wavefront 0's lane l reading word l with device-coherent
+// loads; then lane l of wavefront 0 holds word l in *val (the word is both
+// the flag and the value: no separate arrival).  Bounded as wait_counts:
+// returns (uniformly) false when the wait gave up or another workgroup
+// did.  Progress needs the workgroups that write the words to be running.
+__device__ __forceinline__ bool poll_flags(const uint32_t* p, uint32_t stride, uint32_t n,
+                                           uint32_t valid, uint32_t* val, uint32_t limit,
+                                           uint32_t* abort, uint32_t* host_abort,
+                                           uint32_t* lds_flag) {
+    if (threadIdx.x < 64) {
+        const uint32_t l = threadIdx.x;
+        const bool mine = l < n;
+        const uint32_t* q = p + (mine ? l : 0u) * stride;
+        uint32_t v = 0, ok = 1;
+        const uint64_t t0 = wall_clock64();
+        while (true) {
+            v = ld_coherent(q);
+            v = mine ? v : valid;
+            if (__all((v & valid) != 0)) break;
+            if (ld_coherent(abort) != 0) {
+                ok = 0;
+                break;
+            }
+            if (wall_clock64() - t0 > limit) {
+                if (l == 0) {
+                    st_coherent(abort, 1u);
+                    __hip_atomic_store(host_abort, 1u, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_SYSTEM);
+                }
+                ok = 0;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+        *val = v;
+        if (l == 0) *lds_flag = ok;
+    }
+    __syncthreads();
+    return *lds_flag != 0;
+}
+
 }  // namespace llm

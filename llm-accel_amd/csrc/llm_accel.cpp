@@ -134,7 +134,7 @@ struct llm_ctx {
     int32_t* s_tsum = nullptr;
     int16_t* s_tval = nullptr;
     uint32_t* counters = nullptr;
-    size_t counter_bytes = 0, tmax_count_bytes = 0;
+    size_t counter_bytes = 0, rht_words = 0;
     // fused attention sublayer: arrival counters (growing across launches)
     // and the host-visible word a kernel sets when one of its waits gave up
     uint32_t* sync = nullptr;
@@ -152,7 +152,6 @@ struct llm_ctx {
     // in [-2048, 2047]); LLM_ACCEL_P12=0 keeps the 16-bit copies only
     bool p12 = true;
     int32_t* s_tmax32 = nullptr;       // tile maxima published in that launch
-    uint32_t* tmax_count = nullptr;    // its arrival counters
     uint32_t sync_qkv[32] = {};        // QKV arrivals per line so far, mod 2^32
     uint32_t sync_attn = 0;            // attention arrivals per line, mod 2^32
     // bound of one wait (100 MHz ticks); LLM_ACCEL_WAIT_LIMIT overrides it
@@ -291,7 +290,9 @@ int check_waits(llm_ctx* c) {
     (void)hipMemsetAsync(c->sync, 0, llm::kSyncWords * 4, c->stream);
     // counters a workgroup that left a wait early did not reset
     (void)hipMemsetAsync(c->counters, 0, c->counter_bytes, c->stream);
-    (void)hipMemsetAsync(c->tmax_count, 0, c->tmax_count_bytes, c->stream);
+    // and flags of the one-launch tile path a workgroup did not clear
+    (void)hipMemsetAsync(c->s_tmax32, 0, c->rht_words * 4, c->stream);
+    (void)hipMemsetAsync(c->s_tsum, 0, c->rht_words * 4, c->stream);
     if (c->ds_sync) (void)hipMemsetAsync(c->ds_sync, 0, llm::kStackSyncWords * 4, c->stream);
     (void)hipStreamSynchronize(c->stream);
     std::fill(std::begin(c->sync_qkv), std::end(c->sync_qkv), 0u);
@@ -584,7 +585,7 @@ int enqueue_attention_sublayer(llm_ctx* c, uint32_t layer, uint32_t R,
     at.max_tiles = c->tiles;
     at.tile_fused = c->tile_fused ? 1u : 0u;
     at.s_tmax32 = c->s_tmax32;
-    at.tmax_count = c->tmax_count;
+
     at.abort = c->sync + llm::kSyncAbort;
     at.host_abort = c->host_abort;
     at.wait_limit = c->wait_limit;
@@ -1020,7 +1021,7 @@ int llm_ctx_create(const llm_shape_t* shape, int device, uint32_t num_pairs,
             return cleanup(rc);
     const size_t rht = (size_t)8 * c->Hkv * c->tiles * c->G;  // rows*heads*tiles*group
     c->counter_bytes = std::max(llm::counter_words(c->Hq, c->tiles), (size_t)8 * c->Hkv) * 4;
-    c->tmax_count_bytes = (size_t)8 * c->Hq * 4 * llm::kCounterStride * 4;
+    c->rht_words = rht;
     c->exported.assign(num_pairs, 0);
     if ((rc = dev_alloc(c, (void**)&c->xn_attn, (size_t)8 * c->Hp * 2)) ||
         (rc = dev_alloc(c, (void**)&c->xn_final, (size_t)8 * c->Hp * 2)) ||
@@ -1034,7 +1035,7 @@ int llm_ctx_create(const llm_shape_t* shape, int device, uint32_t num_pairs,
         (rc = dev_alloc(c, (void**)&c->s_tval, rht * d * 2)) ||
         (rc = dev_alloc(c, (void**)&c->counters, c->counter_bytes)) ||
         (rc = dev_alloc(c, (void**)&c->s_tmax32, rht * 4)) ||
-        (rc = dev_alloc(c, (void**)&c->tmax_count, c->tmax_count_bytes)) ||
+
         (rc = dev_alloc(c, (void**)&c->sync, (size_t)llm::kSyncWords * 4)))
         return cleanup(rc);
     if (hipHostMalloc((void**)&c->host_abort, 64, hipHostMallocDefault) != hipSuccess)
