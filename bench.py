@@ -64,11 +64,13 @@ def layer_bytes(spec):
     return spec.weight_bytes_per_layer()
 
 
-def gateup_bytes(spec, rows):
-    """Algorithmic HBM bytes of one gate|up + SiLU*up launch: both weight
-    matrices once, the normalised input rows, the product rows written."""
+def gateup_bytes(spec, rows, weight_bytes=2.0):
+    """HBM bytes of one gate|up + SiLU*up launch: both weight matrices once
+    (weight_bytes per weight: 2 for the int16 weights, the algorithmic
+    figure; 1.5 for the 12-bit copy the decode kernel reads), the
+    normalised input rows, the product rows written."""
     h, i = spec.hidden, spec.inter
-    return 2 * (2 * i * h) + 2 * rows * h + 2 * rows * i
+    return int(weight_bytes * (2 * i * h)) + 2 * rows * h + 2 * rows * i
 
 
 def cpu_model_name():
@@ -429,6 +431,7 @@ def main():
 
     lb = layer_bytes(spec)
     gu_bytes = gateup_bytes(spec, 1)
+    gu_read = gateup_bytes(spec, 1, weight_bytes=1.5)
     achieved = gu_bytes / (gu_us * 1e-6) / 1e9
     traffic = load_traffic()
     out = {
@@ -477,7 +480,8 @@ def main():
         "configs[2]": c2,
         "operators": ops,
         "roofline": {
-            "kernel": "proj_kernel<1,*,EPI_SILU> (gate|up + SiLU*up, decode row)",
+            "kernel": ("proj_p12_kernel<1,EPI_SILU,8,2> (gate|up + SiLU*up, decode row, "
+                       "12-bit weight copies)"),
             "bound": "hbm",
             "achieved": achieved,
             "peak": HBM_PEAK_GBS,
@@ -486,6 +490,11 @@ def main():
             "traffic": traffic,
             "algorithmic_bytes_per_launch": gu_bytes,
             "avg_launch_us": gu_us,
+            # the kernel reads the lossless 12-bit copies: 3/4 of the int16
+            # weight bytes; the bandwidth it draws from HBM
+            "read_bytes_per_launch": gu_read,
+            "read_gbs": gu_read / (gu_us * 1e-6) / 1e9,
+            "read_frac": gu_read / (gu_us * 1e-6) / 1e9 / HBM_PEAK_GBS,
         },
     }
     if not args.no_cpu_baseline:
