@@ -246,13 +246,10 @@ __global__ __launch_bounds__(64 * WPB) void proj_kernel(ProjArgs a) {
 #pragma unroll
     for (int m = 0; m < NM; m++)
 #pragma unroll
-        for (int r = 0; r < RT; r++)
-#pragma unroll
-            for (int off = 8; off > 0; off >>= 1)
-                acc[m][r] += __shfl_xor(acc[m][r], off, 64);
+        for (int r = 0; r < RT; r++) acc[m][r] = row16_sum(acc[m][r]);
 
     __shared__ int64_t red[WPB][NM][4][RT];
-    if (j == 0) {
+    if (j == 15) {
 #pragma unroll
         for (int m = 0; m < NM; m++)
 #pragma unroll
@@ -371,11 +368,10 @@ __global__ __launch_bounds__(64 * WPB) void proj_p12_kernel(ProjArgs a) {
 #pragma unroll
         for (int r = 0; r < RT; r++) {
             acc[m][r] = 256 * (int64_t)ph[m][r] + pl[m][r] - 2048 * (int64_t)sx[r];
-#pragma unroll
-            for (int off = 8; off > 0; off >>= 1) acc[m][r] += __shfl_xor(acc[m][r], off, 64);
+            acc[m][r] = row16_sum(acc[m][r]);
         }
     __shared__ int64_t red[WPB][NM][4][RT];
-    if (j == 0) {
+    if (j == 15) {
 #pragma unroll
         for (int m = 0; m < NM; m++)
 #pragma unroll
@@ -711,14 +707,13 @@ __global__ __launch_bounds__(256) void lm_argmax_kernel(const int16_t* __restric
         const uint32_t v = b * 4 + i;
 #pragma unroll
         for (int r = 0; r < RT; r++) {
-#pragma unroll
-            for (int off = 8; off > 0; off >>= 1) acc[r] += __shfl_xor(acc[r], off, 64);
+            acc[r] = row16_sum(acc[r]);
             const unsigned long long k = argmax_key(acc[r], v);
-            if (j == 0 && v < n && k > best[r]) best[r] = k;
+            if (j == 15 && v < n && k > best[r]) best[r] = k;
         }
     }
     __shared__ unsigned long long wbest[4][4][RT];
-    if (j == 0) {
+    if (j == 15) {
 #pragma unroll
         for (int r = 0; r < RT; r++) wbest[wave][i][r] = best[r];
     }

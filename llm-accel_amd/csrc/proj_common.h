@@ -53,6 +53,21 @@ __device__ __forceinline__ uint4 norm8(uint4 x, uint4 g, int32_t gain) {
     return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
+// Sum of v over the 16 lanes of a DPP row (lanes 16i..16i+15), in lane
+// 16i + 15: an inclusive scan by row shifts of 1, 2, 4, 8 (lanes shifted
+// in from outside the row read 0).
+__device__ __forceinline__ int64_t row16_sum(int64_t v) {
+#define ROW_SHR_ADD(n)                                                                   \
+    {                                                                                    \
+        const uint32_t lo = __builtin_amdgcn_update_dpp(0u, (uint32_t)v, 0x110 + n, 0xf, 0xf, true); \
+        const uint32_t hi = __builtin_amdgcn_update_dpp(0u, (uint32_t)((uint64_t)v >> 32), 0x110 + n, 0xf, 0xf, true); \
+        v += (int64_t)(((uint64_t)hi << 32) | lo);                                         \
+    }
+    ROW_SHR_ADD(1) ROW_SHR_ADD(2) ROW_SHR_ADD(4) ROW_SHR_ADD(8)
+#undef ROW_SHR_ADD
+    return v;
+}
+
 // Epilogue operands that do not depend on the sums (residual, norm
 // gammas), fetched when the kernel starts so that the epilogue waits on no
 // memory round trip.
@@ -196,9 +211,8 @@ __device__ __forceinline__ bool proj_block(const ProjArgs& a, uint32_t b, int64_
 #pragma unroll
         for (int r = 0; r < RT; r++) {
             int64_t acc = wide[nb][r] + part[nb][r];
-#pragma unroll
-            for (int off = 8; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
-            if (j == 0) red[((nb * WPB + wave) * 4 + i) * RT + r] = acc;
+            acc = row16_sum(acc);
+            if (j == 15) red[((nb * WPB + wave) * 4 + i) * RT + r] = acc;
         }
     lds_barrier();
     if (eout) {
