@@ -83,6 +83,17 @@ FX_HD int16_t fx_rmsnorm_gain(int64_t sum_sq, uint32_t cols) {
     return fx_rsqrt(mean);  // + accum(1e-6), which is raw 0
 }
 
+// fx_silu in two steps: the table index its argument selects, then the
+// value from that entry.
+FX_HD int32_t fx_silu_index(int32_t x) {
+    const int32_t c = x >= 0 ? (-x < -2048 ? -2048 : -x) : (x < -2048 ? -2048 : x);
+    return c + 2048;
+}
+FX_HD int16_t fx_silu_entry(int32_t x, int32_t e) {
+    const int32_t r = fx_recip(256 + e);
+    if (x >= 0) return fx_sat16(fx_rnd((int64_t)x * r, 8));
+    return fx_sat16(fx_rnd((int64_t)x * e * r, 16));
+}
 // golden_silu (host:658-668) with the Q8.8 exp table e8[x + 2048],
 // x in [-2048, 0].
 FX_HD int16_t fx_silu(int32_t x, const int16_t* e8) {

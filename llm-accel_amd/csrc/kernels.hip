@@ -265,7 +265,10 @@ __global__ __launch_bounds__(64 * WPB) void proj_kernel(ProjArgs a) {
 #pragma unroll
             for (int w = 0; w < WPB; w++) tot[m] += red[w][m][ii][er];
         }
-        proj_out<EPI>(a, er, en, tot[0], tot[NM - 1], ei, e8s);
+        if constexpr (EPI == EPI_SILU && RT <= 2)
+            silu_out_scalar<4 * RT>(a, er, en, tot[0], tot[NM - 1], et);
+        else
+            proj_out<EPI>(a, er, en, tot[0], tot[NM - 1], ei, e8s);
     }
     if (efill) a.final_out[(size_t)fr * a.ldn + fn] = fill;
 }
@@ -387,7 +390,10 @@ __global__ __launch_bounds__(64 * WPB) void proj_p12_kernel(ProjArgs a) {
 #pragma unroll
             for (int w = 0; w < WPB; w++) tot[m] += red[w][m][ii][er];
         }
-        proj_out<EPI>(a, er, en, tot[0], tot[NM - 1], ei, a.exp8);
+        if constexpr (EPI == EPI_SILU)
+            silu_out_scalar<4 * RT>(a, er, en, tot[0], tot[NM - 1], et);
+        else
+            proj_out<EPI>(a, er, en, tot[0], tot[NM - 1], ei, a.exp8);
     }
     if (efill) a.final_out[(size_t)fr * a.ldn + fn] = fill;
 }

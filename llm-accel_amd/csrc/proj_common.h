@@ -114,6 +114,32 @@ __device__ __forceinline__ void proj_out(const ProjArgs& a, uint32_t r, uint32_t
 }
 
 
+// The SiLU epilogue of lanes 0..NL-1 of wavefront 0 (the calling lanes; at
+// most 64), output (r, n) of lane et: the table entries through the scalar
+// cache, one uniform load per lane, which do not queue behind the vector
+// loads of the weight stream (a lane's dependent table load did).
+template <int NL>
+__device__ __forceinline__ void silu_out_scalar(const ProjArgs& a, uint32_t r, uint32_t n,
+                                                int64_t t0, int64_t t1, int et) {
+    static_assert(NL <= 64, "lanes of wavefront 0");
+    const int16_t y = fx_narrow_projection(t0);
+    const int16_t up = fx_narrow_projection(t1);
+    const int32_t ix = fx_silu_index(y);  // 0..2048
+    typedef const __attribute__((address_space(4))) uint32_t* ctab;
+    const ctab tab = (ctab)(const void*)a.exp8;
+    int32_t e = 0;
+#pragma unroll
+    for (int l = 0; l < NL; l++) {
+        uint32_t il = __builtin_amdgcn_readlane(ix, l);
+        il = il > 2048u ? 2048u : il;  // a lane past the matrix holds anything
+        const uint32_t wd = tab[il >> 1];
+        const int32_t el = (int32_t)((wd >> (16 * (il & 1))) & 0xffffu);
+        e = et == l ? el : e;
+    }
+    const int16_t sg = fx_silu_entry(y, e);
+    a.out[(size_t)r * a.ldo + n] = fx_sat16(fx_rnd((int64_t)sg * up, 8));
+}
+
 // NB consecutive 4-row blocks NB b .. NB b + NB - 1 of a projection inside
 // a fused launch, on WPB wavefronts that each hold at most SPW k-steps of
 // every block (SPW no larger than the widening interval: the int32 sums
