@@ -49,6 +49,12 @@ struct AttnArgs {
     // the device's compute units
     uint32_t tile_fused;
     int32_t* s_tmax32;    // [8][kv_heads][max_tiles][group]
+    // GQA path in one launch (scores and PV): the tile maxima go into
+    // s_gmax32 [8][kv_heads][max_tiles][group] tagged with the launch's
+    // epoch (epoch << 16 | (uint16) max; 1..kGqaEpochMax, different from
+    // every launch since s_gmax32 was last cleared)
+    uint32_t epoch;
+    int32_t* s_gmax32;
     uint32_t* abort;      // device word set when a wait gave up
     uint32_t* host_abort; // host-visible copy
     uint32_t wait_limit;  // bound of one wait (100 MHz ticks)
@@ -65,6 +71,10 @@ constexpr uint32_t tile_groups(uint32_t tiles) { return (tiles + kArriveGroup - 
 constexpr size_t counter_words(uint32_t num_heads, uint32_t tiles) {
     return (size_t)8 * num_heads * (1 + tile_groups(tiles)) * kCounterStride;
 }
+
+// Epochs of the GQA path's tagged maxima run 1..kGqaEpochMax; then the
+// host clears s_gmax32 and starts again.
+constexpr uint32_t kGqaEpochMax = 65535;
 
 // Tiles per split-path workgroup: at most kMaxChunkTiles.
 constexpr uint32_t kMaxChunkTiles = 8;

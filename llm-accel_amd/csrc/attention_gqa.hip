@@ -74,57 +74,85 @@ struct __attribute__((aligned(16))) GqaScoresSmem {
     uint32_t sat;                       // a staged K value saturates
 };
 
+// Scores of a (row, KV head, tile) workgroup: lane = position, heads w and
+// w + 4.  FUSED keeps them (and the tile maxima) in sc / mt for the PV phase
+// of the same workgroup and publishes the maxima as tagged words; else they
+// go to s_scores.  The maxima go to s_tmax either way (the scan reads them).
 template <int D>
-__global__ __launch_bounds__(GNT) void attention_gqa_scores_kernel(AttnArgs a) {
-    static_assert(D == 64 || D == 128, "GQA tile path: head_dim 64 or 128");
+struct GqaScoresLoads {
+    static constexpr uint32_t HD = D / 2, C8 = D / 8;
+    static constexpr int KC = TILE * C8 / GNT;               // K chunks per thread
+    static constexpr int QP = (GMAXG * HD + GNT - 1) / GNT;  // query pairs per thread
+    static constexpr int NK = (8 * HD + GNT - 1) / GNT;      // block K pairs per thread
+    v4u kc[KC];
+    int32_t qx[QP][4], kx[NK][4];
+};
+// The scores phase's loads (indices clamped: every load is issued): the
+// tile's K page, the group's query rows and the block's K rows in the tile
+// with their RoPE rows.
+template <int D>
+__device__ __forceinline__ void gqa_scores_loads(const AttnArgs& a, const GqaWg& wg,
+                                                 GqaScoresLoads<D>& L) {
     constexpr uint32_t HD = D / 2, C8 = D / 8;
-    constexpr int KC = TILE * C8 / GNT;                   // K chunks per thread
-    constexpr int QP = (GMAXG * HD + GNT - 1) / GNT;      // query pairs per thread
-    constexpr int NK = (8 * HD + GNT - 1) / GNT;          // block K pairs per thread
-    __shared__ GqaScoresSmem<D> sm;
-    GqaWg wg;
-    if (!gqa_wg(a, wg)) return;
     const uint32_t t = wg.t, h = wg.h, tile = wg.tile, tid = threadIdx.x;
-    const uint32_t n = a.pos0 + t + 1, own = n - 1, G = a.group;
-    const uint32_t lane = tid & 63, w = tid >> 6;
-    const int64_t scale = (int64_t)a.qk_scale << 8;
-
-    // ---- loads (indices clamped: every load is issued) ----
+    const uint32_t own = a.pos0 + t, G = a.group;
     const uint32_t tp = tile < a.tiles ? tile : a.tiles - 1;
     const int16_t* kpage = a.kcache + page_off<D>(a, h, tp);
-    v4u kc[KC];
 #pragma unroll
-    for (int u = 0; u < KC; u++) {
+    for (int u = 0; u < GqaScoresLoads<D>::KC; u++) {
         const uint32_t i = tid + GNT * u;
-        kc[u] = *(const v4u*)(kpage + (i / C8) * D + 8 * (i % C8));
+        L.kc[u] = *(const v4u*)(kpage + (i / C8) * D + 8 * (i % C8));
     }
-    int32_t qx[QP][4];
 #pragma unroll
-    for (int u = 0; u < QP; u++) {
+    for (int u = 0; u < GqaScoresLoads<D>::QP; u++) {
         const uint32_t i = tid + GNT * u < G * HD ? tid + GNT * u : 0;
         const uint32_t gi = i / HD, c = i % HD;
         const int16_t* qrow = a.qkv + (size_t)t * a.ldqkv + (size_t)(h * G + gi) * D;
         const int16_t* rp = a.rope + (size_t)own * D;
-        qx[u][0] = qrow[c];
-        qx[u][1] = qrow[HD + c];
-        qx[u][2] = rp[c];
-        qx[u][3] = rp[HD + c];
+        L.qx[u][0] = qrow[c];
+        L.qx[u][1] = qrow[HD + c];
+        L.qx[u][2] = rp[c];
+        L.qx[u][3] = rp[HD + c];
     }
     const GqaRows tr = gqa_rows(a, tile, own);
     const uint32_t nk = tr.nrow * HD;
-    int32_t kx[NK][4];
 #pragma unroll
-    for (int u = 0; u < NK; u++) {
+    for (int u = 0; u < GqaScoresLoads<D>::NK; u++) {
         const uint32_t i = tid + GNT * u < nk ? tid + GNT * u : 0;
         const uint32_t r = tr.r0 + i / HD, c = i % HD;
         const int16_t* krow = a.qkv + (size_t)r * a.ldqkv + (size_t)a.num_heads * D +
                               (size_t)h * D;
         const int16_t* kr = a.rope + (size_t)(a.pos0 + r) * D;
-        kx[u][0] = krow[c];
-        kx[u][1] = krow[HD + c];
-        kx[u][2] = kr[c];
-        kx[u][3] = kr[HD + c];
+        L.kx[u][0] = krow[c];
+        L.kx[u][1] = krow[HD + c];
+        L.kx[u][2] = kr[c];
+        L.kx[u][3] = kr[HD + c];
     }
+}
+
+// Scores of a (row, KV head, tile) workgroup from its loads: lane =
+// position, heads w and w + 4.  FUSED keeps them (and the tile maxima) in
+// sc / mt for the PV phase of the same workgroup and publishes the maxima
+// as tagged words; else they go to s_scores.  The maxima go to s_tmax
+// either way (the scan reads them).
+template <int D, bool FUSED>
+__device__ __forceinline__ void gqa_scores_body(const AttnArgs& a, const GqaWg& wg,
+                                                GqaScoresSmem<D>& sm,
+                                                const GqaScoresLoads<D>& L, int32_t (&sc)[2],
+                                                int32_t (&mt)[2]) {
+    static_assert(D == 64 || D == 128, "GQA tile path: head_dim 64 or 128");
+    constexpr uint32_t HD = D / 2, C8 = D / 8;
+    constexpr int KC = GqaScoresLoads<D>::KC, QP = GqaScoresLoads<D>::QP,
+                  NK = GqaScoresLoads<D>::NK;
+    const uint32_t t = wg.t, h = wg.h, tile = wg.tile, tid = threadIdx.x;
+    const uint32_t n = a.pos0 + t + 1, own = n - 1, G = a.group;
+    const uint32_t lane = tid & 63, w = tid >> 6;
+    const int64_t scale = (int64_t)a.qk_scale << 8;
+    const v4u* kc = L.kc;
+    const int32_t(*qx)[4] = L.qx;
+    const int32_t(*kx)[4] = L.kx;
+    const GqaRows tr = gqa_rows(a, tile, own);
+    const uint32_t nk = tr.nrow * HD;
     // ---- the group's queries and the block's K rows, rotated ----
     if (tid == 0) sm.sat = 0;
 #pragma unroll
@@ -203,13 +231,33 @@ __global__ __launch_bounds__(GNT) void attention_gqa_scores_kernel(AttnArgs a) {
         ts = fx_sat32(fx_rnd((int64_t)ts * scale, 16));
         const int32_t s = valid ? fx_sat16(fx_rnd(ts, 8)) : INT16_MIN;
         const size_t base = (((size_t)t * a.num_kv_heads + h) * a.max_tiles + tile) * G + gi;
-        a.s_scores[base * TILE + lane] = (int16_t)s;
         const int32_t mx = wave_max(s);
-        if (lane == 0) a.s_tmax[base] = (int16_t)mx;
+        if (FUSED) {
+            sc[kk] = s;
+            mt[kk] = mx;
+            if (lane == 0) {
+                a.s_tmax[base] = (int16_t)mx;
+                st_coherent(&a.s_gmax32[base], (int32_t)((a.epoch << 16) | (uint16_t)mx));
+            }
+        } else {
+            a.s_scores[base * TILE + lane] = (int16_t)s;
+            if (lane == 0) a.s_tmax[base] = (int16_t)mx;
+        }
     }
     if (own / TILE == tile && tid < C8)  // this row's K into the cache
         *(v4u*)(a.kcache + page_off<D>(a, h, tile) + (own % TILE) * D + 8 * tid) =
             *(const v4u*)(sm.kv[t] + 8 * tid);
+}
+
+template <int D>
+__global__ __launch_bounds__(GNT) void attention_gqa_scores_kernel(AttnArgs a) {
+    __shared__ GqaScoresSmem<D> sm;
+    GqaWg wg;
+    if (!gqa_wg(a, wg)) return;
+    int32_t sc[2], mt[2];
+    GqaScoresLoads<D> L;
+    gqa_scores_loads<D>(a, wg, L);
+    gqa_scores_body<D, false>(a, wg, sm, L, sc, mt);
 }
 
 template <int D>
@@ -221,61 +269,123 @@ struct __attribute__((aligned(16))) GqaPvSmem {
     int32_t mrun[GMAXG];                // running max before the tile, per head
 };
 
+// One-launch GQA path: a context of at most kGqaFusedMaxTiles tiles, so that
+// the maxima of the tiles before any tile (tile x G <= GNT x GPW words) are
+// polled GPW words per thread.
+constexpr uint32_t kGqaFusedMaxTiles = 257;
+constexpr int GPW = (kGqaFusedMaxTiles - 1) * GMAXG / GNT;
+
+// PV of a (row, KV head, tile) workgroup.  FUSED: the scores and tile
+// maxima come from the same workgroup's scores phase (sci, mti), and the
+// earlier tiles' maxima are awaited as tagged words (bounded); ok (LDS,
+// 1 on entry) is cleared by a wavefront whose wait gave up, and the
+// workgroup then returns false.
 template <int D>
-__global__ __launch_bounds__(GNT) void attention_gqa_pv_kernel(AttnArgs a) {
+struct GqaPvLoads {
+    static constexpr uint32_t VC = D * TILE / 8 / GNT;  // V^T chunks per thread
+    static constexpr int NE = (257 + GNT - 1) / GNT;    // exp table pieces per thread
+    static constexpr int NV = (8 * D + GNT - 1) / GNT;  // block V values per thread
+    v4u ex[NE];
+    v4u vc[VC];
+    int16_t vx[NV];
+};
+// The PV phase's loads that depend on nothing computed (indices clamped:
+// every load is issued): the exp table, the tile's V page, the block's V
+// rows in the tile.
+template <int D>
+__device__ __forceinline__ void gqa_pv_loads(const AttnArgs& a, const GqaWg& wg,
+                                             GqaPvLoads<D>& L) {
+    const uint32_t t = wg.t, h = wg.h, tile = wg.tile, tid = threadIdx.x;
+    const uint32_t own = a.pos0 + t;
+#pragma unroll
+    for (int u = 0; u < GqaPvLoads<D>::NE; u++) {
+        const uint32_t c = tid + GNT * u;
+        L.ex[u] = *(const v4u*)(a.exp14 + 8 * (c < 257 ? c : 256));
+    }
+    const uint32_t tp = tile < a.tiles ? tile : a.tiles - 1;
+    const int16_t* vpage = a.vcache + page_off<D>(a, h, tp);
+#pragma unroll
+    for (int u = 0; u < (int)GqaPvLoads<D>::VC; u++) {
+        const uint32_t i = tid + GNT * u;  // row i / 8, slots 8 (i % 8) ..
+        L.vc[u] = *(const v4u*)(vpage + (i / 8) * TILE + 8 * (i % 8));
+    }
+    const GqaRows tr = gqa_rows(a, tile, own);
+    const uint32_t nv = tr.nrow * D;
+#pragma unroll
+    for (int u = 0; u < GqaPvLoads<D>::NV; u++) {
+        const uint32_t i = tid + GNT * u < nv ? tid + GNT * u : 0;
+        L.vx[u] = a.qkv[(size_t)(tr.r0 + i / D) * a.ldqkv +
+                        (size_t)(a.num_heads + a.num_kv_heads) * D + (size_t)h * D + i % D];
+    }
+}
+
+template <int D, bool FUSED>
+__device__ __forceinline__ bool gqa_pv_body(const AttnArgs& a, const GqaWg& wg,
+                                            GqaPvSmem<D>& sm, const GqaPvLoads<D>& L,
+                                            const int32_t (&sci)[2],
+                                            const int32_t (&mti)[2], uint32_t& ok_all) {
     static_assert(D == 64 || D == 128, "GQA tile path: head_dim 64 or 128");
     constexpr uint32_t VC = D * TILE / 8 / GNT;        // V^T chunks per thread
     constexpr int NE = (257 + GNT - 1) / GNT;          // exp table pieces per thread
     constexpr int NV = (8 * D + GNT - 1) / GNT;        // block V values per thread
     constexpr uint32_t NHS = GNT / D;                  // heads a PV pass covers at once
-    __shared__ GqaPvSmem<D> sm;
-    GqaWg wg;
-    if (!gqa_wg(a, wg)) return;
     const uint32_t t = wg.t, h = wg.h, tile = wg.tile, tid = threadIdx.x;
     const uint32_t n = a.pos0 + t + 1, own = n - 1, G = a.group;
     const uint32_t lane = tid & 63, w = tid >> 6;
     const size_t rh = (size_t)t * a.num_kv_heads + h;
 
-    // ---- loads (indices clamped: every load is issued) ----
-    v4u ex[NE];
-#pragma unroll
-    for (int u = 0; u < NE; u++) {
-        const uint32_t c = tid + GNT * u;
-        ex[u] = *(const v4u*)(a.exp14 + 8 * (c < 257 ? c : 256));
-    }
-    const uint32_t tp = tile < a.tiles ? tile : a.tiles - 1;
-    const int16_t* vpage = a.vcache + page_off<D>(a, h, tp);
-    v4u vc[VC];
-#pragma unroll
-    for (int u = 0; u < (int)VC; u++) {
-        const uint32_t i = tid + GNT * u;  // row i / 8, slots 8 (i % 8) ..
-        vc[u] = *(const v4u*)(vpage + (i / 8) * TILE + 8 * (i % 8));
-    }
+    // ---- loads (issued by the caller: FUSED at the start of the launch) ----
+    const v4u* ex = L.ex;
+    const v4u* vc = L.vc;
+    const int16_t* vx = L.vx;
     const GqaRows tr = gqa_rows(a, tile, own);
     const uint32_t nv = tr.nrow * D;
-    int16_t vx[NV];
-#pragma unroll
-    for (int u = 0; u < NV; u++) {
-        const uint32_t i = tid + GNT * u < nv ? tid + GNT * u : 0;
-        vx[u] = a.qkv[(size_t)(tr.r0 + i / D) * a.ldqkv +
-                      (size_t)(a.num_heads + a.num_kv_heads) * D + (size_t)h * D + i % D];
-    }
     // scores and this tile's maxima of heads w and w + 4 (lane = position)
     int32_t sc[2], mt[2];
+    if (FUSED) {
+        sc[0] = sci[0], sc[1] = sci[1], mt[0] = mti[0], mt[1] = mti[1];
+    } else {
 #pragma unroll
-    for (int kk = 0; kk < 2; kk++) {
-        const uint32_t gi = w + 4 * kk < G ? w + 4 * kk : 0;
-        const size_t base = (rh * a.max_tiles + tile) * G + gi;
-        sc[kk] = a.s_scores[base * TILE + lane];
-        mt[kk] = a.s_tmax[base];
+        for (int kk = 0; kk < 2; kk++) {
+            const uint32_t gi = w + 4 * kk < G ? w + 4 * kk : 0;
+            const size_t base = (rh * a.max_tiles + tile) * G + gi;
+            sc[kk] = a.s_scores[base * TILE + lane];
+            mt[kk] = a.s_tmax[base];
+        }
     }
     // maxima of the tiles before this one, (tile, head) pairs over threads
-    int32_t pm[4];
+    constexpr int NPM = FUSED ? GPW : 4;
+    int32_t pm[NPM];
     const uint32_t npm = tile * G;
+    if (FUSED) {
+        // the tagged words of the earlier tiles (contiguous: [0, tile) x G),
+        // every one read until it carries this launch's epoch; a wavefront
+        // waits for its own words, one that gives up clears sm.ok
+        const int32_t* gm = a.s_gmax32 + rh * a.max_tiles * G;
+        const TagWait tw{(uint64_t)wall_clock64(), a.wait_limit, a.abort, a.host_abort};
+        bool waited = true;
+        while (true) {
+            bool ok = true;
 #pragma unroll
-    for (int u = 0; u < 4; u++) {
-        const uint32_t i = tid + GNT * u < npm ? tid + GNT * u : 0;
-        pm[u] = npm ? a.s_tmax[(rh * a.max_tiles + i / G) * G + i % G] : INT16_MIN;
+            for (int u = 0; u < NPM; u++) {
+                const uint32_t i = tid + GNT * u;
+                const uint32_t wd = (uint32_t)ld_coherent(&gm[i < npm ? i : 0]);
+                ok = ok && (i >= npm || tag_ok(wd, 16, a.epoch));
+                pm[u] = i < npm ? (int32_t)(int16_t)(wd & 0xffffu) : INT16_MIN;
+            }
+            if (__all(ok)) break;
+            if (!tw.keep_waiting()) {
+                waited = false;
+                break;
+            }
+        }
+        if (!waited) ok_all = 0;
+    } else {
+#pragma unroll
+        for (int u = 0; u < NPM; u++) {
+            const uint32_t i = tid + GNT * u < npm ? tid + GNT * u : 0;
+            pm[u] = npm ? a.s_tmax[(rh * a.max_tiles + i / G) * G + i % G] : INT16_MIN;
+        }
     }
     // ---- staging ----
     if (tid < GMAXG) sm.mrun[tid] = INT16_MIN;
@@ -297,17 +407,20 @@ __global__ __launch_bounds__(GNT) void attention_gqa_pv_kernel(AttnArgs a) {
         if (i < nv) sm.vb[tr.r0 + i / D][i % D] = vx[u];
     }
     lds_barrier();
+    if (FUSED && ok_all == 0) return false;  // uniform: read after the barrier
 #pragma unroll
-    for (int u = 0; u < 4; u++) {
+    for (int u = 0; u < NPM; u++) {
         const uint32_t i = tid + GNT * u;
         if (i < npm)
             __hip_atomic_fetch_max(&sm.mrun[i % G], pm[u], __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_WORKGROUP);
     }
-    for (uint32_t i = tid + GNT * 4; i < npm; i += GNT)  // contexts beyond 128 tiles x 8 heads
-        __hip_atomic_fetch_max(&sm.mrun[i % G],
-                               (int32_t)a.s_tmax[(rh * a.max_tiles + i / G) * G + i % G],
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (!FUSED) {
+        for (uint32_t i = tid + GNT * NPM; i < npm; i += GNT)  // beyond 128 tiles x 8 heads
+            __hip_atomic_fetch_max(&sm.mrun[i % G],
+                                   (int32_t)a.s_tmax[(rh * a.max_tiles + i / G) * G + i % G],
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
     // the block's V rows into their slots
     for (uint32_t i = tid; i < nv; i += GNT) {
         const uint32_t r = tr.r0 + i / D, e = i % D;
@@ -363,6 +476,46 @@ __global__ __launch_bounds__(GNT) void attention_gqa_pv_kernel(AttnArgs a) {
     }
     if (own / TILE == tile && tid < D)  // this row's V into the cache
         a.vcache[page_off<D>(a, h, tile) + tid * TILE + paired(own % TILE)] = sm.vb[t][tid];
+    return true;
+}
+
+template <int D>
+__global__ __launch_bounds__(GNT) void attention_gqa_pv_kernel(AttnArgs a) {
+    __shared__ GqaPvSmem<D> sm;
+    GqaWg wg;
+    if (!gqa_wg(a, wg)) return;
+    const int32_t none[2] = {0, 0};
+    uint32_t unused = 1;
+    GqaPvLoads<D> L;
+    gqa_pv_loads<D>(a, wg, L);
+    gqa_pv_body<D, false>(a, wg, sm, L, none, none, unused);
+}
+
+// Scores and PV in one launch (at most kGqaFusedMaxTiles tiles; launched
+// only when the whole grid fits on the device at once, so that the tiles a
+// workgroup waits for are all running): the scores phase publishes the
+// tile's tagged maxima, the PV phase issues its loads, then waits for the
+// earlier tiles' maxima.
+template <int D>
+__global__ __launch_bounds__(GNT) void attention_gqa_fused_kernel(AttnArgs a) {
+    __shared__ union {
+        GqaScoresSmem<D> s;
+        GqaPvSmem<D> p;
+    } sm;
+    __shared__ uint32_t ok_all;
+    GqaWg wg;
+    if (!gqa_wg(a, wg)) return;
+    if (threadIdx.x == 0) ok_all = 1;  // ordered by the scores phase's barriers
+    // both phases' loads first (the V page arrives while the scores are
+    // computed: loads complete in order, the K page's first)
+    GqaScoresLoads<D> LS;
+    gqa_scores_loads<D>(a, wg, LS);
+    GqaPvLoads<D> LP;
+    gqa_pv_loads<D>(a, wg, LP);
+    int32_t sc[2], mt[2];
+    gqa_scores_body<D, true>(a, wg, sm.s, LS, sc, mt);
+    __syncthreads();  // the scores phase's LDS use ends
+    gqa_pv_body<D, true>(a, wg, sm.p, LP, sc, mt, ok_all);
 }
 
 struct __attribute__((aligned(16))) GqaScanSmem {
@@ -612,18 +765,41 @@ __global__ __launch_bounds__(GNT) void attention_gqa_scan_kernel(AttnArgs a) {
             fx_sat16(fx_rnd((int64_t)acc * fx_inv_sum(sm.sum), 16));
 }
 
+// Workgroups of the one-launch GQA kernel the device holds at once.
+template <int D>
+uint32_t gqa_fused_capacity(uint32_t cus) {
+    static int per_cu = -1;
+    if (per_cu < 0) {
+        int nb = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                &nb, reinterpret_cast<const void*>(&attention_gqa_fused_kernel<D>), GNT, 0) !=
+            hipSuccess)
+            nb = 0;
+        per_cu = nb;
+    }
+    return (uint32_t)per_cu * cus;
+}
+
 template <int D>
 hipError_t launch_gqa_d(const AttnArgs& a, uint32_t rows, uint32_t tiles, hipStream_t st) {
     AttnArgs g = a;
     g.grid_rows = rows;
     g.grid_tiles = tiles;
     const uint32_t grid = rows * tiles * a.num_kv_heads;
-    attention_gqa_scores_kernel<D><<<grid, GNT, 0, st>>>(g);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    attention_gqa_pv_kernel<D><<<grid, GNT, 0, st>>>(g);
-    e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    hipError_t e;
+    if (a.epoch && a.s_gmax32 && tiles <= kGqaFusedMaxTiles &&
+        grid <= gqa_fused_capacity<D>(a.cus)) {
+        attention_gqa_fused_kernel<D><<<grid, GNT, 0, st>>>(g);
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    } else {
+        attention_gqa_scores_kernel<D><<<grid, GNT, 0, st>>>(g);
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        attention_gqa_pv_kernel<D><<<grid, GNT, 0, st>>>(g);
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
     attention_gqa_scan_kernel<D><<<rows * a.num_heads * (D / GSE), GNT, 0, st>>>(g);
     return hipGetLastError();
 }

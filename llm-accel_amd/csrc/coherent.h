@@ -131,6 +131,37 @@ __device__ __forceinline__ bool wait_counts(const uint32_t* counter, uint32_t st
     return *lds_flag != 0;
 }
 
+// Words tagged with the launch that wrote them: a word published during a
+// launch carries the launch's epoch above bit `shift` and its value below,
+// written by one 32-bit coherent store, so a reader that sees the epoch has
+// the value.  Epochs are never 0 and differ from every launch since the
+// words were last cleared.
+__device__ __forceinline__ bool tag_ok(uint32_t word, uint32_t shift, uint32_t tag) {
+    return (word >> shift) == tag;
+}
+
+// Bounded wait of one wavefront: keep_waiting() sleeps briefly and returns
+// true, or returns false when another workgroup has given up or `limit`
+// ticks have passed (then, once, setting *abort and *host_abort).
+struct TagWait {
+    uint64_t t0;
+    uint32_t limit;
+    uint32_t* abort;
+    uint32_t* host_abort;
+    __device__ __forceinline__ bool keep_waiting() const {
+        if (ld_coherent(abort) != 0) return false;
+        if ((uint64_t)wall_clock64() - t0 > limit) {
+            if ((threadIdx.x & 63) == 0) {
+                st_coherent(abort, 1u);
+                __hip_atomic_store(host_abort, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            }
+            return false;
+        }
+        __builtin_amdgcn_s_sleep(2);
+        return true;
+    }
+};
+
 // Waits until each of the n <= 64 words p[l * stride] (l < n) has a bit of
 // `valid` set, wavefront 0's lane l reading word l with device-coherent
 // loads; then lane l of wavefront 0 holds word l in *val (the word is both

@@ -152,6 +152,11 @@ struct llm_ctx {
     // in [-2048, 2047]); LLM_ACCEL_P12=0 keeps the 16-bit copies only
     bool p12 = true;
     int32_t* s_tmax32 = nullptr;       // tile maxima published in that launch
+    int32_t* s_gmax32 = nullptr;       // GQA path: tagged tile maxima
+    uint32_t gqa_epoch = 0;            // epoch of the last GQA launch
+    // GQA scores and PV in one launch when the grid fits on the device;
+    // LLM_ACCEL_GQA_FUSED=0 keeps three launches
+    bool gqa_fused = true;
     uint32_t sync_qkv[32] = {};        // QKV arrivals per line so far, mod 2^32
     uint32_t sync_attn = 0;            // attention arrivals per line, mod 2^32
     // bound of one wait (100 MHz ticks); LLM_ACCEL_WAIT_LIMIT overrides it
@@ -585,6 +590,16 @@ int enqueue_attention_sublayer(llm_ctx* c, uint32_t layer, uint32_t R,
     at.max_tiles = c->tiles;
     at.tile_fused = c->tile_fused ? 1u : 0u;
     at.s_tmax32 = c->s_tmax32;
+    at.s_gmax32 = c->s_gmax32;
+    if (at.use_gqa && c->gqa_fused) {
+        // a fresh epoch for the GQA path's tagged maxima; past the last one
+        // s_gmax32 is cleared (stream-ordered before this launch)
+        if (++c->gqa_epoch > llm::kGqaEpochMax) {
+            HIP_TRY(hipMemsetAsync(c->s_gmax32, 0, c->rht_words * 4, c->stream));
+            c->gqa_epoch = 1;
+        }
+        at.epoch = c->gqa_epoch;
+    }
 
     at.abort = c->sync + llm::kSyncAbort;
     at.host_abort = c->host_abort;
@@ -1035,6 +1050,7 @@ int llm_ctx_create(const llm_shape_t* shape, int device, uint32_t num_pairs,
         (rc = dev_alloc(c, (void**)&c->s_tval, rht * d * 2)) ||
         (rc = dev_alloc(c, (void**)&c->counters, c->counter_bytes)) ||
         (rc = dev_alloc(c, (void**)&c->s_tmax32, rht * 4)) ||
+        (rc = dev_alloc(c, (void**)&c->s_gmax32, rht * 4)) ||
 
         (rc = dev_alloc(c, (void**)&c->sync, (size_t)llm::kSyncWords * 4)))
         return cleanup(rc);
@@ -1047,6 +1063,8 @@ int llm_ctx_create(const llm_shape_t* shape, int device, uint32_t num_pairs,
         c->tile_fused = std::strcmp(e, "0") != 0;
     if (const char* e = std::getenv("LLM_ACCEL_GQA_MIN_TILES"))
         c->gqa_min_tiles = (uint32_t)std::strtoul(e, nullptr, 10);
+    if (const char* e = std::getenv("LLM_ACCEL_GQA_FUSED"))
+        c->gqa_fused = std::strcmp(e, "0") != 0;
     if (hipDeviceGetAttribute(&c->cus, hipDeviceAttributeMultiprocessorCount, c->device) !=
         hipSuccess)
         return cleanup(fail(LLM_E_HIP, "device attribute query failed"));

@@ -240,8 +240,10 @@ def test_fused_long_mixed_sequence(start):
                     pin, pout = pout, pin
 
 
-def test_tile_path_wait_timeout_is_reported():
-    """The one-launch tile path (decode row at 5 tiles) with a 0-tick wait
+@pytest.mark.parametrize("path", ["tile", "gqa"])
+def test_tile_path_wait_timeout_is_reported(path):
+    """The one-launch tile path, or the one-launch GQA path (scores and PV;
+    forced from 5 tiles), for a decode row at 5 tiles with a 0-tick wait
     bound: the launch ends (every wait is bounded); either every wait was
     already satisfied at its first poll and the row equals the oracle's, or
     the next synchronisation reports the time-out and the one after is
@@ -253,7 +255,10 @@ def test_tile_path_wait_timeout_is_reported():
     synth = workloads.SyntheticModel(spec, seed=workloads.SEED, layers=1)
     om = oracle_from_synthetic(synth, oracle_shape(spec, layers=1, max_seq=512))
     kc, vc = om.new_kv()
-    acc = _accel(spec, 1, 512, {"LLM_ACCEL_WAIT_LIMIT": "0"})
+    env = {"LLM_ACCEL_WAIT_LIMIT": "0"}
+    if path == "gqa":
+        env["LLM_ACCEL_GQA_MIN_TILES"] = "5"
+    acc = _accel(spec, 1, 512, env)
     with acc:
         acc.load_model(synth)
         for h in range(spec.kv_heads):
@@ -262,7 +267,7 @@ def test_tile_path_wait_timeout_is_reported():
             acc.kv_write(0, h, 0, k, v)
         x = synth.hidden_rows(1, seed_offset=81)
         acc.upload(2, x)
-        _say(f"case tile path 0-tick wait bound n={n}")
+        _say(f"case {path} path 0-tick wait bound n={n}")
         rc, _ = acc.task(18, 0, 1, n, 2, 0)
         assert rc == 0
         try:

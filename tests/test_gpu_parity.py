@@ -474,6 +474,23 @@ def test_gqa_path_running_max_rises(gqa_everywhere):
     test_running_max_rises_often(4096, 3)
 
 
+@pytest.fixture
+def gqa_three_launches(monkeypatch):
+    """The GQA tile path from 5 tiles as three launches (scores, PV, scan)
+    instead of scores and PV in one launch."""
+    monkeypatch.setenv("LLM_ACCEL_GQA_MIN_TILES", "5")
+    monkeypatch.setenv("LLM_ACCEL_GQA_FUSED", "0")
+
+
+@pytest.mark.parametrize("cfg,n,rows", [("B", 1020, 8), ("A", 317, 5), ("B", 319, 1)])
+def test_gqa_three_launches_block_across_tile_boundary(gqa_three_launches, cfg, n, rows):
+    test_block_across_tile_boundary_late_context(cfg, n, rows)
+
+
+def test_gqa_three_launches_running_max_rises(gqa_three_launches):
+    test_running_max_rises_often(4096, 3)
+
+
 def test_norm_cache_invalidation():
     # T18 writes pair 0 and derives its FFN norm; uploading new rows into
     # pair 0 before T19 must discard that copy.  T19 into pair 1 derives the
