@@ -518,6 +518,13 @@ __global__ __launch_bounds__(GNT) void attention_gqa_fused_kernel(AttnArgs a) {
     gqa_pv_body<D, true>(a, wg, sm.p, LP, sc, mt, ok_all);
 }
 
+// Run r of the scan: tiles [a0, a0 + len) (len 0: empty), the rescale
+// factor of its event (<< 2; r >= 1) and the running max before its tiles.
+struct GqaRun {
+    int64_t old;
+    int32_t a0, len, mb, pad;
+};
+
 struct __attribute__((aligned(16))) GqaScanSmem {
     int32_t tm[GMAXT];          // tile maxima
     int32_t ts[GMAXT];          // tile sums
@@ -525,8 +532,7 @@ struct __attribute__((aligned(16))) GqaScanSmem {
     int16_t ev[GMAXT];          // tile of event k (run k + 1 starts there)
     int32_t rsum[GSLOTS][GSE];  // per run, per element: sum of the tile values
     int32_t rts[GSLOTS];        // per run: sum of the tile sums
-    int32_t rlen[GSLOTS];       // per run: tiles
-    int64_t old[GSLOTS];        // per run: the rescale factor of its event, << 2
+    GqaRun ri[GSLOTS];          // per run: its tiles, rescale factor and running max
     int16_t e14[2056];
     int32_t nev, sum;
 };
@@ -622,7 +628,7 @@ __global__ __launch_bounds__(GNT) void attention_gqa_scan_kernel(AttnArgs a) {
     if (tid < 257) *(v4u*)(sm.e14 + 8 * tid) = exr;
     if (tid == 0) *(v4u*)(sm.e14 + 8 * 256) = exr2;
     for (uint32_t i = tid; i < GSLOTS * GSE; i += GNT) (&sm.rsum[0][0])[i] = 0;
-    if (tid < GSLOTS) sm.rts[tid] = sm.rlen[tid] = 0;
+    if (tid < GSLOTS) sm.rts[tid] = 0;
     lds_barrier();
     // ---- events (wavefront 0): tiles whose maximum exceeds every earlier
     // one and the initial -128.0; run of a tile = events at or before it.
@@ -703,32 +709,44 @@ __global__ __launch_bounds__(GNT) void attention_gqa_scan_kernel(AttnArgs a) {
 #pragma unroll
             for (int q = 0; q < 8; q++) atomicAdd(&sm.rsum[cur][8 * oc + q], part[q]);
         }
-        for (uint32_t j = tid; j < ntiles; j += GNT) {
-            atomicAdd(&sm.rts[sm.run[j]], sm.ts[j]);
-            atomicAdd(&sm.rlen[sm.run[j]], 1);
-        }
-        // run r >= 1 starts at event tile ev[r - 1], whose maximum replaces
-        // that of the event before it (or -128.0)
-        if (tid >= 1 && tid <= nev) {
+        for (uint32_t j = tid; j < ntiles; j += GNT) atomicAdd(&sm.rts[sm.run[j]], sm.ts[j]);
+        // run r: tiles [ev[r - 1], ev[r]) (run 0 from tile 0, the last to the
+        // end); run r >= 1 starts at event tile ev[r - 1], whose maximum
+        // replaces that of the event before it (or -128.0), which is also
+        // the running max before the run
+        if (tid <= nev) {
+            const uint32_t a0 = tid == 0 ? 0 : (uint32_t)sm.ev[tid - 1];
+            const uint32_t a1 = tid == nev ? ntiles : (uint32_t)sm.ev[tid];
             const int32_t mprev = tid >= 2 ? sm.tm[sm.ev[tid - 2]] : INT16_MIN;
-            sm.old[tid] = (int64_t)prob(sm.e14, mprev - sm.tm[sm.ev[tid - 1]]) << 2;
+            GqaRun ru;
+            ru.old = tid ? (int64_t)prob(sm.e14, mprev - sm.tm[a0]) << 2 : 0;
+            ru.a0 = (int32_t)a0;
+            ru.len = a1 > a0 ? (int32_t)(a1 - a0) : 0;
+            ru.mb = mprev;
+            ru.pad = 0;
+            sm.ri[tid] = ru;
         }
         lds_barrier();
         // ---- the sum of the probabilities, once per workgroup (lane 0 of
-        // the second wavefront, beside the elements' chains) ----
+        // the second wavefront, beside the elements' chains); the next
+        // run's operands are read while a run is computed ----
         if (tid == 64) {
-            int32_t sum = 0, m = INT16_MIN;
+            int32_t sum = 0;
+            GqaRun nx = sm.ri[0];
+            int32_t tsn = sm.rts[0];
             for (uint32_t r = 0; r <= nev; r++) {
-                const uint32_t a0 = r == 0 ? 0 : (uint32_t)sm.ev[r - 1];
-                const uint32_t a1 = r == nev ? ntiles : (uint32_t)sm.ev[r];
-                if (a0 >= a1) continue;
-                const int64_t sumr = r ? fx_rnd((int64_t)sum * sm.old[r], 16) : sum;
-                const int64_t t4 = (int64_t)sm.rts[r] << 2;
+                const GqaRun cu = nx;
+                const int32_t ts = tsn;
+                const uint32_t rn = r < nev ? r + 1 : r;
+                nx = sm.ri[rn];
+                tsn = sm.rts[rn];
+                if (cu.len == 0) continue;
+                const int64_t sumr = r ? fx_rnd((int64_t)sum * cu.old, 16) : sum;
+                const int64_t t4 = (int64_t)ts << 2;
                 if (sumr + t4 <= INT32_MAX)
                     sum = (int32_t)(sumr + t4);
                 else
-                    sum = sum_tiles_seq(sm, a0, a1, m, sum);
-                m = sm.tm[a0] > m ? sm.tm[a0] : m;
+                    sum = sum_tiles_seq(sm, cu.a0, cu.a0 + cu.len, cu.mb, sum);
             }
             sm.sum = sum;
         }
@@ -744,18 +762,21 @@ __global__ __launch_bounds__(GNT) void attention_gqa_scan_kernel(AttnArgs a) {
         if (!parallel) {
             acc = acc_tiles_seq(a, sm, tv0, G, D, 0, ntiles, INT16_MIN, 0);
         } else {
-            int32_t m = INT16_MIN;
+            GqaRun nx = sm.ri[0];
+            int32_t rsn = sm.rsum[0][tid];
             for (uint32_t r = 0; r <= nev; r++) {
-                const uint32_t a0 = r == 0 ? 0 : (uint32_t)sm.ev[r - 1];
-                const uint32_t a1 = r == nev ? ntiles : (uint32_t)sm.ev[r];
-                if (a0 >= a1) continue;
-                const int32_t accr = r ? fx_sat32(fx_rnd((int64_t)acc * sm.old[r], 16)) : acc;
+                const GqaRun cu = nx;
+                const int32_t rs = rsn;
+                const uint32_t rn = r < nev ? r + 1 : r;
+                nx = sm.ri[rn];
+                rsn = sm.rsum[rn][tid];
+                if (cu.len == 0) continue;
+                const int32_t accr = r ? fx_sat32(fx_rnd((int64_t)acc * cu.old, 16)) : acc;
                 const int64_t aa = accr < 0 ? -(int64_t)accr : accr;
-                if (aa + ((int64_t)sm.rlen[r] << 23) <= INT32_MAX)
-                    acc = accr + sm.rsum[r][tid] * 256;
+                if (aa + ((int64_t)cu.len << 23) <= INT32_MAX)
+                    acc = accr + rs * 256;
                 else
-                    acc = acc_tiles_seq(a, sm, tv0, G, D, a0, a1, m, acc);
-                m = sm.tm[a0] > m ? sm.tm[a0] : m;
+                    acc = acc_tiles_seq(a, sm, tv0, G, D, cu.a0, cu.a0 + cu.len, cu.mb, acc);
             }
         }
     }

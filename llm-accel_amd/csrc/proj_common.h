@@ -32,11 +32,13 @@ __device__ __forceinline__ uint4 and4(uint4 v, uint32_t m) {
     return make_uint4(v.x & m, v.y & m, v.z & m, v.w & m);
 }
 
-// One input normalised with a constant gain: rnd(x * gain * gamma, 16).
-// |x * gain * gamma| < 2^15 * 2^13 * 2^15, so the product shifted right by 16
-// fits 32 bits before the saturation.
+// One input normalised with a constant gain: rnd(x * gg, 16), gg = gain *
+// gamma (int32), in 32-bit arithmetic: with gg = 2^16 gh + gl (0 <= gl <
+// 2^16), floor((x gg + 2^15) / 2^16) = x gh + floor((x gl + 2^15) / 2^16)
+// exactly, |x gl + 2^15| < 2^31 for int16 x and |x gh| <= 2^30.
 __device__ __forceinline__ int32_t norm1(int32_t x, int32_t gg) {
-    const int32_t y = (int32_t)(((int64_t)x * gg + 32768) >> 16);
+    const int32_t gh = gg >> 16, gl = gg & 0xffff;
+    const int32_t y = x * gh + ((x * gl + 32768) >> 16);
     return y < -32768 ? -32768 : (y > 32767 ? 32767 : y);
 }
 // Eight inputs normalised with a constant gain: rnd(x * gain * gamma, 16);
