@@ -134,17 +134,47 @@ __global__ __launch_bounds__(64 * WPB) void proj_kernel(ProjArgs a) {
 
     if constexpr (SPW > 0) {
         const uint32_t cnt = s1 - s0;  // <= SPW (the launcher's choice)
-        uint4 wv[SPW][NM], xv[SPW][RT], gv[SPW];
+        uint4 wv[SPW][NM], xv[SPW][RT];
+        // EPI_STORE_NORM_IN: lane l loads and normalises columns 2l, 2l + 1
+        // of each step and row (once per wavefront, not once per row of the
+        // block), shared through LDS
+        constexpr bool NIN = EPI == EPI_STORE_NORM_IN;
+        uint32_t x2[SPW][RT], g2[SPW];
 #pragma unroll
         for (int u = 0; u < SPW; u++) {
             const uint32_t du = cnt == 0 ? 0 : ((uint32_t)u < cnt ? u : cnt - 1);
             wv[u][0] = *(const uint4*)(wp0 + (size_t)du * 512);
             if (NM == 2) wv[u][NM - 1] = *(const uint4*)(wp1 + (size_t)du * 512);
+            if constexpr (NIN) {
 #pragma unroll
-            for (int r = 0; r < RT; r++)
-                xv[u][r] = *(const uint4*)(xp + (size_t)r * a.ldx + du * 128);
-            if (EPI == EPI_STORE_NORM_IN)
-                gv[u] = *(const uint4*)(a.in_gamma + (s0 + du) * 128 + j * 8);
+                for (int r = 0; r < RT; r++)
+                    x2[u][r] = *(const uint32_t*)(a.x + (size_t)r * a.ldx +
+                                                  (size_t)(s0 + du) * 128 + 2 * lane);
+                g2[u] = *(const uint32_t*)(a.in_gamma + (s0 + du) * 128 + 2 * lane);
+            } else {
+#pragma unroll
+                for (int r = 0; r < RT; r++)
+                    xv[u][r] = *(const uint4*)(xp + (size_t)r * a.ldx + du * 128);
+            }
+        }
+        if constexpr (NIN) {
+            // a wavefront's LDS operations complete in order: no barrier
+            __shared__ uint32_t xs[WPB][SPW][RT][64];
+#pragma unroll
+            for (int u = 0; u < SPW; u++) {
+                const int32_t glo = a.in_gain * (int16_t)(g2[u] & 0xffff);
+                const int32_t ghi = a.in_gain * (int16_t)(g2[u] >> 16);
+#pragma unroll
+                for (int r = 0; r < RT; r++) {
+                    const int32_t lo16 = norm1((int16_t)(x2[u][r] & 0xffff), glo);
+                    const int32_t hi16 = norm1((int16_t)(x2[u][r] >> 16), ghi);
+                    xs[wave][u][r][lane] = (uint32_t)(uint16_t)lo16 | ((uint32_t)hi16 << 16);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < SPW; u++)
+#pragma unroll
+                for (int r = 0; r < RT; r++) xv[u][r] = *(const uint4*)&xs[wave][u][r][4 * j];
         }
         // every step is computed: no branch may separate a load from its
         // use, or the compiler sinks the load into the branch; steps past
@@ -154,10 +184,6 @@ __global__ __launch_bounds__(64 * WPB) void proj_kernel(ProjArgs a) {
             const uint32_t keep = lane_mask((uint32_t)u < cnt);
 #pragma unroll
             for (int m = 0; m < NM; m++) wv[u][m] = and4(wv[u][m], keep);
-            if (EPI == EPI_STORE_NORM_IN) {
-#pragma unroll
-                for (int r = 0; r < RT; r++) xv[u][r] = norm8(xv[u][r], gv[u], a.in_gain);
-            }
 #pragma unroll
             for (int m = 0; m < NM; m++)
 #pragma unroll
@@ -313,6 +339,10 @@ __global__ __launch_bounds__(64 * WPB) void proj_p12_kernel(ProjArgs a) {
     uint2 lo[SPW][NM];
     uint32_t hi[SPW][NM];
     uint4 xv[SPW][RT], gv[SPW];
+    uint32_t x2[SPW], g2[SPW];
+    // EPI_STORE_NORM_IN (one row: the kernel's only use): lane l loads and
+    // normalises columns 2l, 2l + 1 of each step once per wavefront
+    constexpr bool NIN = EPI == EPI_STORE_NORM_IN && RT == 1;
 #pragma unroll
     for (int u = 0; u < SPW; u++) {
         const uint32_t du = cnt == 0 ? 0 : ((uint32_t)u < cnt ? u : cnt - 1);
@@ -321,10 +351,29 @@ __global__ __launch_bounds__(64 * WPB) void proj_p12_kernel(ProjArgs a) {
             lo[u][m] = *(const uint2*)(wp[m] + (size_t)du * 768 + 8 * lane);
             hi[u][m] = *(const uint32_t*)(wp[m] + (size_t)du * 768 + 512 + 4 * lane);
         }
+        if constexpr (NIN) {
+            // columns 2 lane, 2 lane + 1 of the step (normalised once per wave)
+            x2[u] = *(const uint32_t*)(a.x + (size_t)(s0 + du) * 128 + 2 * lane);
+            g2[u] = *(const uint32_t*)(a.in_gamma + (s0 + du) * 128 + 2 * lane);
+        } else {
 #pragma unroll
-        for (int r = 0; r < RT; r++) xv[u][r] = *(const uint4*)(xp + (size_t)r * a.ldx + du * 128);
-        if (EPI == EPI_STORE_NORM_IN)  // the norm table is padded to whole k-steps
-            gv[u] = *(const uint4*)(a.in_gamma + (s0 + du) * 128 + j * 8);
+            for (int r = 0; r < RT; r++) xv[u][r] = *(const uint4*)(xp + (size_t)r * a.ldx + du * 128);
+            if (EPI == EPI_STORE_NORM_IN)  // the norm table is padded to whole k-steps
+                gv[u] = *(const uint4*)(a.in_gamma + (s0 + du) * 128 + j * 8);
+        }
+    }
+    if constexpr (NIN) {
+        // the wave's steps normalised, 2 columns per lane, shared through
+        // LDS (a wavefront's LDS operations complete in order)
+        __shared__ uint32_t xs[WPB][SPW][64];
+#pragma unroll
+        for (int u = 0; u < SPW; u++) {
+            const int32_t lo16 = norm1((int16_t)(x2[u] & 0xffff), a.in_gain * (int16_t)(g2[u] & 0xffff));
+            const int32_t hi16 = norm1((int16_t)(x2[u] >> 16), a.in_gain * (int16_t)(g2[u] >> 16));
+            xs[wave][u][lane] = (uint32_t)(uint16_t)lo16 | ((uint32_t)hi16 << 16);
+        }
+#pragma unroll
+        for (int u = 0; u < SPW; u++) xv[u][0] = *(const uint4*)&xs[wave][u][4 * j];
     }
     int32_t pl[NM][RT], ph[NM][RT], sx[RT];
 #pragma unroll
@@ -340,8 +389,8 @@ __global__ __launch_bounds__(64 * WPB) void proj_p12_kernel(ProjArgs a) {
         const uint32_t keep = lane_mask((uint32_t)u < cnt);
 #pragma unroll
         for (int r = 0; r < RT; r++) {
-            const uint4 x = and4(EPI == EPI_STORE_NORM_IN ? norm8(xv[u][r], gv[u], a.in_gain)
-                                                          : xv[u][r],
+            const uint4 x = and4(EPI == EPI_STORE_NORM_IN && !NIN ? norm8(xv[u][r], gv[u], a.in_gain)
+                                                                  : xv[u][r],
                                  keep);
             sx[r] = dot2(0x00010001u, x.x, sx[r]);
             sx[r] = dot2(0x00010001u, x.y, sx[r]);

@@ -186,21 +186,56 @@ __device__ __forceinline__ bool proj_block(const ProjArgs& a, uint32_t b, int64_
             wv[nb][u] = *(const uint4*)(wp + (size_t)du * 512);
         }
     }
+    // EPI_STORE_NORM_IN: lane l normalises columns 2l, 2l + 1 of each of
+    // the wavefront's steps and rows (once per wavefront, not once per row
+    // of the block), shared through LDS
+    constexpr bool NIN = EPI == EPI_STORE_NORM_IN;
+    uint32_t g2[SPW];
 #pragma unroll
     for (int u = 0; u < SPW; u++) {
         const uint32_t du = cnt == 0 ? 0 : ((uint32_t)u < cnt ? u : cnt - 1);
-        if (EPI == EPI_STORE_NORM_IN)
-            gv[u] = *(const uint4*)(a.in_gamma + (s0 + du) * 128 + j * 8);
+        if (NIN) g2[u] = *(const uint32_t*)(a.in_gamma + (s0 + du) * 128 + 2 * lane);
     }
+    (void)gv;
     if (!wait()) return false;
     uint4 xv[SPW][RT];
+    if constexpr (NIN) {
+        uint32_t x2[SPW][RT];
 #pragma unroll
-    for (int u = 0; u < SPW; u++) {
-        const uint32_t du = cnt == 0 ? 0 : ((uint32_t)u < cnt ? u : cnt - 1);
+        for (int u = 0; u < SPW; u++) {
+            const uint32_t du = cnt == 0 ? 0 : ((uint32_t)u < cnt ? u : cnt - 1);
 #pragma unroll
-        for (int r = 0; r < RT; r++) {
-            const int16_t* px = xp + (size_t)r * a.ldx + du * 128;
-            xv[u][r] = XCOH ? ld_coherent16(px) : *(const uint4*)px;
+            for (int r = 0; r < RT; r++) {
+                const int16_t* px = a.x + (size_t)r * a.ldx + (size_t)(s0 + du) * 128 + 2 * lane;
+                x2[u][r] = XCOH ? ld_coherent((const uint32_t*)px) : *(const uint32_t*)px;
+            }
+        }
+        // a wavefront's LDS operations complete in order: no barrier
+        __shared__ uint32_t xs[WPB][SPW][RT][64];
+#pragma unroll
+        for (int u = 0; u < SPW; u++) {
+            const int32_t glo = a.in_gain * (int16_t)(g2[u] & 0xffff);
+            const int32_t ghi = a.in_gain * (int16_t)(g2[u] >> 16);
+#pragma unroll
+            for (int r = 0; r < RT; r++) {
+                const int32_t lo16 = norm1((int16_t)(x2[u][r] & 0xffff), glo);
+                const int32_t hi16 = norm1((int16_t)(x2[u][r] >> 16), ghi);
+                xs[wave][u][r][lane] = (uint32_t)(uint16_t)lo16 | ((uint32_t)hi16 << 16);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < SPW; u++)
+#pragma unroll
+            for (int r = 0; r < RT; r++) xv[u][r] = *(const uint4*)&xs[wave][u][r][4 * j];
+    } else {
+#pragma unroll
+        for (int u = 0; u < SPW; u++) {
+            const uint32_t du = cnt == 0 ? 0 : ((uint32_t)u < cnt ? u : cnt - 1);
+#pragma unroll
+            for (int r = 0; r < RT; r++) {
+                const int16_t* px = xp + (size_t)r * a.ldx + du * 128;
+                xv[u][r] = XCOH ? ld_coherent16(px) : *(const uint4*)px;
+            }
         }
     }
     int32_t part[NB][RT];
@@ -214,8 +249,7 @@ __device__ __forceinline__ bool proj_block(const ProjArgs& a, uint32_t b, int64_
         const uint32_t keep = lane_mask((uint32_t)u < cnt);
 #pragma unroll
         for (int r = 0; r < RT; r++) {
-            const uint4 x = EPI == EPI_STORE_NORM_IN ? norm8(xv[u][r], gv[u], a.in_gain)
-                                                     : xv[u][r];
+            const uint4 x = xv[u][r];
 #pragma unroll
             for (int nb = 0; nb < NB; nb++) {
                 const uint4 w = and4(wv[nb][u], keep);
