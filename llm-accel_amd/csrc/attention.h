@@ -55,6 +55,10 @@ struct AttnArgs {
     // every launch since s_gmax32 was last cleared)
     uint32_t epoch;
     int32_t* s_gmax32;
+    // ... and, with the scan in the same launch, the tile sums as
+    // s_gsum64 [8][kv_heads][max_tiles][group] = epoch << 32 | sum, stored
+    // after the tile's values (null: the scan is a launch of its own)
+    uint64_t* s_gsum64;
     uint32_t* abort;      // device word set when a wait gave up
     uint32_t* host_abort; // host-visible copy
     uint32_t wait_limit;  // bound of one wait (100 MHz ticks)
@@ -72,8 +76,8 @@ constexpr size_t counter_words(uint32_t num_heads, uint32_t tiles) {
     return (size_t)8 * num_heads * (1 + tile_groups(tiles)) * kCounterStride;
 }
 
-// Epochs of the GQA path's tagged maxima run 1..kGqaEpochMax; then the
-// host clears s_gmax32 and starts again.
+// Epochs of the GQA path's tagged maxima and sums run 1..kGqaEpochMax;
+// then the host clears s_gmax32 and s_gsum64 and starts again.
 constexpr uint32_t kGqaEpochMax = 65535;
 
 // Tiles per split-path workgroup: at most kMaxChunkTiles.

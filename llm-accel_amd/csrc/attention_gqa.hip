@@ -4,7 +4,10 @@
 // golden_tiled_flash_attention_q2_14, raw-payload semantics,
 // host/host_qwen_8x64.cpp:3609-3738; the controller gives each compute
 // unit one KV head and runs the whole query group against each 64-position
-// tile, kernel/control_cache_8x64.cpp:5604-5748).  Three launches:
+// tile, kernel/control_cache_8x64.cpp:5604-5748).  Three steps, in one
+// launch when the grid is resident (attention_gqa_fused_kernel: the tiles'
+// maxima and sums handed to the scan's workgroups as epoch-tagged words),
+// else in two or three launches:
 //   (1) scores: one workgroup per (row, KV head, tile) stages the tile's K
 //       rows in LDS once and forms the scores and tile maxima of all G query
 //       heads; the K row of each row's own position is appended;
@@ -267,6 +270,8 @@ struct __attribute__((aligned(16))) GqaPvSmem {
     int16_t p[GMAXG][TILE], cp[GMAXG][TILE];  // probabilities, c(p), bank-paired
     int16_t e14[2056];                  // Q2.14 exp table
     int32_t mrun[GMAXG];                // running max before the tile, per head
+    int32_t tsum[GMAXG];                // the tile's probability sums (SCAN)
+    int16_t tv[GMAXG][D];               // the tile's values, staged (SCAN)
 };
 
 // One-launch GQA path: a context of at most kGqaFusedMaxTiles tiles, so that
@@ -319,7 +324,7 @@ __device__ __forceinline__ void gqa_pv_loads(const AttnArgs& a, const GqaWg& wg,
     }
 }
 
-template <int D, bool FUSED>
+template <int D, bool FUSED, bool SCAN = false>
 __device__ __forceinline__ bool gqa_pv_body(const AttnArgs& a, const GqaWg& wg,
                                             GqaPvSmem<D>& sm, const GqaPvLoads<D>& L,
                                             const int32_t (&sci)[2],
@@ -439,7 +444,12 @@ __device__ __forceinline__ bool gqa_pv_body(const AttnArgs& a, const GqaWg& wg,
         sm.p[gi][paired(lane)] = (int16_t)pr;
         sm.cp[gi][paired(lane)] = (int16_t)sat_corr(pr);
         const int32_t tsum = wave_sum(pr);  // <= 64 * 16384
-        if (lane == 0) a.s_tsum[(rh * a.max_tiles + tile) * G + gi] = tsum;
+        if (lane == 0) {
+            if (SCAN)
+                sm.tsum[gi] = tsum;
+            else
+                a.s_tsum[(rh * a.max_tiles + tile) * G + gi] = tsum;
+        }
     }
     lds_barrier();
     // ---- PV: element e, heads e_set + NHS k ----
@@ -472,10 +482,28 @@ __device__ __forceinline__ bool gqa_pv_body(const AttnArgs& a, const GqaWg& wg,
         int32_t tv = fx_sat32((int64_t)b0 + b1 + b2 + b3);
         tv = fx_sat32(fx_rnd((int64_t)tv * 1024, 16));
         tv = fx_sat16(fx_rnd(tv, 8));
-        a.s_tval[((rh * a.max_tiles + tile) * G + gi) * D + e] = (int16_t)tv;
+        if (SCAN)
+            sm.tv[gi][e] = (int16_t)tv;
+        else
+            a.s_tval[((rh * a.max_tiles + tile) * G + gi) * D + e] = (int16_t)tv;
     }
     if (own / TILE == tile && tid < D)  // this row's V into the cache
         a.vcache[page_off<D>(a, h, tile) + tid * TILE + paired(own % TILE)] = sm.vb[t][tid];
+    if (SCAN) {
+        // the tile's G x D values (contiguous in s_tval) go out in 8-byte
+        // device-coherent stores; once they are performed (every wavefront
+        // waited for its stores) the sums go out tagged: a scan workgroup
+        // that sees a sum's epoch reads the values after
+        lds_barrier();
+        uint64_t* dst = (uint64_t*)(a.s_tval + (rh * a.max_tiles + tile) * G * D);
+        const uint64_t* src = (const uint64_t*)&sm.tv[0][0];
+        for (uint32_t i = tid; i < G * D / 4; i += GNT) st_coherent(dst + i, src[i]);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (tid < G)
+            st_coherent(&a.s_gsum64[(rh * a.max_tiles + tile) * G + tid],
+                        ((uint64_t)a.epoch << 32) | (uint32_t)sm.tsum[tid]);
+    }
     return true;
 }
 
@@ -491,31 +519,10 @@ __global__ __launch_bounds__(GNT) void attention_gqa_pv_kernel(AttnArgs a) {
     gqa_pv_body<D, false>(a, wg, sm, L, none, none, unused);
 }
 
-// Scores and PV in one launch (at most kGqaFusedMaxTiles tiles; launched
-// only when the whole grid fits on the device at once, so that the tiles a
-// workgroup waits for are all running): the scores phase publishes the
-// tile's tagged maxima, the PV phase issues its loads, then waits for the
-// earlier tiles' maxima.
-template <int D>
-__global__ __launch_bounds__(GNT) void attention_gqa_fused_kernel(AttnArgs a) {
-    __shared__ union {
-        GqaScoresSmem<D> s;
-        GqaPvSmem<D> p;
-    } sm;
-    __shared__ uint32_t ok_all;
-    GqaWg wg;
-    if (!gqa_wg(a, wg)) return;
-    if (threadIdx.x == 0) ok_all = 1;  // ordered by the scores phase's barriers
-    // both phases' loads first (the V page arrives while the scores are
-    // computed: loads complete in order, the K page's first)
-    GqaScoresLoads<D> LS;
-    gqa_scores_loads<D>(a, wg, LS);
-    GqaPvLoads<D> LP;
-    gqa_pv_loads<D>(a, wg, LP);
-    int32_t sc[2], mt[2];
-    gqa_scores_body<D, true>(a, wg, sm.s, LS, sc, mt);
-    __syncthreads();  // the scores phase's LDS use ends
-    gqa_pv_body<D, true>(a, wg, sm.p, LP, sc, mt, ok_all);
+// 16 bytes of tile values read with device-coherent loads.
+__device__ __forceinline__ v4u ld_coherent_v4(const int16_t* p) {
+    const uint4 u = ld_coherent16(p);
+    return v4u{u.x, u.y, u.z, u.w};
 }
 
 // Run r of the scan: tiles [a0, a0 + len) (len 0: empty), the rescale
@@ -539,6 +546,7 @@ struct __attribute__((aligned(16))) GqaScanSmem {
 
 // The per-tile recurrence of the accumulator of one element over tiles
 // [j0, j1) (the reference's order), from running max m.
+template <bool FUSED>
 __device__ __forceinline__ int32_t acc_tiles_seq(const AttnArgs& a, const GqaScanSmem& sm,
                                                  size_t tv0, uint32_t G, uint32_t D,
                                                  uint32_t j0, uint32_t j1, int32_t m,
@@ -548,7 +556,8 @@ __device__ __forceinline__ int32_t acc_tiles_seq(const AttnArgs& a, const GqaSca
 #pragma unroll
         for (int u = 0; u < 16; u++) {
             const uint32_t j = jb + u < j1 ? jb + u : j0;
-            tvv[u] = a.s_tval[tv0 + (size_t)j * G * D];
+            const int16_t* src = a.s_tval + tv0 + (size_t)j * G * D;
+            tvv[u] = FUSED ? ld_coherent(src) : *src;
         }
 #pragma unroll
         for (int u = 0; u < 16; u++) {  // no early exit: tvv stays in registers
@@ -582,14 +591,21 @@ __device__ __forceinline__ int32_t sum_tiles_seq(const GqaScanSmem& sm, uint32_t
     return sum;
 }
 
-template <int D>
-__global__ __launch_bounds__(GNT) void attention_gqa_scan_kernel(AttnArgs a) {
+// The scan of workgroup `bid` (row, query head, 32 elements).  FUSED: a
+// workgroup of the one-launch GQA kernel; the tile maxima and sums are
+// awaited as tagged words (bounded; a wavefront that gives up clears
+// ok_all and the workgroup returns) and the tile values read with
+// device-coherent loads after their sums were seen.
+template <int D, bool FUSED>
+__device__ __forceinline__ void gqa_scan_body(const AttnArgs& a, GqaScanSmem& sm, uint32_t bid,
+                                              uint32_t& ok_all) {
     static_assert(D == 64 || D == 128, "GQA tile path: head_dim 64 or 128");
+    static_assert(kGqaFusedMaxTiles <= 2 * GNT, "two tagged words per thread");
     constexpr uint32_t ES = D / GSE;                // workgroups per (row, head)
     constexpr uint32_t C8 = GSE / 8, NSL = GNT / C8;  // element octets, tile slices
     constexpr int TVB = 8;                          // tile-value loads in flight per thread
-    __shared__ GqaScanSmem sm;
-    const uint32_t es = blockIdx.x % ES, tg = blockIdx.x / ES;
+    constexpr int NU = FUSED ? 2 : (int)(GMAXT / GNT);  // tiles per thread (maxima, sums)
+    const uint32_t es = bid % ES, tg = bid / ES;
     const uint32_t t = tg / a.num_heads, g = tg % a.num_heads;
     if (t >= a.grid_rows) return;
     const uint32_t tid = threadIdx.x, lane = tid & 63;
@@ -599,30 +615,53 @@ __global__ __launch_bounds__(GNT) void attention_gqa_scan_kernel(AttnArgs a) {
     const size_t tv_base = (rh * a.max_tiles * G + gi) * D + GSE * es;  // + j G D + e
     // ---- every load that does not depend on another is issued first: tile
     // maxima and sums, the exp table, this thread's first tile values ----
-    int32_t tmr[GMAXT / GNT], tsr[GMAXT / GNT];
+    int32_t tmr[NU], tsr[NU];
+    if (!FUSED) {
 #pragma unroll
-    for (int u = 0; u < (int)(GMAXT / GNT); u++) {
-        const uint32_t j = tid + GNT * u < ntiles ? tid + GNT * u : 0;
-        tmr[u] = a.s_tmax[(rh * a.max_tiles + j) * G + gi];
-        tsr[u] = a.s_tsum[(rh * a.max_tiles + j) * G + gi];
+        for (int u = 0; u < NU; u++) {
+            const uint32_t j = tid + GNT * u < ntiles ? tid + GNT * u : 0;
+            tmr[u] = a.s_tmax[(rh * a.max_tiles + j) * G + gi];
+            tsr[u] = a.s_tsum[(rh * a.max_tiles + j) * G + gi];
+        }
     }
     const v4u exr = *(const v4u*)(a.exp14 + 8 * (tid < 257 ? tid : 256));
     const v4u exr2 = *(const v4u*)(a.exp14 + 8 * 256);
     const uint32_t oc = tid % C8, sl = tid / C8;
     const uint32_t per = (ntiles + NSL - 1) / NSL;
     const uint32_t j0 = sl * per, j1 = j0 + per < ntiles ? j0 + per : ntiles;
+    const size_t tw0 = (rh * a.max_tiles) * G + gi;  // tagged word of tile j: tw0 + j G
     v4u ld[TVB];
+    if (!FUSED) {
 #pragma unroll
-    for (int u = 0; u < TVB; u++) {
-        const uint32_t j = j0 + u < j1 ? j0 + u : (j0 < j1 ? j0 : 0);
-        ld[u] = *(const v4u*)(a.s_tval + tv_base + (size_t)j * G * D + 8 * oc);
+        for (int u = 0; u < TVB; u++) {
+            const uint32_t j = j0 + u < j1 ? j0 + u : (j0 < j1 ? j0 : 0);
+            ld[u] = *(const v4u*)(a.s_tval + tv_base + (size_t)j * G * D + 8 * oc);
+        }
+    } else {
+        // the tile maxima, each read until it carries this launch's epoch
+        const TagWait tw{(uint64_t)wall_clock64(), a.wait_limit, a.abort, a.host_abort};
+        while (true) {
+            bool ok = true;
+#pragma unroll
+            for (int u = 0; u < NU; u++) {
+                const uint32_t j = tid + GNT * u;
+                const uint32_t wd = (uint32_t)ld_coherent(&a.s_gmax32[tw0 + (size_t)(j < ntiles ? j : 0) * G]);
+                ok = ok && (j >= ntiles || tag_ok(wd, 16, a.epoch));
+                tmr[u] = (int32_t)(int16_t)(wd & 0xffffu);
+            }
+            if (__all(ok)) break;
+            if (!tw.keep_waiting()) {
+                ok_all = 0;
+                break;
+            }
+        }
     }
 #pragma unroll
-    for (int u = 0; u < (int)(GMAXT / GNT); u++) {
+    for (int u = 0; u < NU; u++) {
         const uint32_t j = tid + GNT * u;
         if (j < ntiles) {
             sm.tm[j] = tmr[u];
-            sm.ts[j] = tsr[u];
+            if (!FUSED) sm.ts[j] = tsr[u];
         }
     }
     if (tid < 257) *(v4u*)(sm.e14 + 8 * tid) = exr;
@@ -630,6 +669,7 @@ __global__ __launch_bounds__(GNT) void attention_gqa_scan_kernel(AttnArgs a) {
     for (uint32_t i = tid; i < GSLOTS * GSE; i += GNT) (&sm.rsum[0][0])[i] = 0;
     if (tid < GSLOTS) sm.rts[tid] = 0;
     lds_barrier();
+    if (FUSED && ok_all == 0) return;  // uniform: read after the barrier
     // ---- events (wavefront 0): tiles whose maximum exceeds every earlier
     // one and the initial -128.0; run of a tile = events at or before it.
     // Lane L holds tiles [L T, L T + T).
@@ -666,7 +706,43 @@ __global__ __launch_bounds__(GNT) void attention_gqa_scan_kernel(AttnArgs a) {
         }
         if (lane == 63) sm.nev = (int32_t)c;
     }
-    lds_barrier();
+    if (FUSED) {
+        // the tile sums (tagged after the tiles' values were performed),
+        // then this thread's first tile values
+        const TagWait tw{(uint64_t)wall_clock64(), a.wait_limit, a.abort, a.host_abort};
+        while (true) {
+            bool ok = true;
+#pragma unroll
+            for (int u = 0; u < NU; u++) {
+                const uint32_t j = tid + GNT * u;
+                const uint64_t wd = ld_coherent(&a.s_gsum64[tw0 + (size_t)(j < ntiles ? j : 0) * G]);
+                ok = ok && (j >= ntiles || (uint32_t)(wd >> 32) == a.epoch);
+                tsr[u] = (int32_t)(uint32_t)wd;
+            }
+            if (__all(ok)) break;
+            if (!tw.keep_waiting()) {
+                ok_all = 0;
+                break;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < NU; u++) {
+            const uint32_t j = tid + GNT * u;
+            if (j < ntiles) sm.ts[j] = tsr[u];
+        }
+        // a wavefront has seen the sums of its own tiles only; a thread's
+        // slice of tile values spans other wavefronts' tiles, so every
+        // wavefront's wait ends before any value is read
+        lds_barrier();
+        if (ok_all == 0) return;  // uniform: read after the barrier
+#pragma unroll
+        for (int u = 0; u < TVB; u++) {
+            const uint32_t j = j0 + u < j1 ? j0 + u : (j0 < j1 ? j0 : 0);
+            ld[u] = ld_coherent_v4(a.s_tval + tv_base + (size_t)j * G * D + 8 * oc);
+        }
+    } else {
+        lds_barrier();  // the events
+    }
     const uint32_t nev = (uint32_t)sm.nev;
     const bool parallel = nev + 1 <= GSLOTS;
     if (parallel) {
@@ -680,7 +756,8 @@ __global__ __launch_bounds__(GNT) void attention_gqa_scan_kernel(AttnArgs a) {
 #pragma unroll
                 for (int u = 0; u < TVB; u++) {
                     const uint32_t j = jb + u < j1 ? jb + u : j0;
-                    ld[u] = *(const v4u*)(a.s_tval + tv_base + (size_t)j * G * D + 8 * oc);
+                    const int16_t* src = a.s_tval + tv_base + (size_t)j * G * D + 8 * oc;
+                    ld[u] = FUSED ? ld_coherent_v4(src) : *(const v4u*)src;
                 }
             }
 #pragma unroll
@@ -760,7 +837,7 @@ __global__ __launch_bounds__(GNT) void attention_gqa_scan_kernel(AttnArgs a) {
     if (tid < GSE) {
         const size_t tv0 = tv_base + tid;
         if (!parallel) {
-            acc = acc_tiles_seq(a, sm, tv0, G, D, 0, ntiles, INT16_MIN, 0);
+            acc = acc_tiles_seq<FUSED>(a, sm, tv0, G, D, 0, ntiles, INT16_MIN, 0);
         } else {
             GqaRun nx = sm.ri[0];
             int32_t rsn = sm.rsum[0][tid];
@@ -776,7 +853,7 @@ __global__ __launch_bounds__(GNT) void attention_gqa_scan_kernel(AttnArgs a) {
                 if (aa + ((int64_t)cu.len << 23) <= INT32_MAX)
                     acc = accr + rs * 256;
                 else
-                    acc = acc_tiles_seq(a, sm, tv0, G, D, cu.a0, cu.a0 + cu.len, cu.mb, acc);
+                    acc = acc_tiles_seq<FUSED>(a, sm, tv0, G, D, cu.a0, cu.a0 + cu.len, cu.mb, acc);
             }
         }
     }
@@ -786,14 +863,70 @@ __global__ __launch_bounds__(GNT) void attention_gqa_scan_kernel(AttnArgs a) {
             fx_sat16(fx_rnd((int64_t)acc * fx_inv_sum(sm.sum), 16));
 }
 
-// Workgroups of the one-launch GQA kernel the device holds at once.
 template <int D>
+__global__ __launch_bounds__(GNT) void attention_gqa_scan_kernel(AttnArgs a) {
+    __shared__ GqaScanSmem sm;
+    uint32_t unused = 1;
+    gqa_scan_body<D, false>(a, sm, blockIdx.x, unused);
+}
+
+template <int D, bool SCAN>
+union GqaFusedSmem {
+    GqaScoresSmem<D> s;
+    GqaPvSmem<D> p;
+};
+template <int D>
+union GqaFusedSmem<D, true> {
+    GqaScoresSmem<D> s;
+    GqaPvSmem<D> p;
+    GqaScanSmem c;
+};
+
+// Scores and PV in one launch (at most kGqaFusedMaxTiles tiles; launched
+// only when the whole grid fits on the device at once, so that the tiles a
+// workgroup waits for are all running): the scores phase publishes the
+// tile's tagged maxima, the PV phase issues its loads, then waits for the
+// earlier tiles' maxima.  SCAN: the scan's workgroups follow the tiles'
+// in the same grid; the tiles publish their sums tagged after their
+// values, and each scan workgroup forms its events as soon as the maxima
+// are in, while the tiles' PV phases run.
+template <int D, bool SCAN>
+__global__ __launch_bounds__(GNT) void attention_gqa_fused_kernel(AttnArgs a) {
+    __shared__ GqaFusedSmem<D, SCAN> sm;
+    __shared__ uint32_t ok_all;
+    if (SCAN) {
+        const uint32_t tile_wgs = a.grid_rows * a.grid_tiles * a.num_kv_heads;
+        if (blockIdx.x >= tile_wgs) {
+            if (threadIdx.x == 0) ok_all = 1;
+            __syncthreads();
+            if constexpr (SCAN) gqa_scan_body<D, true>(a, sm.c, blockIdx.x - tile_wgs, ok_all);
+            return;
+        }
+    }
+    GqaWg wg;
+    if (!gqa_wg(a, wg)) return;
+    if (threadIdx.x == 0) ok_all = 1;  // ordered by the scores phase's barriers
+    // both phases' loads first (the V page arrives while the scores are
+    // computed: loads complete in order, the K page's first)
+    GqaScoresLoads<D> LS;
+    gqa_scores_loads<D>(a, wg, LS);
+    GqaPvLoads<D> LP;
+    gqa_pv_loads<D>(a, wg, LP);
+    int32_t sc[2], mt[2];
+    gqa_scores_body<D, true>(a, wg, sm.s, LS, sc, mt);
+    __syncthreads();  // the scores phase's LDS use ends
+    gqa_pv_body<D, true, SCAN>(a, wg, sm.p, LP, sc, mt, ok_all);
+}
+
+// Workgroups of the one-launch GQA kernel the device holds at once.
+template <int D, bool SCAN>
 uint32_t gqa_fused_capacity(uint32_t cus) {
     static int per_cu = -1;
     if (per_cu < 0) {
         int nb = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                &nb, reinterpret_cast<const void*>(&attention_gqa_fused_kernel<D>), GNT, 0) !=
+                &nb, reinterpret_cast<const void*>(&attention_gqa_fused_kernel<D, SCAN>), GNT,
+                0) !=
             hipSuccess)
             nb = 0;
         per_cu = nb;
@@ -807,10 +940,15 @@ hipError_t launch_gqa_d(const AttnArgs& a, uint32_t rows, uint32_t tiles, hipStr
     g.grid_rows = rows;
     g.grid_tiles = tiles;
     const uint32_t grid = rows * tiles * a.num_kv_heads;
+    const uint32_t scan_grid = rows * a.num_heads * (D / GSE);
+    const bool one = a.epoch && a.s_gmax32 && tiles <= kGqaFusedMaxTiles;
     hipError_t e;
-    if (a.epoch && a.s_gmax32 && tiles <= kGqaFusedMaxTiles &&
-        grid <= gqa_fused_capacity<D>(a.cus)) {
-        attention_gqa_fused_kernel<D><<<grid, GNT, 0, st>>>(g);
+    if (one && a.s_gsum64 && grid + scan_grid <= gqa_fused_capacity<D, true>(a.cus)) {
+        attention_gqa_fused_kernel<D, true><<<grid + scan_grid, GNT, 0, st>>>(g);
+        return hipGetLastError();
+    }
+    if (one && grid <= gqa_fused_capacity<D, false>(a.cus)) {
+        attention_gqa_fused_kernel<D, false><<<grid, GNT, 0, st>>>(g);
         e = hipGetLastError();
         if (e != hipSuccess) return e;
     } else {
@@ -821,7 +959,7 @@ hipError_t launch_gqa_d(const AttnArgs& a, uint32_t rows, uint32_t tiles, hipStr
         e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
-    attention_gqa_scan_kernel<D><<<rows * a.num_heads * (D / GSE), GNT, 0, st>>>(g);
+    attention_gqa_scan_kernel<D><<<scan_grid, GNT, 0, st>>>(g);
     return hipGetLastError();
 }
 

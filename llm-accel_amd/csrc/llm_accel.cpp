@@ -157,6 +157,10 @@ struct llm_ctx {
     // GQA scores and PV in one launch when the grid fits on the device;
     // LLM_ACCEL_GQA_FUSED=0 keeps three launches
     bool gqa_fused = true;
+    // ... with the run-sum scan as workgroups of that launch (tagged tile
+    // sums in s_gsum64); LLM_ACCEL_GQA_SCAN_FUSED=0 keeps it a launch
+    uint64_t* s_gsum64 = nullptr;
+    bool gqa_scan_fused = true;
     uint32_t sync_qkv[32] = {};        // QKV arrivals per line so far, mod 2^32
     uint32_t sync_attn = 0;            // attention arrivals per line, mod 2^32
     // bound of one wait (100 MHz ticks); LLM_ACCEL_WAIT_LIMIT overrides it
@@ -591,11 +595,13 @@ int enqueue_attention_sublayer(llm_ctx* c, uint32_t layer, uint32_t R,
     at.tile_fused = c->tile_fused ? 1u : 0u;
     at.s_tmax32 = c->s_tmax32;
     at.s_gmax32 = c->s_gmax32;
+    at.s_gsum64 = c->gqa_scan_fused ? c->s_gsum64 : nullptr;
     if (at.use_gqa && c->gqa_fused) {
-        // a fresh epoch for the GQA path's tagged maxima; past the last one
-        // s_gmax32 is cleared (stream-ordered before this launch)
+        // a fresh epoch for the GQA path's tagged maxima and sums; past the
+        // last one both are cleared (stream-ordered before this launch)
         if (++c->gqa_epoch > llm::kGqaEpochMax) {
             HIP_TRY(hipMemsetAsync(c->s_gmax32, 0, c->rht_words * 4, c->stream));
+            HIP_TRY(hipMemsetAsync(c->s_gsum64, 0, c->rht_words * 8, c->stream));
             c->gqa_epoch = 1;
         }
         at.epoch = c->gqa_epoch;
@@ -1051,6 +1057,7 @@ int llm_ctx_create(const llm_shape_t* shape, int device, uint32_t num_pairs,
         (rc = dev_alloc(c, (void**)&c->counters, c->counter_bytes)) ||
         (rc = dev_alloc(c, (void**)&c->s_tmax32, rht * 4)) ||
         (rc = dev_alloc(c, (void**)&c->s_gmax32, rht * 4)) ||
+        (rc = dev_alloc(c, (void**)&c->s_gsum64, rht * 8)) ||
 
         (rc = dev_alloc(c, (void**)&c->sync, (size_t)llm::kSyncWords * 4)))
         return cleanup(rc);
@@ -1065,6 +1072,8 @@ int llm_ctx_create(const llm_shape_t* shape, int device, uint32_t num_pairs,
         c->gqa_min_tiles = (uint32_t)std::strtoul(e, nullptr, 10);
     if (const char* e = std::getenv("LLM_ACCEL_GQA_FUSED"))
         c->gqa_fused = std::strcmp(e, "0") != 0;
+    if (const char* e = std::getenv("LLM_ACCEL_GQA_SCAN_FUSED"))
+        c->gqa_scan_fused = std::strcmp(e, "0") != 0;
     if (hipDeviceGetAttribute(&c->cus, hipDeviceAttributeMultiprocessorCount, c->device) !=
         hipSuccess)
         return cleanup(fail(LLM_E_HIP, "device attribute query failed"));

@@ -491,6 +491,24 @@ def test_gqa_three_launches_running_max_rises(gqa_three_launches):
     test_running_max_rises_often(4096, 3)
 
 
+@pytest.fixture
+def gqa_scan_launch(monkeypatch):
+    """The GQA tile path from 5 tiles with scores and PV in one launch and
+    the scan as a launch of its own (by default the scan's workgroups run
+    in the same launch, reading the tiles' tagged sums)."""
+    monkeypatch.setenv("LLM_ACCEL_GQA_MIN_TILES", "5")
+    monkeypatch.setenv("LLM_ACCEL_GQA_SCAN_FUSED", "0")
+
+
+@pytest.mark.parametrize("cfg,n,rows", [("B", 1020, 8), ("A", 317, 5), ("B", 319, 1)])
+def test_gqa_scan_launch_block_across_tile_boundary(gqa_scan_launch, cfg, n, rows):
+    test_block_across_tile_boundary_late_context(cfg, n, rows)
+
+
+def test_gqa_scan_launch_running_max_rises(gqa_scan_launch):
+    test_running_max_rises_often(16384, 10)
+
+
 def test_norm_cache_invalidation():
     # T18 writes pair 0 and derives its FFN norm; uploading new rows into
     # pair 0 before T19 must discard that copy.  T19 into pair 1 derives the
