@@ -401,6 +401,14 @@ def main():
         acc.download(0, 1)
         io.append(time.perf_counter() - t0)
     dec_io_us = float(np.median(io)) * 1e6
+    # Decode forwards back to back, one event pair around all K (no marker
+    # between forwards, as the request loop runs its 36 layers): mean.
+    acc.record(0)
+    for s in range(K):
+        decode(s % C)
+    acc.record(1)
+    acc.sync()
+    dec_b2b_us = acc.elapsed_ms(0, 1) * 1e3 / K
     # The dominant kernel back to back (same launches as in a decode
     # forward, rotating the layer copies): its mean launch duration.
     gu_us = acc.bench_projection("gateup", 1, C, 4 * K)
@@ -410,7 +418,8 @@ def main():
     copy_gbs = 2 * copy_bytes / copy_ms / 1e6
     acc.close()
     if args.part == "configs1":
-        print(json.dumps({"part": "configs1", "decode_forward_us": dec_us, "p8_block_us": p8_us,
+        print(json.dumps({"part": "configs1", "decode_forward_us": dec_us,
+                          "decode_forward_us_back_to_back": dec_b2b_us, "p8_block_us": p8_us,
                           "kernel_us_decode": {k: round(v[1], 3) for k, v in kdec.items()},
                           "kernel_us_p8": {k: round(v[1], 3) for k, v in kp8.items()},
                           "gateup_launch_us": gu_us}), flush=True)
@@ -467,6 +476,7 @@ def main():
             "decode_tok_s": 1e6 / dec_us,
             "p8_block_us": p8_us,
             "decode_forward_us": dec_us,
+            "decode_forward_us_back_to_back": dec_b2b_us,
             "decode_hbm_frac": lb / (dec_us * 1e-6) / 1e9 / HBM_PEAK_GBS,
             "p8_hbm_frac": lb / (p8_us * 1e-6) / 1e9 / HBM_PEAK_GBS,
             "ms_per_pass": total_ms / K,
