@@ -705,19 +705,42 @@ __device__ __forceinline__ void gqa_scan_body(const AttnArgs& a, GqaScanSmem& sm
             sm.run[j] = (int16_t)k;
         }
         if (lane == 63) sm.nev = (int32_t)c;
+        // run r's operands (lane r), from the events alone: run r covers
+        // tiles [ev[r - 1], ev[r]) (run 0 from tile 0, the last to the
+        // end); run r >= 1 starts at event tile ev[r - 1], whose maximum
+        // replaces that of the event before it (or -128.0), which is also
+        // the running max before the run
+        const uint32_t nw = __builtin_amdgcn_readlane(c, 63);
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        if (nw + 1 <= GSLOTS && lane <= nw) {
+            const uint32_t a0 = lane == 0 ? 0 : (uint32_t)sm.ev[lane - 1];
+            const uint32_t a1 = lane == nw ? ntiles : (uint32_t)sm.ev[lane];
+            const int32_t mprev = lane >= 2 ? sm.tm[sm.ev[lane - 2]] : INT16_MIN;
+            GqaRun ru;
+            ru.old = lane ? (int64_t)prob(sm.e14, mprev - sm.tm[a0]) << 2 : 0;
+            ru.a0 = (int32_t)a0;
+            ru.len = a1 > a0 ? (int32_t)(a1 - a0) : 0;
+            ru.mb = mprev;
+            ru.pad = 0;
+            sm.ri[lane] = ru;
+        }
     }
+    int32_t tsl[TVB];  // FUSED: the sums of this thread's slice of tiles
+    lds_barrier();  // the events
     if (FUSED) {
-        // the tile sums (tagged after the tiles' values were performed),
-        // then this thread's first tile values
+        // the sums of this thread's slice of tiles (tagged after the tiles'
+        // values were performed; the slice has at most TVB tiles), then the
+        // slice's values, while later tiles may still be running
         const TagWait tw{(uint64_t)wall_clock64(), a.wait_limit, a.abort, a.host_abort};
         while (true) {
             bool ok = true;
 #pragma unroll
-            for (int u = 0; u < NU; u++) {
-                const uint32_t j = tid + GNT * u;
-                const uint64_t wd = ld_coherent(&a.s_gsum64[tw0 + (size_t)(j < ntiles ? j : 0) * G]);
-                ok = ok && (j >= ntiles || (uint32_t)(wd >> 32) == a.epoch);
-                tsr[u] = (int32_t)(uint32_t)wd;
+            for (int u = 0; u < TVB; u++) {
+                const uint32_t j = j0 + u;
+                const uint64_t wd = ld_coherent(&a.s_gsum64[tw0 + (size_t)(j < j1 ? j : 0) * G]);
+                ok = ok && (j >= j1 || (uint32_t)(wd >> 32) == a.epoch);
+                tsl[u] = (int32_t)(uint32_t)wd;
             }
             if (__all(ok)) break;
             if (!tw.keep_waiting()) {
@@ -726,22 +749,15 @@ __device__ __forceinline__ void gqa_scan_body(const AttnArgs& a, GqaScanSmem& sm
             }
         }
 #pragma unroll
-        for (int u = 0; u < NU; u++) {
-            const uint32_t j = tid + GNT * u;
-            if (j < ntiles) sm.ts[j] = tsr[u];
-        }
-        // a wavefront has seen the sums of its own tiles only; a thread's
-        // slice of tile values spans other wavefronts' tiles, so every
-        // wavefront's wait ends before any value is read
-        lds_barrier();
-        if (ok_all == 0) return;  // uniform: read after the barrier
-#pragma unroll
         for (int u = 0; u < TVB; u++) {
             const uint32_t j = j0 + u < j1 ? j0 + u : (j0 < j1 ? j0 : 0);
             ld[u] = ld_coherent_v4(a.s_tval + tv_base + (size_t)j * G * D + 8 * oc);
         }
-    } else {
-        lds_barrier();  // the events
+        if (oc == 0) {
+#pragma unroll
+            for (int u = 0; u < TVB; u++)
+                if (j0 + u < j1) sm.ts[j0 + u] = tsl[u];
+        }
     }
     const uint32_t nev = (uint32_t)sm.nev;
     const bool parallel = nev + 1 <= GSLOTS;
@@ -786,24 +802,17 @@ __device__ __forceinline__ void gqa_scan_body(const AttnArgs& a, GqaScanSmem& sm
 #pragma unroll
             for (int q = 0; q < 8; q++) atomicAdd(&sm.rsum[cur][8 * oc + q], part[q]);
         }
-        for (uint32_t j = tid; j < ntiles; j += GNT) atomicAdd(&sm.rts[sm.run[j]], sm.ts[j]);
-        // run r: tiles [ev[r - 1], ev[r]) (run 0 from tile 0, the last to the
-        // end); run r >= 1 starts at event tile ev[r - 1], whose maximum
-        // replaces that of the event before it (or -128.0), which is also
-        // the running max before the run
-        if (tid <= nev) {
-            const uint32_t a0 = tid == 0 ? 0 : (uint32_t)sm.ev[tid - 1];
-            const uint32_t a1 = tid == nev ? ntiles : (uint32_t)sm.ev[tid];
-            const int32_t mprev = tid >= 2 ? sm.tm[sm.ev[tid - 2]] : INT16_MIN;
-            GqaRun ru;
-            ru.old = tid ? (int64_t)prob(sm.e14, mprev - sm.tm[a0]) << 2 : 0;
-            ru.a0 = (int32_t)a0;
-            ru.len = a1 > a0 ? (int32_t)(a1 - a0) : 0;
-            ru.mb = mprev;
-            ru.pad = 0;
-            sm.ri[tid] = ru;
+        if (oc == 0) {  // the slice's tile sums into their runs
+            if (FUSED) {
+#pragma unroll
+                for (int u = 0; u < TVB; u++)
+                    if (j0 + u < j1) atomicAdd(&sm.rts[sm.run[j0 + u]], tsl[u]);
+            } else {
+                for (uint32_t j = j0; j < j1; j++) atomicAdd(&sm.rts[sm.run[j]], sm.ts[j]);
+            }
         }
         lds_barrier();
+        if (FUSED && ok_all == 0) return;  // uniform: read after the barrier
         // ---- the sum of the probabilities, once per workgroup (lane 0 of
         // the second wavefront, beside the elements' chains); the next
         // run's operands are read while a run is computed ----
@@ -827,8 +836,12 @@ __device__ __forceinline__ void gqa_scan_body(const AttnArgs& a, GqaScanSmem& sm
             }
             sm.sum = sum;
         }
-    } else if (tid == 64) {
-        sm.sum = sum_tiles_seq(sm, 0, ntiles, INT16_MIN, 0);
+    } else {
+        if (FUSED) {
+            lds_barrier();  // every slice's sums
+            if (ok_all == 0) return;
+        }
+        if (tid == 64) sm.sum = sum_tiles_seq(sm, 0, ntiles, INT16_MIN, 0);
     }
     // ---- the accumulator, one element per thread: one step per run when
     // no partial sum of the run can reach the int32 bounds (tile values
