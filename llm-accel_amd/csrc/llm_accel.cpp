@@ -1074,6 +1074,10 @@ int llm_ctx_create(const llm_shape_t* shape, int device, uint32_t num_pairs,
         c->gqa_fused = std::strcmp(e, "0") != 0;
     if (const char* e = std::getenv("LLM_ACCEL_GQA_SCAN_FUSED"))
         c->gqa_scan_fused = std::strcmp(e, "0") != 0;
+    // the GQA path's epoch before the first launch (tests start it just
+    // below kGqaEpochMax so that it wraps within a few launches)
+    if (const char* e = std::getenv("LLM_ACCEL_GQA_EPOCH_START"))
+        c->gqa_epoch = std::min<uint32_t>((uint32_t)std::strtoul(e, nullptr, 0), llm::kGqaEpochMax);
     if (hipDeviceGetAttribute(&c->cus, hipDeviceAttributeMultiprocessorCount, c->device) !=
         hipSuccess)
         return cleanup(fail(LLM_E_HIP, "device attribute query failed"));

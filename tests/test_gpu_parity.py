@@ -491,6 +491,45 @@ def test_gqa_three_launches_running_max_rises(gqa_three_launches):
     test_running_max_rises_often(4096, 3)
 
 
+@pytest.mark.parametrize("scan_fused", ["1", "0"])
+def test_gqa_epoch_wraps(monkeypatch, scan_fused):
+    """The GQA path's launch epoch started just below its maximum: six
+    decode rows in a row (5-6 tiles, the GQA path forced from 5 tiles), the
+    fourth launch past the maximum clears the tagged maxima and sums and
+    starts again at 1; every row and K/V append against the oracle."""
+    import llm_accel
+    monkeypatch.setenv("LLM_ACCEL_GQA_MIN_TILES", "5")
+    monkeypatch.setenv("LLM_ACCEL_GQA_EPOCH_START", "65532")
+    monkeypatch.setenv("LLM_ACCEL_GQA_SCAN_FUSED", scan_fused)
+    spec = workloads.CONFIG_B
+    synth = workloads.SyntheticModel(spec, layers=1)
+    n0 = 317
+    om = oracle_from_synthetic(synth, oracle_shape(spec, layers=1, max_seq=n0 + 16))
+    kc, vc = om.new_kv()
+    xs = synth.hidden_rows(6, seed_offset=77)
+    with llm_accel.Accelerator(accel_shape(spec, layers=1, max_seq=n0 + 16)) as a:
+        a.load_model(synth)
+        for h in range(spec.kv_heads):
+            k, v = synth.kv_rows(n0, seed_offset=30 + h)
+            kc[0, h, :n0], vc[0, h, :n0] = k, v
+            a.kv_write(0, h, 0, k, v)
+        for i in range(6):
+            pos = n0 + i
+            _say(f"case epoch wrap scan_fused={scan_fused} pos={pos}")
+            a.upload(2, xs[i:i + 1])
+            rc, _ = a.task(18, 0, 1, pos, 2, 0)
+            assert rc == 0
+            got = a.download(0, 1)
+            code, want, _ = om.task((kc, vc), 18, 0, xs[i:i + 1], pos)
+            assert code == 0
+            err = first_mismatch(got, want)
+            assert err is None, f"pos {pos}: {err}"
+        for h in range(spec.kv_heads):
+            k, v = a.kv_read(0, h, n0, 6)
+            assert first_mismatch(k, kc[0, h, n0:n0 + 6]) is None
+            assert first_mismatch(v, vc[0, h, n0:n0 + 6]) is None
+
+
 @pytest.fixture
 def gqa_scan_launch(monkeypatch):
     """The GQA tile path from 5 tiles with scores and PV in one launch and
