@@ -2064,8 +2064,12 @@ int run_stack(llm_ctx_t* c, const int16_t* rows_host, uint32_t rows, uint32_t po
     }
     const auto host0 = std::chrono::steady_clock::now();
     invalidate_pair(c, 1);
-    HIP_TRY(hipMemcpy2DAsync(c->pairs[1], (size_t)c->Hp * 2, rows_host, (size_t)c->H * 2,
-                             (size_t)c->H * 2, rows, hipMemcpyHostToDevice, c->stream));
+    if (rows == 1)  // a decode row: one contiguous copy (cheaper than a 2-D one)
+        HIP_TRY(hipMemcpyAsync(c->pairs[1], rows_host, (size_t)c->H * 2, hipMemcpyHostToDevice,
+                               c->stream));
+    else
+        HIP_TRY(hipMemcpy2DAsync(c->pairs[1], (size_t)c->Hp * 2, rows_host, (size_t)c->H * 2,
+                                 (size_t)c->H * 2, rows, hipMemcpyHostToDevice, c->stream));
     c->n_h2d_rows++;
     if (prof) HIP_TRY(hipEventRecord(c->gen_events[1], c->stream));
     llm_status_t st;
