@@ -605,6 +605,8 @@ __device__ __forceinline__ void gqa_scan_body(const AttnArgs& a, GqaScanSmem& sm
     constexpr uint32_t C8 = GSE / 8, NSL = GNT / C8;  // element octets, tile slices
     constexpr int TVB = 8;                          // tile-value loads in flight per thread
     constexpr int NU = FUSED ? 2 : (int)(GMAXT / GNT);  // tiles per thread (maxima, sums)
+    static_assert((kGqaFusedMaxTiles + NSL - 1) / NSL <= (uint32_t)TVB,
+                  "FUSED: a thread's slice of tiles fits one batch of value loads");
     const uint32_t es = bid % ES, tg = bid / ES;
     const uint32_t t = tg / a.num_heads, g = tg % a.num_heads;
     if (t >= a.grid_rows) return;
