@@ -428,6 +428,16 @@ def test_tile_path_one_launch(cfg, n, rows):
     test_block_across_tile_boundary_late_context(cfg, n, rows)
 
 
+@pytest.mark.parametrize("cfg,n,rows", [("B", 16447, 1), ("B", 16448, 1), ("B", 16446, 2),
+                                         ("A", 16447, 1)])
+def test_gqa_one_launch_tile_limit(cfg, n, rows):
+    """The GQA path at the one-launch limit: 257 tiles with one row (scores,
+    PV and scan in one launch), 258 tiles (three launches), 257 tiles with
+    two rows (a grid past what the device holds at once: separate
+    launches); both head_dims."""
+    test_block_across_tile_boundary_late_context(cfg, n, rows)
+
+
 @pytest.fixture
 def tile_two_launches(monkeypatch):
     """The tile path as two launches (scores, then PV and recurrence)."""
