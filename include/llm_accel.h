@@ -276,8 +276,7 @@ enum {
     LLM_K_GATEUP = 5,    /* gate | up projection + SiLU * up           */
     LLM_K_DOWN = 6,      /* down projection + residual                 */
     LLM_K_ATTN_SUBLAYER = 7, /* QKV + attention + O in one launch (decode) */
-    LLM_K_DECODE_STACK = 8,  /* a run of decode sublayers in one launch   */
-    LLM_K_COUNT = 9
+    LLM_K_COUNT = 8
 };
 int llm_kernel_timing(llm_ctx_t* ctx, int enable);
 int llm_kernel_stats(llm_ctx_t* ctx, uint32_t kernel, uint64_t* launches,
@@ -338,7 +337,9 @@ typedef struct {
     uint32_t coarse_task_count;       /* ceil(P/B)*2L + 1 + (G-1)*(2L+1) */
     uint32_t output_materializations;
     uint32_t released_prompt_blocks;
-    uint32_t reserved0;
+    uint32_t wait_reruns;             /* runs re-done on launches without
+                                         waits between workgroups after a
+                                         bounded wait gave up (0 normally) */
     double prompt_forward_ms;         /* all prompt blocks */
     double time_to_first_token_ms;    /* host clock, call to first token */
     double generated_forward_ms;      /* sum over the sampled tokens' forwards */
@@ -376,15 +377,24 @@ int llm_set_log(llm_ctx_t* ctx, llm_log_fn fn, void* user);
  * tokens, each the LM-head argmax of the last row, with a one-row forward
  * (Tasks 18/19 per layer and 20) for every sampled token but the last.
  * Embedding rows are gathered on the host from `embedding` [vocab][hidden]
- * and uploaded, as in the reference.  Requires llm_load_lm_head first. */
+ * and uploaded, as in the reference.  Requires llm_load_lm_head first.
+ * A one-launch kernel whose bounded wait between workgroups gives up
+ * (e.g. a device shared with other work) does not fail the request: the
+ * forwards since the previous synchronisation run again on launches
+ * without such waits (counted in stats->wait_reruns), as the reference's
+ * controller completes every command it accepts
+ * (kernel/control_cache_8x64.cpp:5892-5957).  llm_task reports the same
+ * event as LLM_E_HIP at its caller's next synchronisation. */
 int llm_generate(llm_ctx_t* ctx, const int16_t* embedding, uint32_t vocab,
                  const uint32_t* prompt, uint32_t n_prompt, uint32_t block_size,
                  uint32_t layer_count, uint32_t max_new_tokens,
                  uint32_t* out_tokens, llm_generate_stats_t* stats);
 
 /* The two exp tables the kernels use, 2049 entries for x = -8 .. 0 in
- * Q8.8 steps: q8_8 = floor(e^x * 256) (SiLU), q2_14 = floor(e^x * 16384)
- * (attention probabilities). */
+ * Q8.8 steps: q8_8 = the reference's hls::exp on ap_fixed<16,8> (SiLU and
+ * the Q8.8 softmax / flash operators; golden_exp, host/host_qwen_8x64.cpp
+ * :578-586), q2_14 = floor(e^x * 16384) (attention probabilities,
+ * hls::exp on ap_fixed<18,4>, host:588-596). */
 int llm_exp_tables(int16_t* q8_8, int16_t* q2_14);
 
 #ifdef __cplusplus

@@ -1523,18 +1523,20 @@ __global__ __launch_bounds__(D * 2) void attention_tile_fused_kernel(AttnArgs a)
     tile_pv_phase<D, true>(a, wg, sm.p, lsc, &lmt);
 }
 
-// Workgroups of the one-launch tile path the device holds at once.
+// Workgroups of the one-launch tile path the device holds at once.  The
+// per-CU occupancy is a property of the kernel's gfx950 code object (the
+// only target this library builds), the same on every device; it is
+// queried once, under C++'s thread-safe initialisation of a local static.
 template <int D>
 uint32_t tile_fused_capacity(uint32_t cus) {
-    static int per_cu = -1;
-    if (per_cu < 0) {
+    static const int per_cu = [] {
         int nb = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
                 &nb, reinterpret_cast<const void*>(&attention_tile_fused_kernel<D>), 2 * D, 0) !=
             hipSuccess)
             nb = 0;
-        per_cu = nb;
-    }
+        return nb;
+    }();
     return (uint32_t)per_cu * cus;
 }
 template <int D>

@@ -933,19 +933,19 @@ __global__ __launch_bounds__(GNT) void attention_gqa_fused_kernel(AttnArgs a) {
     gqa_pv_body<D, true, SCAN>(a, wg, sm.p, LP, sc, mt, ok_all);
 }
 
-// Workgroups of the one-launch GQA kernel the device holds at once.
+// Workgroups of the one-launch GQA kernel the device holds at once (the
+// per-CU occupancy of the gfx950 code object, queried once under C++'s
+// thread-safe initialisation of a local static).
 template <int D, bool SCAN>
 uint32_t gqa_fused_capacity(uint32_t cus) {
-    static int per_cu = -1;
-    if (per_cu < 0) {
+    static const int per_cu = [] {
         int nb = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
                 &nb, reinterpret_cast<const void*>(&attention_gqa_fused_kernel<D, SCAN>), GNT,
-                0) !=
-            hipSuccess)
+                0) != hipSuccess)
             nb = 0;
-        per_cu = nb;
-    }
+        return nb;
+    }();
     return (uint32_t)per_cu * cus;
 }
 

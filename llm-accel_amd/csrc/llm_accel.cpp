@@ -18,12 +18,12 @@
 #include <cstring>
 #include <string>
 #include <chrono>
+#include <functional>
 #include <thread>
 #include <vector>
 
 #include "attention.h"
 #include "coherent.h"
-#include "decode_stack.h"
 #include "fixed_point.h"
 #include "kernels.h"
 #include "ops.h"
@@ -206,24 +206,6 @@ struct llm_ctx {
     double kernel_ms[LLM_K_COUNT] = {};
     uint64_t kernel_n[LLM_K_COUNT] = {};
 
-    // Persistent decode launches (decode_stack.hip): decode tasks (1-2
-    // rows, Task 18 / 19 / 16) are collected and run as one launch when
-    // the caller next needs a result or issues anything else.
-    uint32_t ds_nwg[2] = {0, 0};      // workgroups for 1 / 2 rows; 0: unavailable
-    uint32_t* ds_sync = nullptr;      // arrival counters (kStackSyncWords)
-    uint32_t ds_occ[llm::kStackGroups] = {};  // group occurrences so far, mod 2^32
-    uint32_t ds_start = 0;            // counter value at creation
-    bool ds_enabled = false;          // LLM_ACCEL_STACK=1 enables
-    size_t ds_layer_stride = 0;       // elements between layers' matrices
-    struct DsStep {
-        uint32_t layer;
-        int in, out;
-        uint32_t ffn;
-    };
-    std::vector<DsStep> ds_pending;
-    uint32_t ds_rows = 0, ds_pos = 0;
-    int ds_lw = 4;                    // widening of the pending run (4 or 1)
-
     // LM head [vocab][hidden] (tile4x128) and the argmax keys of 8 rows
     Matrix lm;
     uint32_t lm_vocab = 0;
@@ -243,6 +225,10 @@ struct llm_ctx {
     uint64_t n_d2h_rows = 0;   // hidden-row downloads (calls)
     uint64_t n_kv_moves = 0;   // KV reads / writes (calls)
     uint64_t n_argmax = 0;     // argmax key read-backs (calls)
+    uint64_t n_wait_reruns = 0;  // forwards re-run without waits (llm_generate)
+    // Stream-event times of the profiled forwards (a line sink set), summed
+    // over the context's life: the reference's coarse_* report fields.
+    double coarse_active_ms = 0, coarse_input_ms = 0, coarse_host_ms = 0;
 
     Matrix& mat(uint32_t layer, int m) { return mats[layer * M_COUNT + m]; }
 };
@@ -293,25 +279,50 @@ void harvest_timing(llm_ctx* c) {
 
 // After a synchronisation: a fused launch whose wait gave up (bounded
 // waits end the kernel instead of hanging) left its counters behind and
-// invalid results; clear both and report it.
-int check_waits(llm_ctx* c) {
-    if (!c->host_abort || __atomic_load_n(c->host_abort, __ATOMIC_ACQUIRE) == 0) return 0;
+// invalid results; clear both.  Returns whether there was one.
+bool clear_waits(llm_ctx* c) {
+    if (!c->host_abort || __atomic_load_n(c->host_abort, __ATOMIC_ACQUIRE) == 0) return false;
     (void)hipMemsetAsync(c->sync, 0, llm::kSyncWords * 4, c->stream);
     // counters a workgroup that left a wait early did not reset
     (void)hipMemsetAsync(c->counters, 0, c->counter_bytes, c->stream);
     // and flags of the one-launch tile path a workgroup did not clear
     (void)hipMemsetAsync(c->s_tmax32, 0, c->rht_words * 4, c->stream);
     (void)hipMemsetAsync(c->s_tsum, 0, c->rht_words * 4, c->stream);
-    if (c->ds_sync) (void)hipMemsetAsync(c->ds_sync, 0, llm::kStackSyncWords * 4, c->stream);
     (void)hipStreamSynchronize(c->stream);
     std::fill(std::begin(c->sync_qkv), std::end(c->sync_qkv), 0u);
     c->sync_attn = 0;
-    std::fill(std::begin(c->ds_occ), std::end(c->ds_occ), 0u);
-    c->ds_start = 0;
     __atomic_store_n(c->host_abort, 0u, __ATOMIC_RELEASE);
+    return true;
+}
+
+// The same, reported as an error of the call that synchronised.
+int check_waits(llm_ctx* c) {
+    if (!clear_waits(c)) return 0;
     return fail(LLM_E_HIP, "a wait between workgroups of a fused launch timed out; "
                            "results since the last synchronisation are invalid");
 }
+
+// While in scope, the context enqueues only launches whose workgroups never
+// wait for one another (separate QKV / attention / O launches, the
+// two-launch tile and GQA paths): the request loop re-runs with it what a
+// bounded wait that gave up invalidated.  The reference's controller either
+// completes a command or returns a status code
+// (kernel/control_cache_8x64.cpp:5892-5957); a device shared with other
+// work can leave a one-launch kernel's workgroups without a slot, which is
+// the case this covers.
+struct WaitFreeScope {
+    llm_ctx* c;
+    bool fused, tile_fused, gqa_fused;
+    explicit WaitFreeScope(llm_ctx* ctx)
+        : c(ctx), fused(ctx->fused), tile_fused(ctx->tile_fused), gqa_fused(ctx->gqa_fused) {
+        c->fused = c->tile_fused = c->gqa_fused = false;
+    }
+    ~WaitFreeScope() {
+        c->fused = fused;
+        c->tile_fused = tile_fused;
+        c->gqa_fused = gqa_fused;
+    }
+};
 
 int dev_alloc(llm_ctx* c, void** p, size_t bytes) {
     hipError_t e = hipMalloc(p, bytes);
@@ -324,11 +335,44 @@ int dev_alloc(llm_ctx* c, void** p, size_t bytes) {
     return 0;
 }
 
-// exp tables: floor(e^x * 2^F) for x = -2048/256 .. 0.
+// Nearest integer to v * 2^bits, v >= 0 (an AP_RND table constant).
+int64_t table_const(long double v, int bits) {
+    return (int64_t)floorl(ldexpl(v, bits) + 0.5L);
+}
+
+// hls::exp on ap_fixed<16,8>: the Q8.8 exponential of SiLU and of the
+// Q8.8 softmax / flash operators (golden_exp, host/host_qwen_8x64.cpp:
+// 578-586; cu_exp_approx, kernel/compute_stream.cpp:50-55).  The
+// reference's HLS build instantiates it as three ROM lookups and two
+// products (ROMs exp_x_msb_1_table, exp_x_msb_2_m_1_table, f_x_lsb_table;
+// a 5-bit msb_2 field of weights 2^-2..2^-6; 25x18- and 25x25-bit
+// multipliers -- results/qwen3b-e2e-20260820/build.raw.log:1469-1471,
+// :1506-1516).  For x split into m1 (bits >= 2^-1, two's complement),
+// m2 (bits 2^-2..2^-6) and l (bits 2^-7, 2^-8):
+//   e^x ~= E1 (1 + E2)(1 + L),  E1 = e^m1 rounded at 2^-14,
+//   E2 = e^m2 - 1 rounded at 2^-26, L = l + (e^l - 1 - l) rounded at 2^-24,
+// truncated to Q8.8.  These widths reproduce the reference's published
+// post-FFN fingerprint and final-hidden checksums; the result differs
+// from floor(e^x * 256) at 13 inputs in [-8, 0].
+int16_t hls_exp_q8_8(int x) {
+    const int m1 = x & ~127, m2 = (x - m1) & ~3, l = (x - m1) & 3;
+    const __int128 e1 = table_const(expl((long double)m1 / 256.0L), 14);
+    const __int128 e2 = table_const(expm1l((long double)m2 / 256.0L), 26);
+    const long double lf = (long double)l / 256.0L;
+    const __int128 lt = ((__int128)l << 16) + table_const(expm1l(lf) - lf, 24);
+    // (1 + E2)(1 + L) in units of 2^-50, then E1 * that in units of 2^-64.
+    const __int128 f = ((__int128)1 << 50) + (e2 << 24) + (lt << 26) + e2 * lt;
+    const __int128 y = (e1 * f) >> 56;
+    return y > 32767 ? (int16_t)32767 : (int16_t)y;
+}
+
+// exp tables for x = -2048/256 .. 0: the Q8.8 one above, and the Q2.14
+// probabilities floor(e^x * 2^14) (hls::exp on ap_fixed<18,4>,
+// host/host_qwen_8x64.cpp:588-596).
 void build_exp_tables(int16_t* q8_8, int16_t* q2_14) {
     for (int x = -2048; x <= 0; x++) {
+        q8_8[x + 2048] = hls_exp_q8_8(x);
         long double e = expl((long double)x / 256.0L);
-        q8_8[x + 2048] = (int16_t)floorl(e * 256.0L);
         q2_14[x + 2048] = (int16_t)floorl(e * 16384.0L);
     }
 }
@@ -763,147 +807,7 @@ int enqueue_ffn_sublayer(llm_ctx* c, uint32_t layer, uint32_t R, int in_pair,
     return 0;
 }
 
-// Whether decode task (op, R rows at pos, layer) can join a persistent
-// launch; *lw receives the widening it needs (4 or 1).
-bool ds_eligible(const llm_ctx* c, uint32_t R, uint32_t pos, uint32_t layer, int* lw) {
-    if (!c->ds_enabled || R == 0 || R > 2 || c->ds_nwg[R - 1] == 0) return false;
-    if (c->d != llm::kStackHeadDim || c->const_gain <= 0) return false;
-    if (c->Hp / llm::kStepCols > llm::kStackMaxStepsH ||
-        c->Ip / llm::kStepCols > llm::kStackMaxStepsI)
-        return false;
-    const uint32_t nwg = c->ds_nwg[R - 1];
-    const uint32_t nbq = (c->Nqkv + 3) / 4, nbo = (c->H + 3) / 4;
-    if (R * c->Hq > nwg || 2 * nwg < nbq || 2 * nwg < nbo) return false;
-    // the attention of the persistent launch is the split-head path
-    if (pos + R > 4 * llm::kTile) return false;
-    int L = 16;
-    for (int m = 0; m < M_COUNT; m++)
-        L = std::min(L, const_cast<llm_ctx*>(c)->mat(layer, m).L);
-    if (L < 1) return false;
-    *lw = L >= 4 ? 4 : 1;
-    return true;
-}
-
-// Runs the collected decode tasks as one persistent launch.
-int ds_flush(llm_ctx* c) {
-    if (c->ds_pending.empty()) return 0;
-    const uint32_t R = c->ds_rows;
-    llm::StackArgs a{};
-    a.nsteps = (uint32_t)c->ds_pending.size();
-    for (uint32_t k = 0; k < a.nsteps; k++) {
-        const auto& p = c->ds_pending[k];
-        a.steps[k] = {c->pairs[p.in], c->pairs[p.out], p.layer, p.ffn};
-    }
-    a.rows = R;
-    a.pos0 = c->ds_pos;
-    a.H = c->H;
-    a.I = c->I;
-    a.Hp = c->Hp;
-    a.Ip = c->Ip;
-    a.Nqkv = c->Nqkv;
-    for (int m = 0; m < M_COUNT; m++) a.w[m] = c->mat(0, m).d;
-    a.layer_stride = c->ds_layer_stride;
-    a.norms = c->norms;
-    a.gain = c->const_gain;
-    a.L = c->L;
-    a.exp8 = c->exp8;
-    llm::AttnArgs& at = a.at;
-    at.qkv = c->qkv;
-    at.ldqkv = c->Nqkv;
-    at.rope = c->rope;
-    at.kcache = c->kcache;
-    at.vcache = c->vcache;
-    at.tiles = c->tiles;
-    at.pos0 = c->ds_pos;
-    at.num_heads = c->Hq;
-    at.num_kv_heads = c->Hkv;
-    at.group = c->G;
-    at.head_dim = c->d;
-    at.qk_scale = c->qk_scale;
-    at.exp14 = c->exp14;
-    at.out = c->attn;
-    at.ldo = c->Hp;
-    a.kv_layer_stride = (size_t)c->Hkv * c->tiles * llm::kTile * c->d;
-    a.qkv = c->qkv;
-    a.attn = c->attn;
-    a.act = c->act;
-    const auto& last = c->ds_pending.back();
-    a.final_out = last.ffn ? c->xn_final : nullptr;
-    a.sync = c->ds_sync;
-    std::copy(std::begin(c->ds_occ), std::end(c->ds_occ), a.occ);
-    a.start = c->ds_start;
-    a.abort = c->sync + llm::kSyncAbort;
-    a.host_abort = c->host_abort;
-    a.wait_limit = c->wait_limit;
-    {
-        TimedScope ts(c, LLM_K_DECODE_STACK);
-        HIP_TRY(llm::launch_decode_stack(a, c->ds_nwg[R - 1], c->ds_lw, c->stream));
-    }
-    for (const auto& p : c->ds_pending) {
-        if (p.ffn) {
-            c->ds_occ[3]++;
-            c->ds_occ[4]++;
-        } else {
-            c->ds_occ[0]++;
-            c->ds_occ[1]++;
-            c->ds_occ[2]++;
-        }
-    }
-    // the launch writes no normalised side copies but the final norm of
-    // its last FFN sublayer (rows R..7 copied from that sublayer's input)
-    c->attn_cache.pair = c->ffn_cache.pair = -1;
-    c->final_cache.pair = c->final_cache.src = -1;
-    if (last.ffn) c->final_cache = {last.out, last.in, R};
-    c->ds_pending.clear();
-    return 0;
-}
-
-// Collects decode task op (16, 18 or 19) when it can join a persistent
-// launch; returns 1 when it was taken, 0 when the caller runs it itself
-// (after the collected ones), < 0 on error.
-int ds_collect(llm_ctx* c, uint32_t op, uint32_t layer, uint32_t R, uint32_t pos, int in,
-               int out) {
-    int lw = 4;
-    const uint32_t n = op == LLM_OP_DECODER_LAYER ? 2 : 1;
-    if (!ds_eligible(c, R, pos, layer, &lw)) {
-        const int rc = ds_flush(c);
-        return rc < 0 ? rc : 0;
-    }
-    if (!c->ds_pending.empty() &&
-        (R != c->ds_rows || pos != c->ds_pos ||
-         c->ds_pending.size() + n > llm::kStackMaxSteps)) {
-        const int rc = ds_flush(c);
-        if (rc < 0) return rc;
-    }
-    if (c->ds_pending.empty()) {
-        c->ds_rows = R;
-        c->ds_pos = pos;
-        c->ds_lw = 4;
-    }
-    c->ds_lw = std::min(c->ds_lw, lw);
-    if (op == LLM_OP_ATTENTION_SUBLAYER) {
-        c->ds_pending.push_back({layer, in, out, 0});
-    } else if (op == LLM_OP_FFN_SUBLAYER) {
-        c->ds_pending.push_back({layer, in, out, 1});
-    } else {
-        c->ds_pending.push_back({layer, in, out, 0});
-        c->ds_pending.push_back({layer, out, out, 1});
-    }
-    return 1;
-}
-
 }  // namespace
-
-namespace llm {
-// Every entry point that observes or changes device state runs the
-// collected decode tasks first.
-int flush_pending(llm_ctx* c) { return ds_flush(c); }
-}  // namespace llm
-
-#define FLUSH_TRY(c)                                         \
-    do {                                                     \
-        if (int rc_ = ds_flush(c)) return rc_;               \
-    } while (0)
 
 extern "C" {
 
@@ -1127,31 +1031,6 @@ int llm_ctx_create(const llm_shape_t* shape, int device, uint32_t num_pairs,
     }
     if (fx_recip(fx_sat16((int64_t)c->H * 256)) == 0)
         c->const_gain = fx_rmsnorm_gain(0, c->H);
-    {
-        // persistent decode launches: counters, residency, layer stride
-        if ((rc = dev_alloc(c, (void**)&c->ds_sync, (size_t)llm::kStackSyncWords * 4)))
-            return cleanup(rc);
-        if (const char* e = std::getenv("LLM_ACCEL_STACK")) c->ds_enabled = std::strcmp(e, "1") == 0;
-        if (const char* e = std::getenv("LLM_ACCEL_SYNC_START")) {
-            const uint32_t v = (uint32_t)std::strtoul(e, nullptr, 0);
-            std::vector<uint32_t> init(llm::kStackSyncWords, 0);
-            for (uint32_t l = 0; l < llm::kStackGroups * llm::kStackLines; l++)
-                init[l * llm::kStackStride] = v;
-            if (hipMemcpy(c->ds_sync, init.data(), init.size() * 4, hipMemcpyHostToDevice) !=
-                hipSuccess)
-                return cleanup(fail(LLM_E_HIP, "counter initialisation failed"));
-            c->ds_start = v;
-        }
-        if (d == llm::kStackHeadDim) {
-            c->ds_nwg[0] = llm::stack_workgroups(c->cus, 1);
-            c->ds_nwg[1] = llm::stack_workgroups(c->cus, 2);
-        }
-        c->ds_layer_stride = c->L > 1 ? (size_t)(c->mat(1, 0).d - c->mat(0, 0).d) : 0;
-        for (uint32_t l = 0; l < c->L; l++)
-            for (int m = 0; m < M_COUNT; m++)
-                if (c->mat(l, m).d != c->mat(0, m).d + l * c->ds_layer_stride)
-                    c->ds_enabled = false;
-    }
     *out = c;
     return 0;
 }
@@ -1159,7 +1038,6 @@ int llm_ctx_create(const llm_shape_t* shape, int device, uint32_t num_pairs,
 void llm_ctx_destroy(llm_ctx_t* c) {
     if (!c) return;
     (void)hipSetDevice(c->device);
-    (void)ds_flush(c);
     if (c->stream) (void)hipStreamSynchronize(c->stream);
     for (auto e : c->events) (void)hipEventDestroy(e);
     for (auto e : c->ev_pool) (void)hipEventDestroy(e);
@@ -1181,7 +1059,6 @@ int llm_load_projection(llm_ctx_t* c, uint32_t layer, uint32_t proj,
     if (!c || !w || layer >= c->L || proj > LLM_PROJ_DOWN)
         return fail(LLM_E_ARG, "bad projection load arguments");
     HIP_TRY(hipSetDevice(c->device));
-    FLUSH_TRY(c);
     int rc;
     switch (proj) {
     case LLM_PROJ_Q:
@@ -1323,7 +1200,6 @@ int llm_load_checkpoint_dir(llm_ctx_t* c, const char* dir, uint32_t flags,
     if (!tie && !have_lm && (flags & LLM_CKPT_REQUIRE_LM_HEAD))
         return fail(LLM_E_ARG, "generate mode requires lm_head.fix16.bin or tied embeddings");
     HIP_TRY(hipSetDevice(c->device));
-    FLUSH_TRY(c);
     {
         std::vector<int16_t> norms(norm_vals);
         if ((rc = load_exact(norm_path, norms.data(), norm_vals * 2, "norm weights")) ||
@@ -1361,7 +1237,6 @@ int llm_load_checkpoint_dir(llm_ctx_t* c, const char* dir, uint32_t flags,
 int llm_load_norms(llm_ctx_t* c, const int16_t* norms) {
     if (!c || !norms) return fail(LLM_E_ARG, "null argument");
     HIP_TRY(hipSetDevice(c->device));
-    FLUSH_TRY(c);
     HIP_TRY(hipMemcpy(c->norms, norms, (size_t)(2 * c->L + 1) * c->H * 2,
                       hipMemcpyHostToDevice));
     c->norms_loaded = true;
@@ -1373,7 +1248,6 @@ int llm_hidden_upload(llm_ctx_t* c, uint32_t pair, const int16_t* rows,
     if (!c || !rows || pair >= c->pairs.size() || n > 8)
         return fail(LLM_E_ARG, "bad hidden upload arguments");
     HIP_TRY(hipSetDevice(c->device));
-    FLUSH_TRY(c);
     invalidate_pair(c, (int)pair);
     HIP_TRY(hipMemcpy2DAsync(c->pairs[pair], (size_t)c->Hp * 2, rows,
                              (size_t)c->H * 2, (size_t)c->H * 2, n,
@@ -1388,7 +1262,6 @@ int llm_hidden_download(llm_ctx_t* c, uint32_t pair, int16_t* rows,
     if (!c || !rows || pair >= c->pairs.size() || n > 8)
         return fail(LLM_E_ARG, "bad hidden download arguments");
     HIP_TRY(hipSetDevice(c->device));
-    FLUSH_TRY(c);
     HIP_TRY(hipMemcpy2DAsync(rows, (size_t)c->H * 2, c->pairs[pair],
                              (size_t)c->Hp * 2, (size_t)c->H * 2, n,
                              hipMemcpyDeviceToHost, c->stream));
@@ -1454,7 +1327,6 @@ int llm_task(llm_ctx_t* c, uint32_t op, uint32_t layer, uint32_t token_count,
     if (hipSetDevice(c->device) != hipSuccess)
         return fail(LLM_E_HIP, "hipSetDevice failed");
     if (op == LLM_OP_FINAL_NORM) {
-        FLUSH_TRY(c);
         const int16_t* in = c->pairs[in_pair];
         int16_t* out = c->pairs[out_pair];
         if (token_count == 0) return reject(LLM_STATUS_BAD_TOKEN_COUNT);
@@ -1483,12 +1355,6 @@ int llm_task(llm_ctx_t* c, uint32_t op, uint32_t layer, uint32_t token_count,
         int rc = check_layer_loaded(c, layer, op != LLM_OP_FFN_SUBLAYER,
                                     op != LLM_OP_ATTENTION_SUBLAYER);
         if (rc) return rc;
-        rc = ds_collect(c, op, layer, token_count, position, ip, opr);
-        if (rc < 0) return rc;
-        if (rc == 1) {
-            fill_counters(c, op, token_count, position, st);
-            return LLM_STATUS_OK;
-        }
         if (op == LLM_OP_ATTENTION_SUBLAYER) {
             rc = enqueue_attention_sublayer(c, layer, token_count, position, ip, opr);
         } else if (op == LLM_OP_FFN_SUBLAYER) {
@@ -1628,7 +1494,6 @@ int llm_port_write(llm_ctx_t* c, uint32_t port, const int16_t* host, size_t elem
     HIP_TRY(hipSetDevice(c->device));
     if (int rc = ensure_ports(c)) return rc;
     if (elems > c->port_n) return fail(LLM_E_ARG, "port write exceeds the port");
-    FLUSH_TRY(c);
     if (elems)
         HIP_TRY(hipMemcpyAsync(c->ports[port], host, elems * 2, hipMemcpyHostToDevice,
                                c->stream));
@@ -1641,7 +1506,6 @@ int llm_port_read(llm_ctx_t* c, uint32_t port, int16_t* host, size_t elems) {
     HIP_TRY(hipSetDevice(c->device));
     if (int rc = ensure_ports(c)) return rc;
     if (elems > c->port_n) return fail(LLM_E_ARG, "port read exceeds the port");
-    FLUSH_TRY(c);
     if (elems)
         HIP_TRY(hipMemcpyAsync(host, c->ports[port], elems * 2, hipMemcpyDeviceToHost,
                                c->stream));
@@ -1698,7 +1562,6 @@ int llm_op(llm_ctx_t* c, uint32_t op, uint32_t layer, uint32_t token_count,
     }
     HIP_TRY(hipSetDevice(c->device));
     if (int rc = ensure_ports(c)) return rc;
-    FLUSH_TRY(c);
     if (!in) in = c->ports[LLM_PORT_IN];
     if (!aux) aux = c->ports[LLM_PORT_AUX];
     if (!out) out = c->ports[LLM_PORT_OUT];
@@ -1804,7 +1667,6 @@ int llm_kv_read(llm_ctx_t* c, uint32_t layer, uint32_t h, uint32_t pos0,
     if (!c || layer >= c->L || h >= c->Hkv || pos0 + n > c->max_seq)
         return fail(LLM_E_ARG, "bad KV read arguments");
     HIP_TRY(hipSetDevice(c->device));
-    FLUSH_TRY(c);
     SYNC_TRY(c);
     c->n_kv_moves++;
     return kv_transfer(c, layer, h, pos0, n, k, v, false);
@@ -1815,7 +1677,6 @@ int llm_kv_write(llm_ctx_t* c, uint32_t layer, uint32_t h, uint32_t pos0,
     if (!c || layer >= c->L || h >= c->Hkv || pos0 + n > c->max_seq)
         return fail(LLM_E_ARG, "bad KV write arguments");
     HIP_TRY(hipSetDevice(c->device));
-    FLUSH_TRY(c);
     SYNC_TRY(c);
     c->n_kv_moves++;
     return kv_transfer(c, layer, h, pos0, n, const_cast<int16_t*>(k),
@@ -1825,7 +1686,6 @@ int llm_kv_write(llm_ctx_t* c, uint32_t layer, uint32_t h, uint32_t pos0,
 int llm_kv_clear(llm_ctx_t* c) {
     if (!c) return fail(LLM_E_ARG, "null context");
     HIP_TRY(hipSetDevice(c->device));
-    FLUSH_TRY(c);
     const size_t bytes = (size_t)c->L * c->Hkv * c->tiles * 64 * c->d * 2;
     HIP_TRY(hipMemsetAsync(c->kcache, 0, bytes, c->stream));
     HIP_TRY(hipMemsetAsync(c->vcache, 0, bytes, c->stream));
@@ -1835,7 +1695,7 @@ int llm_kv_clear(llm_ctx_t* c) {
 
 void* llm_pair_device_ptr(llm_ctx_t* c, uint32_t pair) {
     if (!c || pair >= c->pairs.size()) return nullptr;
-    if (hipSetDevice(c->device) != hipSuccess || ds_flush(c)) return nullptr;
+    if (hipSetDevice(c->device) != hipSuccess) return nullptr;
     invalidate_pair(c, (int)pair);  // the caller may write through it
     c->exported[pair] = 1;          // and keeps using this address
     return c->pairs[pair];
@@ -1844,14 +1704,13 @@ void* llm_pair_device_ptr(llm_ctx_t* c, uint32_t pair) {
 void* llm_stream(llm_ctx_t* c) {
     if (!c) return nullptr;
     // work collected for a persistent launch goes onto the stream first
-    if (hipSetDevice(c->device) != hipSuccess || ds_flush(c)) return nullptr;
+    if (hipSetDevice(c->device) != hipSuccess) return nullptr;
     return (void*)c->stream;
 }
 
 int llm_sync(llm_ctx_t* c) {
     if (!c) return fail(LLM_E_ARG, "null context");
     HIP_TRY(hipSetDevice(c->device));
-    FLUSH_TRY(c);
     SYNC_TRY(c);
     return 0;
 }
@@ -1859,7 +1718,6 @@ int llm_sync(llm_ctx_t* c) {
 int llm_event_record(llm_ctx_t* c, uint32_t slot) {
     if (!c || slot >= 1024) return fail(LLM_E_ARG, "bad event slot");
     HIP_TRY(hipSetDevice(c->device));
-    FLUSH_TRY(c);
     if (c->events.empty()) {
         c->events.resize(1024);
         for (auto& e : c->events) HIP_TRY(hipEventCreate(&e));
@@ -1879,7 +1737,6 @@ int llm_event_elapsed_ms(llm_ctx_t* c, uint32_t a, uint32_t b, float* ms) {
 int llm_kernel_timing(llm_ctx_t* c, int enable) {
     if (!c) return fail(LLM_E_ARG, "null context");
     HIP_TRY(hipSetDevice(c->device));
-    FLUSH_TRY(c);
     harvest_timing(c);
     for (int k = 0; k < LLM_K_COUNT; k++) c->kernel_ms[k] = 0, c->kernel_n[k] = 0;
     c->timing = enable != 0;
@@ -1890,7 +1747,6 @@ int llm_kernel_stats(llm_ctx_t* c, uint32_t kernel, uint64_t* launches,
                      double* total_ms) {
     if (!c || kernel >= LLM_K_COUNT) return fail(LLM_E_ARG, "bad kernel id");
     HIP_TRY(hipSetDevice(c->device));
-    FLUSH_TRY(c);
     harvest_timing(c);
     if (launches) *launches = c->kernel_n[kernel];
     if (total_ms) *total_ms = c->kernel_ms[kernel];
@@ -1906,7 +1762,6 @@ int llm_bench_projection(llm_ctx_t* c, uint32_t kernel, uint32_t rows,
         kernel != LLM_K_GATEUP && kernel != LLM_K_DOWN)
         return fail(LLM_E_ARG, "not a projection kernel");
     HIP_TRY(hipSetDevice(c->device));
-    FLUSH_TRY(c);
     auto launch = [&](uint32_t layer) -> hipError_t {
         llm::ProjArgs a{};
         a.rows = rows;
@@ -1966,7 +1821,6 @@ int llm_bench_copy(llm_ctx_t* c, uint64_t bytes, uint32_t iters, float* ms) {
     if (!c || !ms || bytes < 16 || iters == 0)
         return fail(LLM_E_ARG, "bad copy arguments");
     HIP_TRY(hipSetDevice(c->device));
-    FLUSH_TRY(c);
     const size_t n16 = bytes / 16;
     void *src = nullptr, *dst = nullptr;
     HIP_TRY(hipMalloc(&src, n16 * 16));
@@ -2055,48 +1909,56 @@ std::string fmt_ms(double v) {
 int run_stack(llm_ctx_t* c, const int16_t* rows_host, uint32_t rows, uint32_t position,
               uint32_t layer_count, bool final_norm, bool prompt_block,
               uint32_t* tasks) {
-    if (int rc = ds_flush(c)) return rc;  // pending tasks may read pair 1
     const bool prof = c->log_fn != nullptr;
     const uint32_t ntask = 2 * layer_count + (final_norm ? 1u : 0u);
-    if (prof) {
+    if (prof)
         if (int rc = gen_events(c, 2 + ntask)) return rc;
-        HIP_TRY(hipEventRecord(c->gen_events[0], c->stream));
-    }
     const auto host0 = std::chrono::steady_clock::now();
-    invalidate_pair(c, 1);
-    if (rows == 1)  // a decode row: one contiguous copy (cheaper than a 2-D one)
-        HIP_TRY(hipMemcpyAsync(c->pairs[1], rows_host, (size_t)c->H * 2, hipMemcpyHostToDevice,
-                               c->stream));
-    else
-        HIP_TRY(hipMemcpy2DAsync(c->pairs[1], (size_t)c->Hp * 2, rows_host, (size_t)c->H * 2,
-                                 (size_t)c->H * 2, rows, hipMemcpyHostToDevice, c->stream));
-    c->n_h2d_rows++;
-    if (prof) HIP_TRY(hipEventRecord(c->gen_events[1], c->stream));
-    llm_status_t st;
-    uint32_t done = 0;
-    auto task = [&](uint32_t op, uint32_t layer, uint32_t in, uint32_t out) {
-        const int r = llm_task(c, op, layer, rows, position, 0, in, out, &st);
-        if (r < 0) return r;
-        if (r != 0 || st.op != op || !st.last_task)
-            return fail(LLM_E_STATE, "controller status failure: op " +
-                                         std::to_string(op) + " code " +
-                                         std::to_string(st.code));
-        (*tasks)++;
-        if (prof) {
-            if (int rc = ds_flush(c)) return rc;
-            HIP_TRY(hipEventRecord(c->gen_events[2 + done], c->stream));
+    auto enqueue = [&]() -> int {
+        if (prof) HIP_TRY(hipEventRecord(c->gen_events[0], c->stream));
+        invalidate_pair(c, 1);
+        if (rows == 1)  // a decode row: one contiguous copy (cheaper than a 2-D one)
+            HIP_TRY(hipMemcpyAsync(c->pairs[1], rows_host, (size_t)c->H * 2,
+                                   hipMemcpyHostToDevice, c->stream));
+        else
+            HIP_TRY(hipMemcpy2DAsync(c->pairs[1], (size_t)c->Hp * 2, rows_host,
+                                     (size_t)c->H * 2, (size_t)c->H * 2, rows,
+                                     hipMemcpyHostToDevice, c->stream));
+        c->n_h2d_rows++;
+        if (prof) HIP_TRY(hipEventRecord(c->gen_events[1], c->stream));
+        llm_status_t st;
+        uint32_t done = 0;
+        auto task = [&](uint32_t op, uint32_t layer, uint32_t in, uint32_t out) {
+            const int r = llm_task(c, op, layer, rows, position, 0, in, out, &st);
+            if (r < 0) return r;
+            if (r != 0 || st.op != op || !st.last_task)
+                return fail(LLM_E_STATE, "controller status failure: op " +
+                                             std::to_string(op) + " code " +
+                                             std::to_string(st.code));
+            if (prof) HIP_TRY(hipEventRecord(c->gen_events[2 + done], c->stream));
+            done++;
+            return 0;
+        };
+        int rc;
+        for (uint32_t layer = 0; layer < layer_count; layer++) {
+            if ((rc = task(LLM_OP_ATTENTION_SUBLAYER, layer, 1, 0))) return rc;
+            if ((rc = task(LLM_OP_FFN_SUBLAYER, layer, 0, 1))) return rc;
         }
-        done++;
+        if (final_norm && (rc = task(LLM_OP_FINAL_NORM, 0, 1, 0))) return rc;
         return 0;
     };
-    int rc;
-    for (uint32_t layer = 0; layer < layer_count; layer++) {
-        if ((rc = task(LLM_OP_ATTENTION_SUBLAYER, layer, 1, 0))) return rc;
-        if ((rc = task(LLM_OP_FFN_SUBLAYER, layer, 0, 1))) return rc;
-    }
-    if (final_norm && (rc = task(LLM_OP_FINAL_NORM, 0, 1, 0))) return rc;
+    if (int rc = enqueue()) return rc;
+    *tasks += ntask;
     if (!prof) return 0;
-    SYNC_TRY(c);
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    if (clear_waits(c)) {
+        // a bounded wait gave up: this forward again, without such waits
+        // (its K/V rows are rewritten from the same rows)
+        WaitFreeScope wf(c);
+        c->n_wait_reruns++;
+        if (int rc = enqueue()) return rc;
+        SYNC_TRY(c);
+    }
     const double host_ms = ms_since(host0);
     double phase_ms[3] = {0, 0, 0};  // attention, FFN, final norm
     for (uint32_t k = 0; k < ntask; k++) {
@@ -2134,7 +1996,10 @@ int run_stack(llm_ctx_t* c, const int16_t* rows_host, uint32_t rows, uint32_t po
             fmt_ms(input_ms + active_ms) + " host_elapsed_ms=" + fmt_ms(host_ms);
     if (prompt_block) line += std::string(" output_materialized=") + (final_norm ? "1" : "0");
     line += " intermediate_host_copy=0";
-    if (prompt_block) line += " kv_cache_owner=device";
+    if (prompt_block) line += " kv_cache_owner=controller";
+    c->coarse_active_ms += active_ms;
+    c->coarse_input_ms += input_ms;
+    c->coarse_host_ms += host_ms;
     emit(c, line);
     return 0;
 }
@@ -2150,7 +2015,6 @@ int ensure_keys_host(llm_ctx_t* c) {
 }
 
 int enqueue_argmax(llm_ctx_t* c, uint32_t pair, uint32_t row0, uint32_t rows) {
-    if (int rc = ds_flush(c)) return rc;
     HIP_TRY(hipMemsetAsync(c->lm_keys, 0, 8 * sizeof(unsigned long long), c->stream));
     HIP_TRY(llm::launch_lm_argmax(c->lm.d, c->lm.steps, c->lm_vocab,
                                   c->pairs[pair] + (size_t)row0 * c->Hp, c->Hp, rows,
@@ -2170,7 +2034,6 @@ int llm_load_lm_head(llm_ctx_t* c, const int16_t* table, uint32_t vocab) {
         return fail(LLM_E_ARG, "bad LM head arguments");
     if (c->H > 16384) return fail(LLM_E_ARG, "hidden too large for the argmax key");
     HIP_TRY(hipSetDevice(c->device));
-    FLUSH_TRY(c);
     Matrix& m = c->lm;
     const uint32_t n_pad = round_up(vocab, llm::kBlockRows);
     if (!m.d || m.n != vocab) {
@@ -2198,7 +2061,6 @@ int llm_lm_head_argmax(llm_ctx_t* c, uint32_t pair, uint32_t row0, uint32_t rows
         return fail(LLM_E_ARG, "bad LM head argmax arguments");
     if (!c->lm_vocab) return fail(LLM_E_STATE, "LM head not loaded");
     HIP_TRY(hipSetDevice(c->device));
-    FLUSH_TRY(c);
     if (int rc = ensure_keys_host(c)) return rc;
     if (int rc = enqueue_argmax(c, pair, row0, rows)) return rc;
     SYNC_TRY(c);
@@ -2224,7 +2086,6 @@ int llm_generate(llm_ctx_t* c, const int16_t* embedding, uint32_t vocab,
     for (uint32_t t = 0; t < n_prompt; t++)
         if (prompt[t] >= vocab) return fail(LLM_E_ARG, "prompt token outside the vocabulary");
     HIP_TRY(hipSetDevice(c->device));
-    FLUSH_TRY(c);
     llm_generate_stats_t local{};
     llm_generate_stats_t& S = stats ? *stats : local;
     S = llm_generate_stats_t{};
@@ -2256,24 +2117,49 @@ int llm_generate(llm_ctx_t* c, const int16_t* embedding, uint32_t vocab,
                     (size_t)c->H * 2);
     const uint64_t h2d0 = c->n_h2d_rows, d2h0 = c->n_d2h_rows, kv0 = c->n_kv_moves,
                    am0 = c->n_argmax;
+    const double active0 = c->coarse_active_ms, input0 = c->coarse_input_ms,
+                 hostapi0 = c->coarse_host_ms;
+    const uint64_t rr0 = c->n_wait_reruns;
     uint32_t last_row = 0;
     int rc;
-    // prompt blocks (host/host_qwen_8x64.cpp:9016-9060, :7840-7884)
-    HIP_TRY(hipEventRecord(ev_p0, c->stream));
-    for (uint32_t b0 = 0; b0 < n_prompt; b0 += block_size) {
-        const uint32_t rows = std::min(block_size, n_prompt - b0);
-        const bool final_block = b0 + rows == n_prompt;
-        if ((rc = run_stack(c, c->stage + (size_t)b0 * c->H, rows, b0, layer_count,
-                            final_block, true, &S.coarse_task_count)))
-            return rc;
-        S.prompt_forward_passes++;
-        if (final_block) S.output_materializations++;
-        else S.released_prompt_blocks++;
-        last_row = rows - 1;
-    }
-    HIP_TRY(hipEventRecord(ev_p1, c->stream));
-    if (max_new_tokens == 0) {
+    // prompt blocks (host/host_qwen_8x64.cpp:9016-9060, :7840-7884), enqueued
+    // without waiting; `count` adds them to the request's counters (a re-run
+    // after a wait that gave up does not)
+    auto run_prompt = [&](bool count) -> int {
+        uint32_t uncounted = 0;
+        HIP_TRY(hipEventRecord(ev_p0, c->stream));
+        for (uint32_t b0 = 0; b0 < n_prompt; b0 += block_size) {
+            const uint32_t rows = std::min(block_size, n_prompt - b0);
+            const bool final_block = b0 + rows == n_prompt;
+            if (int r = run_stack(c, c->stage + (size_t)b0 * c->H, rows, b0, layer_count,
+                                  final_block, true, count ? &S.coarse_task_count : &uncounted))
+                return r;
+            if (count) {
+                S.prompt_forward_passes++;
+                if (final_block) S.output_materializations++;
+                else S.released_prompt_blocks++;
+            }
+            last_row = rows - 1;
+        }
+        HIP_TRY(hipEventRecord(ev_p1, c->stream));
+        return 0;
+    };
+    // A synchronisation that finds a bounded wait between workgroups given
+    // up: what was enqueued since the previous one (`redo`) runs again, once,
+    // on launches without such waits, and is synchronised.  K/V rows of the
+    // invalid run are rewritten by the re-run from the same inputs.
+    auto settle = [&](const std::function<int()>& redo) -> int {
+        HIP_TRY(hipStreamSynchronize(c->stream));
+        if (!clear_waits(c)) return 0;
+        WaitFreeScope wf(c);
+        c->n_wait_reruns++;
+        if (int r = redo()) return r;
         SYNC_TRY(c);
+        return 0;
+    };
+    if ((rc = run_prompt(true))) return rc;
+    if (max_new_tokens == 0) {
+        if ((rc = settle([&] { return run_prompt(false); }))) return rc;
         S.prompt_forward_ms = event_ms(ev_p0, ev_p1);
     }
     // sampled tokens (host/host_qwen_8x64.cpp:9091-9136); times from stream
@@ -2282,9 +2168,30 @@ int llm_generate(llm_ctx_t* c, const int16_t* embedding, uint32_t vocab,
     auto gen0 = std::chrono::steady_clock::now();
     uint32_t token = 0;
     for (uint32_t step = 0; step < max_new_tokens; step++) {
-        if ((rc = enqueue_argmax(c, 0, last_row, 1))) return rc;
-        HIP_TRY(hipEventRecord(ev_l, c->stream));
-        SYNC_TRY(c);
+        auto argmax = [&]() -> int {
+            if (int r = enqueue_argmax(c, 0, last_row, 1)) return r;
+            HIP_TRY(hipEventRecord(ev_l, c->stream));
+            return 0;
+        };
+        if ((rc = argmax())) return rc;
+        if (step == 0) {
+            rc = settle([&] {
+                const int r = run_prompt(false);
+                return r ? r : argmax();
+            });
+        } else {
+            const uint32_t prev = n_prompt + step - 1;  // the last forward's row
+            rc = settle([&]() -> int {
+                uint32_t uncounted = 0;
+                HIP_TRY(hipEventRecord(ev_a, c->stream));
+                if (int r = run_stack(c, c->stage + (size_t)prev * c->H, 1, prev, layer_count,
+                                      true, false, &uncounted))
+                    return r;
+                HIP_TRY(hipEventRecord(ev_b, c->stream));
+                return argmax();
+            });
+        }
+        if (rc) return rc;
         token = key_token(c->keys_host[0]);
         if (step == 0) {
             S.prompt_forward_ms = event_ms(ev_p0, ev_p1);
@@ -2316,6 +2223,7 @@ int llm_generate(llm_ctx_t* c, const int16_t* embedding, uint32_t vocab,
     S.output_migrations = (uint32_t)(c->n_d2h_rows - d2h0);
     S.kv_migrations = (uint32_t)(c->n_kv_moves - kv0);
     S.argmax_readbacks = (uint32_t)(c->n_argmax - am0);
+    S.wait_reruns = (uint32_t)(c->n_wait_reruns - rr0);
     if (c->log_fn) {
         const double mean_ms =
             S.generated_forward_passes ? S.generated_forward_ms / S.generated_forward_passes : 0;
@@ -2334,14 +2242,26 @@ int llm_generate(llm_ctx_t* c, const int16_t* embedding, uint32_t vocab,
                     " mean_inter_token_ms=" + fmt_ms(mean_ms) + " decode_token_s=" +
                     fmt_ms(dec) + " lm_head_host_ms=" + fmt_ms(S.lm_head_ms) +
                     " total_host_elapsed_ms=" + fmt_ms(S.total_ms) +
+                    // no golden check runs inside the request: the process
+                    // time is the inference time and validation is off
+                    " total_process_elapsed_ms=" + fmt_ms(S.total_ms) +
+                    " post_inference_validation_ms=0 validation_schedule=disabled"
                     " event_timing_domain=hip_stream_event coarse_task_count=" +
-                    std::to_string(S.coarse_task_count) +
+                    std::to_string(S.coarse_task_count) + " coarse_kernel_active_ms=" +
+                    fmt_ms(c->coarse_active_ms - active0) + " coarse_profiled_sequence_ms=" +
+                    fmt_ms(c->coarse_active_ms - active0 + c->coarse_input_ms - input0) +
+                    " coarse_host_api_elapsed_ms=" + fmt_ms(c->coarse_host_ms - hostapi0) +
+                    " coarse_input_migration_ms=" + fmt_ms(c->coarse_input_ms - input0) +
+                    " coarse_status_kernel_ms=0 coarse_status_migration_ms=0"
+                    " coarse_output_migration_ms=0"
                     " output_materializations=" + std::to_string(S.output_materializations) +
                     " released_prompt_blocks=" + std::to_string(S.released_prompt_blocks) +
+                    " e2e_numeric_golden=0 e2e_numeric_steps=0 e2e_numeric_checked_values=0"
+                    " e2e_numeric_max_raw_error=0 e2e_numeric_tolerance=0 e2e_golden_host_ms=0"
                     " input_migrations=" + std::to_string(S.input_migrations) +
                     " output_migrations=" + std::to_string(S.output_migrations) +
                     " kv_migrations=" + std::to_string(S.kv_migrations) +
-                    " intermediate_host_copy=0 kv_cache_owner=device PASS");
+                    " intermediate_host_copy=0 kv_cache_owner=controller PASS");
     }
     return 0;
 }

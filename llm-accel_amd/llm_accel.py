@@ -48,7 +48,7 @@ EXPORTS = (
 CKPT_TIE_EMBEDDINGS = 1
 CKPT_REQUIRE_LM_HEAD = 2
 KERNELS = ("rmsnorm", "qkv", "rope", "attention", "oproj", "gateup", "down",
-           "attn_sublayer", "decode_stack")
+           "attn_sublayer")
 
 
 class Shape(ctypes.Structure):
@@ -82,7 +82,7 @@ class GenerateStats(ctypes.Structure):
     _fields_ = [(n, ctypes.c_uint32) for n in (
         "prompt_tokens", "generated_tokens", "prompt_forward_passes",
         "generated_forward_passes", "coarse_task_count",
-        "output_materializations", "released_prompt_blocks", "reserved0")] + [
+        "output_materializations", "released_prompt_blocks", "wait_reruns")] + [
             (n, ctypes.c_double) for n in (
                 "prompt_forward_ms", "time_to_first_token_ms",
                 "generated_forward_ms", "lm_head_ms", "total_ms",
@@ -92,7 +92,7 @@ class GenerateStats(ctypes.Structure):
                 "argmax_readbacks")]
 
     def as_dict(self):
-        return {n: getattr(self, n) for n, _ in self._fields_ if n != "reserved0"}
+        return {n: getattr(self, n) for n, _ in self._fields_}
 
 
 class AccelError(RuntimeError):

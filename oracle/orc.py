@@ -12,7 +12,7 @@ import numpy as np
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB_PATH = os.path.join(_HERE, "liborc.so")
 
-EXP_FLOOR, EXP_ROUND = 0, 1
+EXP_FLOOR, EXP_ROUND, EXP_HLS = 0, 1, 2
 UID_DIVREJ, UID_LEMIRE = 0, 1
 SEM_RAW_PAYLOAD, SEM_DIRECT, SEM_LEGACY_Q8_8 = 0, 1, 2
 PROJ_Q, PROJ_K, PROJ_V, PROJ_O, PROJ_GATE, PROJ_UP, PROJ_DOWN = range(7)
@@ -124,7 +124,7 @@ def p16(a):
     return a.ctypes.data_as(_i16p)
 
 
-def set_exp_policy(q8_8=EXP_FLOOR, q2_14=EXP_FLOOR):
+def set_exp_policy(q8_8=EXP_HLS, q2_14=EXP_HLS):
     lib.orc_set_exp_policy(q8_8, q2_14)
 
 

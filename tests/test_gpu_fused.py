@@ -21,12 +21,9 @@ def _say(msg):
 
 
 def _accel(spec, layers, max_seq, env):
-    """A context created with `env` set (read once, at creation).  Decode
-    tasks here take the fused sublayer or the separate launches: the
-    persistent decode launch (tests/test_gpu_stack.py) is switched off."""
+    """A context created with `env` set (read once, at creation)."""
     import llm_accel
     env = dict(env)
-    env.setdefault("LLM_ACCEL_STACK", "0")
     old = {k: os.environ.get(k) for k in env}
     os.environ.update(env)
     try:

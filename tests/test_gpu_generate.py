@@ -163,7 +163,7 @@ def test_generate_report_lines_and_residency_contract():
     assert [f["output_materialized"] for f in pre] == ["0", "0", "1"]
     assert [int(f["tasks"]) for f in pre] == [ntask, ntask, ntask + 1]
     for f in pre:
-        assert f["intermediate_host_copy"] == "0" and f["kv_cache_owner"] == "device"
+        assert f["intermediate_host_copy"] == "0" and f["kv_cache_owner"] == "controller"
         assert float(f["kernel_active_ms"]) > 0
         assert float(f["input_migration_ms"]) >= 0
         assert float(f["output_migration_ms"]) == 0
@@ -188,12 +188,31 @@ def test_generate_report_lines_and_residency_contract():
     assert int(prof["released_prompt_blocks"]) == blocks - 1
     assert int(prof["input_migrations"]) == blocks + G - 1
     assert int(prof["output_migrations"]) == 0 and int(prof["kv_migrations"]) == 0
-    assert prof["intermediate_host_copy"] == "0" and prof["kv_cache_owner"] == "device"
+    assert prof["intermediate_host_copy"] == "0" and prof["kv_cache_owner"] == "controller"
     assert float(prof["decode_token_s"]) > 0
+    # the fields the reference's release checks read from this line
+    # (scripts/report_vitis_8x64_e2e_trace.sh:201-231,
+    # scripts/verify_qwen3b_e2e_release.sh:200-218); event_timing_domain
+    # names this platform's clock (hip_stream_event), as the reference's
+    # names its own
+    assert int(prof["output_materializations"]) == G
+    assert int(prof["coarse_task_count"]) == blocks * ntask + 1 + (G - 1) * (ntask + 1)
+    assert prof["validation_schedule"] == "disabled" and prof["e2e_numeric_golden"] == "0"
+    assert prof["event_timing_domain"] == "hip_stream_event"
     for key in ("prompt_forward_ms", "prefill_token_s", "time_to_first_token_ms",
                 "generated_forward_ms", "mean_inter_token_ms", "lm_head_host_ms",
-                "total_host_elapsed_ms"):
+                "total_host_elapsed_ms", "total_process_elapsed_ms",
+                "post_inference_validation_ms", "coarse_kernel_active_ms",
+                "coarse_profiled_sequence_ms", "coarse_host_api_elapsed_ms",
+                "coarse_input_migration_ms", "coarse_status_kernel_ms",
+                "coarse_status_migration_ms", "coarse_output_migration_ms",
+                "e2e_golden_host_ms"):
         assert float(prof[key]) >= 0, key
+    assert float(prof["coarse_kernel_active_ms"]) >= sum(
+        float(f["kernel_active_ms"]) for f in pre) > 0
+    for key in ("e2e_numeric_steps", "e2e_numeric_checked_values",
+                "e2e_numeric_max_raw_error", "e2e_numeric_tolerance"):
+        assert int(prof[key]) == 0, key
     assert st["input_migrations"] == blocks + G - 1
     assert st["output_migrations"] == 0 and st["kv_migrations"] == 0
 
@@ -270,9 +289,6 @@ def test_kat2_kat3_final_hidden_rows_match_oracle(qwen3b_reference_model, layers
     assert [orc.checksum(got[p]) for p in range(8)] == [orc.checksum(want[p]) for p in range(8)]
 
 
-@pytest.mark.xfail(strict=True, reason="parity unpinned: the reference's hls::exp<16,8> "
-                   "(SiLU, host/host_qwen_8x64.cpp:578-586) is not floor(e^x*256) at every "
-                   "entry, so the post-FFN rows differ from the reference's in low bits")
 @pytest.mark.parametrize("layers,kat", [(1, "kat2_qwen3b_l1"), (2, "kat3_qwen3b_l2")])
 def test_kat2_kat3_final_hidden_checksums_on_gpu(qwen3b_reference_model, layers, kat):
     """results/qwen3b-e2e-20260820/host.evidence.log:40-47 (1 layer, 8
@@ -286,3 +302,70 @@ def test_kat2_kat3_final_hidden_checksums_on_gpu(qwen3b_reference_model, layers,
     else:
         assert orc.checksum(got[7]) == int(k["final_hidden_checksum_pos7"], 16)
 
+
+
+@pytest.mark.parametrize("path,env,with_log", [
+    ("tile", {}, False),
+    ("tile", {}, True),
+    ("gqa", {"LLM_ACCEL_GQA_MIN_TILES": "5"}, False),
+])
+def test_generate_recovers_when_waits_give_up(monkeypatch, path, env, with_log):
+    """Every bounded wait between workgroups forced to give up at once
+    (LLM_ACCEL_WAIT_LIMIT=0): the one-launch kernels of the forwards (the
+    fused decode sublayer at <= 4 tiles, the one-launch tile or GQA path
+    beyond) abort, and llm_generate runs each invalidated stretch again on
+    launches without such waits -- the reference's controller completes
+    every command it accepts (kernel/control_cache_8x64.cpp:5892-5957).
+    Tokens and every K/V row equal the oracle's, no error is returned and
+    the re-runs are counted.  With a line sink each forward is synchronised
+    and re-run on its own."""
+    import llm_accel
+    monkeypatch.setenv("LLM_ACCEL_WAIT_LIMIT", "0")
+    for k, v in env.items():
+        monkeypatch.setenv(k, v)
+    spec = workloads.CONFIG_A
+    layers = 2
+    synth = workloads.SyntheticModel(spec, layers=layers)
+    emb = synth.embedding()
+    P, G, B = 300, 4, 8
+    prompt = [int(t) for t in synth.tokens(P)]
+    max_seq = P + G + 8
+    log = [] if with_log else None
+    with llm_accel.Accelerator(accel_shape(spec, layers=layers, max_seq=max_seq)) as a:
+        a.load_model(synth)
+        a.load_lm_head(emb)
+        _say(f"case generate with every wait giving up: {path} log={with_log}")
+        toks, st = a.generate(emb, prompt, B, layers, G, log=log)
+        n = P + G - 1
+        kv_got = [[a.kv_read(l, h, 0, n) for h in range(spec.kv_heads)]
+                  for l in range(layers)]
+    assert st["wait_reruns"] >= 1
+    assert st["coarse_task_count"] == -(-P // B) * 2 * layers + 1 + (G - 1) * (2 * layers + 1)
+    om = oracle_from_synthetic(synth, oracle_shape(spec, layers=layers, max_seq=max_seq))
+    kv = om.new_kv()
+
+    def forward(rows, pos, final):
+        h = emb[rows].copy()
+        for layer in range(layers):
+            _, h, _ = om.task(kv, 18, layer, h, pos)
+            _, h, _ = om.task(kv, 19, layer, h, pos)
+        if final:
+            _, h, _ = om.task(kv, 20, 0, h, pos)
+        return h
+
+    for b0 in range(0, P, B):
+        h = forward(prompt[b0:b0 + B], b0, b0 + B >= P)
+    want = []
+    for step in range(G):
+        t = orc.lm_head_argmax(emb, h[-1])
+        want.append(t)
+        if step + 1 < G:
+            h = forward([t], P + step, True)
+    assert toks == want
+    for l in range(layers):
+        for hd in range(spec.kv_heads):
+            k, v = kv_got[l][hd]
+            assert np.array_equal(k, kv[0][l, hd, :n]), (l, hd)
+            assert np.array_equal(v, kv[1][l, hd, :n]), (l, hd)
+    if with_log:
+        assert log[-1].endswith(" PASS")

@@ -72,7 +72,7 @@ def test_outlier_weights_p8_decode_lm_head(value, interval):
             stats = acc.kernel_stats()
             acc.kernel_timing(False)
             if rows == 1:  # one launch for the decode row, not the separate kernels
-                assert stats["attn_sublayer"][0] + stats["decode_stack"][0] >= 1, stats
+                assert stats["attn_sublayer"][0] >= 1, stats
                 assert stats["attention"][0] == 0 and stats["qkv"][0] == 0, stats
             toks, scores = acc.lm_head_argmax(0, 0, rows)
             assert toks == [orc.lm_head_argmax(head, cur[r]) for r in range(rows)]

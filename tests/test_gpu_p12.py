@@ -79,7 +79,7 @@ def test_ffn_p12_matches_oracle_and_16bit(cfg, case):
     rng = np.random.default_rng(5)
     outs = {}
     for p12 in ("1", "0"):
-        with _accel(spec, {"LLM_ACCEL_P12": p12, "LLM_ACCEL_STACK": "0"}) as acc:
+        with _accel(spec, {"LLM_ACCEL_P12": p12}) as acc:
             acc.load_model(model)
             got = []
             for rows in (1, 2):
@@ -128,8 +128,8 @@ def test_attention_p12_matches_oracle_and_16bit(cfg, case, n):
     outs = {}
     for p12 in ("1", "0"):
         import llm_accel
-        old = {k: os.environ.get(k) for k in ("LLM_ACCEL_P12", "LLM_ACCEL_STACK")}
-        os.environ.update({"LLM_ACCEL_P12": p12, "LLM_ACCEL_STACK": "0"})
+        old = {k: os.environ.get(k) for k in ("LLM_ACCEL_P12",)}
+        os.environ.update({"LLM_ACCEL_P12": p12})
         try:
             acc = llm_accel.Accelerator(accel_shape(spec, layers=1, max_seq=n + 8))
         finally:

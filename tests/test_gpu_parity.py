@@ -115,7 +115,10 @@ def test_decoder_layer_op16_matches_18_19():
         oshape = oracle_shape(spec, layers=1, max_seq=64)
         om = oracle_from_synthetic(synth, oshape)
         code, want, ost = om.task(om.new_kv(), 16, 0, h, 0)
+        assert code == 0 and rc == 0
         assert st16.as_tuple() == ost.as_tuple()
+        # op 16's rows against the oracle's decoder layer (host:4876-4977)
+        assert first_mismatch(got16, want) is None
 
 
 def test_in_place_pairs():
@@ -188,7 +191,7 @@ def test_kv_preload_then_decode_long_context():
     assert first_mismatch(got, want) is None
 
 
-@pytest.mark.parametrize("n", [1024, 4096, 16384])
+@pytest.mark.parametrize("n", [128, 1024, 4096, 16384])
 def test_context_sweep_decode_forward(n):
     """K/V of one Qwen2.5-3B-shaped layer preloaded
     with seeded Q8.8 N(0, 0.3) to length n, then one decode forward (Task
@@ -538,6 +541,54 @@ def test_gqa_epoch_wraps(monkeypatch, scan_fused):
             k, v = a.kv_read(0, h, n0, 6)
             assert first_mismatch(k, kc[0, h, n0:n0 + 6]) is None
             assert first_mismatch(v, vc[0, h, n0:n0 + 6]) is None
+
+
+def test_gqa_epoch_wrap_clears_stale_words(monkeypatch):
+    """A full epoch period in one context: a decode row at 700 positions
+    (11 tiles) leaves maxima and sums tagged with epoch 1 at tiles 0-10;
+    65,534 decode rows at position 320 (6 tiles) retag tiles 0-5 only;
+    the next launch wraps to epoch 1 and runs over 11 tiles again with
+    another row, where tiles 6-10 still hold the first row's epoch-1
+    words unless the wrap cleared them.  Both rows and the appended K/V
+    are checked against the oracle."""
+    import llm_accel
+    monkeypatch.setenv("LLM_ACCEL_GQA_MIN_TILES", "5")
+    spec = workloads.CONFIG_A
+    synth = workloads.SyntheticModel(spec, layers=1)
+    n0, filler_pos = 700, 320
+    om = oracle_from_synthetic(synth, oracle_shape(spec, layers=1, max_seq=n0 + 8))
+    kc, vc = om.new_kv()
+    xs = synth.hidden_rows(3, seed_offset=91)
+    with llm_accel.Accelerator(accel_shape(spec, layers=1, max_seq=n0 + 8)) as a:
+        a.load_model(synth)
+        for h in range(spec.kv_heads):
+            k, v = synth.kv_rows(n0, seed_offset=50 + h)
+            kc[0, h, :n0], vc[0, h, :n0] = k, v
+            a.kv_write(0, h, 0, k, v)
+        _say("case epoch period: first row at 700 (epoch 1)")
+        a.upload(2, xs[0:1])
+        assert a.task(18, 0, 1, n0, 2, 0)[0] == 0
+        got = a.download(0, 1)
+        _, want, _ = om.task((kc, vc), 18, 0, xs[0:1], n0)
+        assert first_mismatch(got, want) is None
+        _say("case epoch period: 65,534 rows at 320 (epochs 2..65535)")
+        a.upload(3, xs[1:2])
+        for i in range(65534):
+            rc, _ = a.task(18, 0, 1, filler_pos, 3, 1)
+            assert rc == 0, i
+        got = a.download(1, 1)
+        _, want, _ = om.task((kc, vc), 18, 0, xs[1:2], filler_pos)
+        assert first_mismatch(got, want) is None
+        _say("case epoch period: wrap to epoch 1 at 700 with another row")
+        a.upload(2, xs[2:3])
+        assert a.task(18, 0, 1, n0, 2, 0)[0] == 0
+        got = a.download(0, 1)
+        _, want, _ = om.task((kc, vc), 18, 0, xs[2:3], n0)
+        assert first_mismatch(got, want) is None
+        for h in range(spec.kv_heads):
+            k, v = a.kv_read(0, h, 0, n0 + 1)
+            assert first_mismatch(k, kc[0, h, :n0 + 1]) is None
+            assert first_mismatch(v, vc[0, h, :n0 + 1]) is None
 
 
 @pytest.fixture

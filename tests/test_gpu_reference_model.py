@@ -28,8 +28,8 @@ def _say(msg):
 
 
 @pytest.fixture(autouse=True)
-def _floor_tables():
-    orc.set_exp_policy(orc.EXP_FLOOR, orc.EXP_FLOOR)
+def _reference_tables():
+    orc.set_exp_policy(orc.EXP_HLS, orc.EXP_HLS)
     yield
 
 

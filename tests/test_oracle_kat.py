@@ -16,8 +16,8 @@ KAT = json.load(open(os.path.join(HERE, "golden", "kat.json")))
 
 
 @pytest.fixture(autouse=True)
-def _floor_tables():
-    orc.set_exp_policy(orc.EXP_FLOOR, orc.EXP_FLOOR)
+def _reference_tables():
+    orc.set_exp_policy(orc.EXP_HLS, orc.EXP_HLS)
     yield
 
 
@@ -126,24 +126,45 @@ def test_p2_legacy_q8_8_attention_fingerprint():
     assert (n, mx, first) == (k["mismatches"], k["max_error"], k["first"])
 
 
-def test_kat1_silu_pinned_probes():
-    # Probes whose value does not move with the unpinned hls::exp<16,8>
-    # entries of SiLU.
+def test_kat1_final_probes():
+    """Final-norm probes of row 3 for both semantics (log:27-30): columns 2
+    and 4 move with the Q8.8 hls::exp<16,8> under SiLU, columns 1 and 9 do
+    not."""
     k = KAT["kat1_qwen_layer_p8"]
     r = _kat1(8)
     row = k["final_probe_row"]
     got_p = [int(r["fin_p"][row, c]) for c in k["final_probe_cols"]]
     got_d = [int(r["fin_d"][row, c]) for c in k["final_probe_cols"]]
-    assert got_p[0] == k["final_probe_raw_payload"][0]
-    assert got_p[3] == k["final_probe_raw_payload"][3]
-    assert got_d[0] == k["final_probe_direct"][0]
-    assert got_d[3] == k["final_probe_direct"][3]
+    assert got_p == k["final_probe_raw_payload"]
+    assert got_d == k["final_probe_direct"]
 
 
-@pytest.mark.xfail(strict=True, reason="parity unpinned: hls::exp<16,8> (SiLU) "
-                   "is not floor(e^x*256) at every entry; the HLS math library "
-                   "is not available to pin it")
+def test_kat1_floor_exp_table_is_rejected():
+    """Control: with floor(e^x * 256) as the Q8.8 exponential the post-FFN
+    fingerprint and two of the four probes differ from the reference's,
+    so the KAT-1 checks above do discriminate the table."""
+    k = KAT["kat1_qwen_layer_p8"]
+    orc.set_exp_policy(orc.EXP_FLOOR, orc.EXP_HLS)
+    try:
+        m = orc.Model(orc.profile("qwen-layer"), 1, True)
+        m.init_reference_random(k["seed"], orc.UID_DIVREJ)
+        h = orc.make_random_tensor(8, 2048, k["seed"] ^ k["hidden_seed_xor"], -48, 48)
+        _, out_p = m.prefill_sequence(h, 0, orc.SEM_RAW_PAYLOAD)
+        _, out_d = m.prefill_sequence(h, 0, orc.SEM_DIRECT)
+        fin_p = orc.rmsnorm(out_p, m.norms()[2])
+    finally:
+        orc.set_exp_policy(orc.EXP_HLS, orc.EXP_HLS)
+    n, mx, first = _fingerprint(out_p, out_d)
+    assert (n, mx) != (k["post_ffn_mismatches"], k["post_ffn_max_error"])
+    probes = [int(fin_p[k["final_probe_row"], c]) for c in k["final_probe_cols"]]
+    assert probes[1] != k["final_probe_raw_payload"][1]
+    assert probes[2] != k["final_probe_raw_payload"][2]
+
+
 def test_kat1_post_ffn_fingerprint():
+    """Post-FFN difference fingerprint of the two attention semantics
+    (log:12-26): pins the Q8.8 hls::exp<16,8> under SiLU at the entries
+    the gate values of row 3 reach."""
     k = KAT["kat1_qwen_layer_p8"]
     r = _kat1(8)
     n, mx, first = _fingerprint(r["out_p"], r["out_d"])
@@ -189,16 +210,7 @@ def test_kat3_qwen3b_two_layer_tokens():
     assert toks == KAT["kat3_qwen3b_l2"]["generated"]
 
 
-_SILU_XFAIL = pytest.mark.xfail(
-    strict=True,
-    reason="parity unpinned: the reference's hls::exp<16,8> (SiLU, host/host_qwen_8x64.cpp"
-           ":578-586) is not floor(e^x*256) at every entry; the final hidden rows after "
-           "the FFN differ from the reference's in low bits, so their FNV-1a checksums "
-           "do not reproduce (the sampled tokens do)")
-
-
 @pytest.mark.slow
-@_SILU_XFAIL
 @pytest.mark.parametrize("pos", range(8))
 def test_kat2_qwen3b_one_layer_final_hidden_checksums(pos):
     """results/qwen3b-e2e-20260820/host.evidence.log:40-47: FNV-1a-64 of the
@@ -210,7 +222,6 @@ def test_kat2_qwen3b_one_layer_final_hidden_checksums(pos):
 
 
 @pytest.mark.slow
-@_SILU_XFAIL
 def test_kat3_qwen3b_two_layer_final_hidden_checksum_pos7():
     """results/qwen3b-e2e-l2-20260821/host.evidence.log:49: position 7's
     final-normed row after two layers (golden-verified)."""
