@@ -99,6 +99,13 @@ class SyntheticModel:
     def weight(self, layer, proj):
         return self._w[layer][proj]
 
+    def plant_outliers(self, value=2048):
+        """One weight of raw `value` (outside [-2048, 2047]: the 12-bit
+        copies do not hold it) at row 0, column 0 of every matrix."""
+        for per in self._w:
+            for w in per:
+                w[0, 0] = value
+
     def norms(self):
         return self._norms
 
