@@ -63,6 +63,10 @@ struct AttnArgs {
     uint32_t* host_abort; // host-visible copy
     uint32_t wait_limit;  // bound of one wait (100 MHz ticks)
     uint32_t cus;
+    // one-launch kernels go through hipLaunchCooperativeKernel, which
+    // refuses a grid the device cannot hold at once (other work holding
+    // compute units included); the launcher then takes the separate launches
+    uint32_t coop;
 };
 
 // Tile-path arrivals: the tiles of a (row, query head) arrive in groups of

@@ -1553,8 +1553,16 @@ static hipError_t launch_d(const AttnArgs& a, uint32_t rows, uint32_t kv_heads,
         const uint32_t grid = tile_grid(rows, tiles, a.num_kv_heads, a.group);
         if (a.tile_fused && a.s_tmax32 && tiles <= kTileFusedMaxTiles &&
             grid <= tile_fused_capacity<DT>(a.cus)) {
-            attention_tile_fused_kernel<DT><<<grid, 2 * D, 0, st>>>(g);
-            return hipGetLastError();
+            if (!a.coop) {
+                attention_tile_fused_kernel<DT><<<grid, 2 * D, 0, st>>>(g);
+                return hipGetLastError();
+            }
+            void* args[] = {&g};
+            const hipError_t e = hipLaunchCooperativeKernel(
+                reinterpret_cast<const void*>(&attention_tile_fused_kernel<DT>), dim3(grid),
+                dim3(2 * D), args, 0, st);
+            if (e != hipErrorCooperativeLaunchTooLarge) return e;
+            (void)hipGetLastError();  // refused: the two launches below
         }
         attention_tile_scores_kernel<DT><<<grid, 2 * D, 0, st>>>(g);
         hipError_t e = hipGetLastError();

@@ -958,15 +958,36 @@ hipError_t launch_gqa_d(const AttnArgs& a, uint32_t rows, uint32_t tiles, hipStr
     const uint32_t scan_grid = rows * a.num_heads * (D / GSE);
     const bool one = a.epoch && a.s_gmax32 && tiles <= kGqaFusedMaxTiles;
     hipError_t e;
+    // The one-launch kernels, cooperatively when a.coop: a grid the device
+    // cannot hold at once is refused and the next variant is taken.
+    auto coop_launch = [&](const void* fn, uint32_t n) -> hipError_t {
+        void* args[] = {&g};
+        const hipError_t r = hipLaunchCooperativeKernel(fn, dim3(n), dim3(GNT), args, 0, st);
+        if (r == hipErrorCooperativeLaunchTooLarge) (void)hipGetLastError();
+        return r;
+    };
     if (one && a.s_gsum64 && grid + scan_grid <= gqa_fused_capacity<D, true>(a.cus)) {
-        attention_gqa_fused_kernel<D, true><<<grid + scan_grid, GNT, 0, st>>>(g);
-        return hipGetLastError();
+        if (!a.coop) {
+            attention_gqa_fused_kernel<D, true><<<grid + scan_grid, GNT, 0, st>>>(g);
+            return hipGetLastError();
+        }
+        e = coop_launch(reinterpret_cast<const void*>(&attention_gqa_fused_kernel<D, true>),
+                        grid + scan_grid);
+        if (e != hipErrorCooperativeLaunchTooLarge) return e;
     }
+    bool one_done = false;
     if (one && grid <= gqa_fused_capacity<D, false>(a.cus)) {
-        attention_gqa_fused_kernel<D, false><<<grid, GNT, 0, st>>>(g);
-        e = hipGetLastError();
-        if (e != hipSuccess) return e;
-    } else {
+        if (!a.coop) {
+            attention_gqa_fused_kernel<D, false><<<grid, GNT, 0, st>>>(g);
+            e = hipGetLastError();
+        } else {
+            e = coop_launch(reinterpret_cast<const void*>(&attention_gqa_fused_kernel<D, false>),
+                            grid);
+        }
+        if (e != hipSuccess && e != hipErrorCooperativeLaunchTooLarge) return e;
+        one_done = e == hipSuccess;
+    }
+    if (!one_done) {
         attention_gqa_scores_kernel<D><<<grid, GNT, 0, st>>>(g);
         e = hipGetLastError();
         if (e != hipSuccess) return e;

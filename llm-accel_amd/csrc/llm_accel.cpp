@@ -157,6 +157,13 @@ struct llm_ctx {
     // GQA scores and PV in one launch when the grid fits on the device;
     // LLM_ACCEL_GQA_FUSED=0 keeps three launches
     bool gqa_fused = true;
+    // LLM_ACCEL_COOP=1: the one-launch attention kernels go through the
+    // cooperative launch, which refuses a grid the device cannot hold at
+    // once (then the separate launches run).  Off by default: measured at
+    // +19 us per one-layer decode forward (40.7 -> 59.8 us at 320
+    // positions); the bounded waits and llm_generate's wait-free re-run
+    // cover the same case without that cost.
+    bool coop = false;
     // ... with the run-sum scan as workgroups of that launch (tagged tile
     // sums in s_gsum64); LLM_ACCEL_GQA_SCAN_FUSED=0 keeps it a launch
     uint64_t* s_gsum64 = nullptr;
@@ -655,6 +662,7 @@ int enqueue_attention_sublayer(llm_ctx* c, uint32_t layer, uint32_t R,
     at.host_abort = c->host_abort;
     at.wait_limit = c->wait_limit;
     at.cus = (uint32_t)c->cus;
+    at.coop = c->coop ? 1u : 0u;
     at.s_scores = c->s_scores;
     at.s_tmax = c->s_tmax;
     at.s_tsum = c->s_tsum;
@@ -978,6 +986,7 @@ int llm_ctx_create(const llm_shape_t* shape, int device, uint32_t num_pairs,
         c->gqa_fused = std::strcmp(e, "0") != 0;
     if (const char* e = std::getenv("LLM_ACCEL_GQA_SCAN_FUSED"))
         c->gqa_scan_fused = std::strcmp(e, "0") != 0;
+    if (const char* e = std::getenv("LLM_ACCEL_COOP")) c->coop = std::strcmp(e, "1") == 0;
     // the GQA path's epoch before the first launch (tests start it just
     // below kGqaEpochMax so that it wraps within a few launches)
     if (const char* e = std::getenv("LLM_ACCEL_GQA_EPOCH_START"))

@@ -294,3 +294,44 @@ def test_tile_path_wait_timeout_is_reported(path):
     code, want, _ = om.task((kc2, vc2), 18, 0, h8, 100)
     assert code == 0
     assert first_mismatch(got, want) is None
+
+
+@pytest.mark.parametrize("path", ["tile", "gqa", "gqa_no_scan"])
+def test_cooperative_launch_of_one_launch_kernels(path):
+    """LLM_ACCEL_COOP=1: the one-launch tile and GQA kernels go through
+    hipLaunchCooperativeKernel (a grid the device cannot hold at once is
+    refused and the separate launches run instead).  Decode rows at 300 and
+    700 positions and an 8-row block at 520 against the oracle, every
+    appended K/V row included."""
+    import llm_accel
+    spec = workloads.CONFIG_B
+    n = 700
+    synth = workloads.SyntheticModel(spec, seed=workloads.SEED, layers=1)
+    om = oracle_from_synthetic(synth, oracle_shape(spec, layers=1, max_seq=n + 16))
+    kc, vc = om.new_kv()
+    env = {"LLM_ACCEL_COOP": "1"}
+    if path != "tile":
+        env["LLM_ACCEL_GQA_MIN_TILES"] = "5"
+    if path == "gqa_no_scan":
+        env["LLM_ACCEL_GQA_SCAN_FUSED"] = "0"
+    acc = _accel(spec, 1, n + 16, env)
+    with acc:
+        acc.load_model(synth)
+        for h in range(spec.kv_heads):
+            k, v = synth.kv_rows(n, seed_offset=90 + h)
+            kc[0, h, :n], vc[0, h, :n] = k, v
+            acc.kv_write(0, h, 0, k, v)
+        for pos, rows in ((300, 1), (520, 8), (n, 1)):
+            x = synth.hidden_rows(rows, seed_offset=91 + pos)
+            acc.upload(2, x)
+            _say(f"case cooperative {path} pos={pos} rows={rows}")
+            rc, _ = acc.task(18, 0, rows, pos, 2, 0)
+            assert rc == 0
+            got = acc.download(0, rows)
+            code, want, _ = om.task((kc, vc), 18, 0, x, pos)
+            assert code == 0
+            assert first_mismatch(got, want) is None, (pos, rows)
+        for h in range(spec.kv_heads):
+            k, v = acc.kv_read(0, h, 0, n + 1)
+            assert first_mismatch(k, kc[0, h, :n + 1]) is None
+            assert first_mismatch(v, vc[0, h, :n + 1]) is None
