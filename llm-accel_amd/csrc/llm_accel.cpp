@@ -145,6 +145,13 @@ struct llm_ctx {
     // ones run faster with a workgroup per query head and tile);
     // LLM_ACCEL_GQA_MIN_TILES overrides it
     uint32_t gqa_min_tiles = 64;
+    // blocks of kMfMinRows or more rows take the GQA path from 5 tiles: the
+    // one-launch per-head tile grid (rows x heads x tiles workgroups) no
+    // longer fits the device there and the two-launch pair is slower
+    // (configs[4] prompt: 58.8 -> 57.6 us per 8-row block and layer); one
+    // or two rows keep the per-head tile path below 64 tiles (decode at
+    // ~1.1k positions: 42.2 against 45.8 us per forward)
+    uint32_t gqa_min_tiles_block = 5;
     // the tile path (5-64 tiles) in one launch when the grid fits on the
     // device at once; LLM_ACCEL_TILE_FUSED=0 keeps its two launches
     bool tile_fused = true;
@@ -641,7 +648,8 @@ int enqueue_attention_sublayer(llm_ctx* c, uint32_t layer, uint32_t R,
     at.out = c->attn;
     at.ldo = c->Hp;
     at.chunk_tiles = c->chunk_tiles;
-    at.use_gqa = c->gqa && (uint32_t)cdiv(pos + R, llm::kTile) >= c->gqa_min_tiles ? 1u : 0u;
+    const uint32_t gqa_from = R >= llm::kMfMinRows ? c->gqa_min_tiles_block : c->gqa_min_tiles;
+    at.use_gqa = c->gqa && (uint32_t)cdiv(pos + R, llm::kTile) >= gqa_from ? 1u : 0u;
     at.max_tiles = c->tiles;
     at.tile_fused = c->tile_fused ? 1u : 0u;
     at.s_tmax32 = c->s_tmax32;
@@ -981,7 +989,7 @@ int llm_ctx_create(const llm_shape_t* shape, int device, uint32_t num_pairs,
     if (const char* e = std::getenv("LLM_ACCEL_TILE_FUSED"))
         c->tile_fused = std::strcmp(e, "0") != 0;
     if (const char* e = std::getenv("LLM_ACCEL_GQA_MIN_TILES"))
-        c->gqa_min_tiles = (uint32_t)std::strtoul(e, nullptr, 10);
+        c->gqa_min_tiles = c->gqa_min_tiles_block = (uint32_t)std::strtoul(e, nullptr, 10);
     if (const char* e = std::getenv("LLM_ACCEL_GQA_FUSED"))
         c->gqa_fused = std::strcmp(e, "0") != 0;
     if (const char* e = std::getenv("LLM_ACCEL_GQA_SCAN_FUSED"))

@@ -230,8 +230,12 @@ def test_context_sweep_decode_forward(n):
         assert first_mismatch(kv_got[h][1], vc[0, h, n:n + 1]) is None
 
 
-def test_split_attention_p8_block_late_position():
-    # 8 rows at positions 500..507: 8-9 tiles per row, split over workgroups.
+@pytest.mark.parametrize("gqa", ["1", "0"])
+def test_split_attention_p8_block_late_position(monkeypatch, gqa):
+    # 8 rows at positions 500..507: 8-9 tiles per row, split over workgroups
+    # (blocks of 3+ rows take the GQA path from 5 tiles; LLM_ACCEL_GQA=0
+    # the per-head tile path)
+    monkeypatch.setenv("LLM_ACCEL_GQA", gqa)
     import llm_accel
     spec = workloads.CONFIG_A
     n = 500
@@ -450,6 +454,16 @@ def tile_two_launches(monkeypatch):
 @pytest.mark.parametrize("cfg,n,rows", [("B", 1024, 1), ("A", 382, 1), ("B", 255, 2),
                                          ("A", 4030, 2)])
 def test_tile_path_two_launches(tile_two_launches, cfg, n, rows):
+    test_block_across_tile_boundary_late_context(cfg, n, rows)
+
+
+@pytest.mark.parametrize("cfg,n,rows", [("B", 1020, 8), ("A", 317, 5), ("B", 252, 8),
+                                         ("A", 700, 3)])
+def test_tile_path_multirow_blocks(monkeypatch, cfg, n, rows):
+    # blocks of 3+ rows take the GQA path from 5 tiles by default; with it
+    # off they run the per-head tile path (one launch when the grid fits,
+    # else two)
+    monkeypatch.setenv("LLM_ACCEL_GQA", "0")
     test_block_across_tile_boundary_late_context(cfg, n, rows)
 
 
