@@ -64,6 +64,9 @@ struct ProjArgs {
     // whose weights all lie in [-2048, 2047]; null when absent.
     const uint8_t* p0;
     const uint8_t* p1;
+    // The matrix-core path reads p0 (and p1) instead of the byte planes
+    // when set and present (proj_mfma12_kernel).
+    uint32_t mf_p12;
 };
 // Bytes of the p12 copy per 4-row block and k-step.
 constexpr uint32_t kP12Step = 768;
@@ -108,6 +111,10 @@ struct MfSplit {
     uint32_t ks, parts;
 };
 MfSplit mf_split(uint32_t nc, uint32_t kq);
+// The same for the matrix-core kernel over the 12-bit copy, in k-steps,
+// and whether a launch of the matrix-core path takes that kernel.
+MfSplit mf12_split(uint32_t nc, uint32_t steps);
+bool proj_mfma_reads_p12(const ProjArgs& a, int epi);
 // int32 words of partial sums per (chunk, part) record.
 constexpr uint32_t mf_part_words(uint32_t nm) { return nm * 2 * 256 + 32; }
 bool proj_uses_mfma(const ProjArgs& a, int epi);

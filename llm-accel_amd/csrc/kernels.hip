@@ -45,6 +45,24 @@
 #ifndef LLM_MF_PD2
 #define LLM_MF_PD2 2        // the same for gate|up (two matrices)
 #endif
+#ifndef LLM_P12_MAX_ROWS
+#define LLM_P12_MAX_ROWS 1  // 12-bit VALU kernel: blocks of at most this many rows (1 or 2)
+#endif
+#ifndef LLM_MF12_KS
+#define LLM_MF12_KS 8       // 12-bit matrix-core kernel: wavefronts per workgroup
+#endif
+#ifndef LLM_MF12_MIN_STEPS
+#define LLM_MF12_MIN_STEPS 4  // 12-bit matrix-core kernel: fewer wavefronts below this many steps each
+#endif
+#ifndef LLM_MF12_WG_TARGET
+#define LLM_MF12_WG_TARGET 128  // 12-bit matrix-core kernel: split K below this many workgroups
+#endif
+#ifndef LLM_MF12_PD1
+#define LLM_MF12_PD1 2      // 12-bit matrix-core kernel: k-steps of loads in flight, one matrix
+#endif
+#ifndef LLM_MF12_PD2
+#define LLM_MF12_PD2 1      // the same for gate|up
+#endif
 
 namespace llm {
 
@@ -547,6 +565,21 @@ __device__ __forceinline__ void mf_compute(const ProjArgs& a, const MfChunk<NM, 
     }
 }
 
+// Eight 4-bit high parts h of one p12 nibble word (column 2m at bits 4m,
+// column 2m + 1 at bits 16 + 4m) as the signed bytes h - 8, column e in
+// byte e of the pair: w + 2048 = 256 h + l makes h - 8 = w >> 8, the byte
+// planes' high byte.
+__device__ __forceinline__ uint2 p12_high_bytes(uint32_t w) {
+    const uint32_t x = w & 0x0F0F0F0Fu;         // columns 0 4 1 5
+    const uint32_t y = (w >> 4) & 0x0F0F0F0Fu;  // columns 2 6 3 7
+    uint32_t c0 = __builtin_amdgcn_perm(y, x, 0x06040200u);  // columns 0 1 2 3
+    uint32_t c1 = __builtin_amdgcn_perm(y, x, 0x07050301u);  // columns 4 5 6 7
+    // h - 8 in every byte without borrows between bytes: (h + 128 - 8) ^ 128
+    c0 = ((c0 | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
+    c1 = ((c1 | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
+    return make_uint2(c0, c1);
+}
+
 // Exact sum (int64) of output (r, n) from its four product sums, the weight
 // sums (m0 = sum a, m1 = sum b), the activation sums and K.
 __device__ __forceinline__ int64_t mf_total(int64_t ac, int64_t ad, int64_t bc, int64_t bd,
@@ -556,63 +589,46 @@ __device__ __forceinline__ int64_t mf_total(int64_t ac, int64_t ad, int64_t bc, 
            32768 * sc + 128 * sd + 16384 * k64;
 }
 
-template <int NM, int KS, int QM, int PD, int EPI>
-__global__ __launch_bounds__(64 * KS) void proj_mfma_kernel(ProjArgs a, uint32_t parts) {
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t c = blockIdx.x / parts, p = blockIdx.x % parts, KQ = a.kq;
-    const uint32_t pq0 = p * KQ / parts, pq1 = (p + 1) * KQ / parts;
-    const uint32_t q0 = pq0 + wave * (pq1 - pq0) / KS;
-    const uint32_t q1 = pq0 + (wave + 1) * (pq1 - pq0) / KS;
-    const uint32_t n = q1 - q0;  // <= QM (the launcher's choice)
-    const uint32_t i = lane & 15, g = lane >> 4;
-    const bool hi_plane = i < 8;
-    // every activation buffer holds 8 rows: row i & 7 is always in bounds
-    const int16_t* xp = a.x + (size_t)(i & 7) * a.ldx + 16 * g;
-    const int16_t* gp = EPI == EPI_STORE_NORM_IN ? a.in_gamma + 16 * g : nullptr;
-    // epilogue operands of this thread's first output t = threadIdx.x
+// Epilogue operands of a matrix-core workgroup's first outputs (thread t:
+// row t / 16, output 16c + t % 16), fetched when the kernel starts.
+template <int NM, int EPI>
+struct MfEpi {
+    EpiIn ei;
+    int32_t ems[NM][2];
+    int16_t fill;
+};
+template <int NM, int EPI>
+__device__ __forceinline__ MfEpi<NM, EPI> mf_epi_fetch(const ProjArgs& a, uint32_t c) {
     const uint32_t et = threadIdx.x, er = et >> 4, en = c * kMfRows + (et & 15);
-    EpiIn ei{0, 0, 0};
-    int32_t ems[NM][2] = {};
-    int16_t fill = 0;
+    MfEpi<NM, EPI> e{};
     if (et < 256 && en < a.n) {
         if (er < a.rows) {
-            ei = epi_fetch<EPI>(a, er, en);
+            e.ei = epi_fetch<EPI>(a, er, en);
 #pragma unroll
             for (int m = 0; m < NM; m++) {
                 const int32_t* ms = m == 0 ? a.ms0 : a.ms1;
-                ems[m][0] = ms[2 * en];
-                ems[m][1] = ms[2 * en + 1];
+                e.ems[m][0] = ms[2 * en];
+                e.ems[m][1] = ms[2 * en + 1];
             }
         } else if (EPI == EPI_RESID && a.final_out && er < 8) {
-            fill = a.res[(size_t)er * a.ldr + en];
+            e.fill = a.res[(size_t)er * a.ldr + en];
         }
     }
-    const int8_t* bp[NM];
-    bp[0] = a.mf0 + (size_t)c * KQ * kMfRecord + lane * 16;
-    if (NM == 2) bp[NM - 1] = a.mf1 + (size_t)c * KQ * kMfRecord + lane * 16;
-    v4i c1[NM], c2[NM];
-#pragma unroll
-    for (int m = 0; m < NM; m++) c1[m] = c2[m] = v4i{0, 0, 0, 0};
-    int32_t rs = 0;
-    // Chunk u of this wavefront is q0 + u; loads past the last chunk
-    // repeat it (in bounds, its products add zero).  A wavefront with no
-    // chunk reads chunk pq0 and uses none.
-    auto chunk_q = [&](uint32_t u) -> uint32_t {
-        return n == 0 ? pq0 : q0 + (u < n ? u : n - 1);
-    };
-    MfChunk<NM, EPI> ring[PD];
-#pragma unroll
-    for (int u = 0; u < PD; u++) mf_load<NM, EPI>(a, bp, xp, gp, chunk_q(u), ring[u]);
-#pragma unroll
-    for (int u = 0; u < QM; u++) {
-        const MfChunk<NM, EPI> cur = ring[u % PD];
-        if (u + PD < QM) mf_load<NM, EPI>(a, bp, xp, gp, chunk_q(u + PD), ring[u % PD]);
-        mf_compute<NM, EPI>(a, cur, hi_plane, (uint32_t)u < n, c1, c2, rs);
-    }
-    // C lane l holds rows 4 (l / 16) + s, column l % 16.
-    __shared__ v4i red[KS][NM][2][64];
-    __shared__ int32_t rsum[KS][64];
-    __shared__ uint32_t last;
+    return e;
+}
+
+// The end of a matrix-core workgroup: product sums of the wavefronts
+// reduced in LDS (red, rsum), split-K partials handed to the last
+// workgroup of the chunk to arrive, then the exact sums and the epilogue.
+// C lane l holds rows 4 (l / 16) + s, column l % 16.
+template <int NM, int KS, int EPI>
+__device__ __forceinline__ void mf_finish(const ProjArgs& a, uint32_t c, uint32_t p,
+                                          uint32_t parts, const v4i* c1, const v4i* c2,
+                                          int32_t rs, const MfEpi<NM, EPI>& fe,
+                                          v4i (*red)[NM][2][64], int32_t (*rsum)[64],
+                                          uint32_t* last) {
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t et = threadIdx.x;
 #pragma unroll
     for (int m = 0; m < NM; m++) {
         red[wave][m][0][lane] = c1[m];
@@ -649,9 +665,9 @@ __global__ __launch_bounds__(64 * KS) void proj_mfma_kernel(ProjArgs a, uint32_t
                     st_coherent(&part[(m * 2 + ty) * 256 + t], wsum(m, ty, t >> 4, t & 15));
             if (t < 16) st_coherent(&part[NM * 2 * 256 + t], rsum_row(t));
         }
-        if (!arrive_last(&a.mf_count[c], parts, &last)) return;
+        if (!arrive_last(&a.mf_count[c], parts, last)) return;
     }
-    const int64_t k64 = (int64_t)KQ * kMfCols;
+    const int64_t k64 = (int64_t)a.kq * kMfCols;
     for (uint32_t t = threadIdx.x; t < 256; t += 64 * KS) {
         const uint32_t r = t >> 4, j = t & 15, nn = c * kMfRows + j;
         if (nn >= a.n) continue;
@@ -686,21 +702,202 @@ __global__ __launch_bounds__(64 * KS) void proj_mfma_kernel(ProjArgs a, uint32_t
             // later outputs of this thread (fewer than 4 wavefronts) fetch
             // their operands here
             const bool first = t == et;
-            EpiIn e = first ? ei : epi_fetch<EPI>(a, r, nn);
+            EpiIn e = first ? fe.ei : epi_fetch<EPI>(a, r, nn);
             int64_t tot[NM];
 #pragma unroll
             for (int m = 0; m < NM; m++) {
                 const int32_t* ms = m == 0 ? a.ms0 : a.ms1;
-                const int32_t m0 = first ? ems[m][0] : ms[2 * nn];
-                const int32_t m1 = first ? ems[m][1] : ms[2 * nn + 1];
+                const int32_t m0 = first ? fe.ems[m][0] : ms[2 * nn];
+                const int32_t m1 = first ? fe.ems[m][1] : ms[2 * nn + 1];
                 tot[m] = mf_total(s[m][0], s[m][1], s[m][2], s[m][3], m0, m1, sc, sd, k64);
             }
             proj_out<EPI>(a, r, nn, tot[0], tot[NM - 1], e, a.exp8);
         } else if (EPI == EPI_RESID && a.final_out && r < 8) {
             a.final_out[(size_t)r * a.ldn + nn] =
-                t == et ? fill : a.res[(size_t)r * a.ldr + nn];
+                t == et ? fe.fill : a.res[(size_t)r * a.ldr + nn];
         }
     }
+}
+
+template <int NM, int KS, int QM, int PD, int EPI>
+__global__ __launch_bounds__(64 * KS) void proj_mfma_kernel(ProjArgs a, uint32_t parts) {
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t c = blockIdx.x / parts, p = blockIdx.x % parts, KQ = a.kq;
+    const uint32_t pq0 = p * KQ / parts, pq1 = (p + 1) * KQ / parts;
+    const uint32_t q0 = pq0 + wave * (pq1 - pq0) / KS;
+    const uint32_t q1 = pq0 + (wave + 1) * (pq1 - pq0) / KS;
+    const uint32_t n = q1 - q0;  // <= QM (the launcher's choice)
+    const uint32_t i = lane & 15, g = lane >> 4;
+    const bool hi_plane = i < 8;
+    // every activation buffer holds 8 rows: row i & 7 is always in bounds
+    const int16_t* xp = a.x + (size_t)(i & 7) * a.ldx + 16 * g;
+    const int16_t* gp = EPI == EPI_STORE_NORM_IN ? a.in_gamma + 16 * g : nullptr;
+    const MfEpi<NM, EPI> fe = mf_epi_fetch<NM, EPI>(a, c);
+    const int8_t* bp[NM];
+    bp[0] = a.mf0 + (size_t)c * KQ * kMfRecord + lane * 16;
+    if (NM == 2) bp[NM - 1] = a.mf1 + (size_t)c * KQ * kMfRecord + lane * 16;
+    v4i c1[NM], c2[NM];
+#pragma unroll
+    for (int m = 0; m < NM; m++) c1[m] = c2[m] = v4i{0, 0, 0, 0};
+    int32_t rs = 0;
+    // Chunk u of this wavefront is q0 + u; loads past the last chunk
+    // repeat it (in bounds, its products add zero).  A wavefront with no
+    // chunk reads chunk pq0 and uses none.
+    auto chunk_q = [&](uint32_t u) -> uint32_t {
+        return n == 0 ? pq0 : q0 + (u < n ? u : n - 1);
+    };
+    MfChunk<NM, EPI> ring[PD];
+#pragma unroll
+    for (int u = 0; u < PD; u++) mf_load<NM, EPI>(a, bp, xp, gp, chunk_q(u), ring[u]);
+#pragma unroll
+    for (int u = 0; u < QM; u++) {
+        const MfChunk<NM, EPI> cur = ring[u % PD];
+        if (u + PD < QM) mf_load<NM, EPI>(a, bp, xp, gp, chunk_q(u + PD), ring[u % PD]);
+        mf_compute<NM, EPI>(a, cur, hi_plane, (uint32_t)u < n, c1, c2, rs);
+    }
+    __shared__ v4i red[KS][NM][2][64];
+    __shared__ int32_t rsum[KS][64];
+    __shared__ uint32_t last;
+    mf_finish<NM, KS, EPI>(a, c, p, parts, c1, c2, rs, fe, red, rsum, &last);
+}
+
+// ---------------------------------------------------------------------
+// The matrix-core kernel over the 12-bit copies (p12 layout, see
+// proj_p12_kernel), for matrices whose weights all fit 12 bits: 3/4 of
+// the byte-plane bytes.  w + 2048 = 256 h + l makes h - 8 the byte planes'
+// high byte (w >> 8) and l ^ 128 their biased low byte, so the products,
+// weight sums and exact totals are the byte-plane kernel's.  The operand
+// of lane l (output 16c + l % 16, inputs 64q + 16 (l / 16) .. + 15) lies in
+// 64-byte pieces of four block records, so each wavefront loads whole
+// 768-byte records of its four blocks instead -- 48 contiguous bytes per
+// lane and step, lanes 16b .. 16b + 15 on block 4c + b -- writes them to
+// its own LDS slice and reads the operands back from there (a wavefront's
+// LDS operations complete in order: no barrier).  Work is split in whole
+// 128-column steps (two K chunks); a half past kq carries zero activations.
+// ---------------------------------------------------------------------
+constexpr uint32_t kP12LoRow = 144;  // 128 low bytes of a block row + 16 of padding
+constexpr uint32_t kP12NbRow = 80;   // 64 nibble-word bytes of a block row + 16
+template <int NM>
+struct __attribute__((aligned(16))) P12Stage {
+    uint8_t lo[NM][4][4][kP12LoRow];  // [matrix][block][row][bytes]
+    uint8_t nb[NM][4][4][kP12NbRow];
+};
+
+template <int NM, int EPI>
+struct P12Step {
+    v4i r[NM][3];         // record bytes 16 (lane % 16) + {0, 256, 512}
+    v4u x0[2], x1[2];     // activations of the step's two K chunks
+    v4u g0[2], g1[2];     // their gammas (EPI_STORE_NORM_IN)
+};
+
+template <int NM, int EPI>
+__device__ __forceinline__ void p12_step_load(const ProjArgs& a, const uint8_t* const* src,
+                                              const int16_t* xp, const int16_t* gp, uint32_t s,
+                                              P12Step<NM, EPI>& st) {
+#pragma unroll
+    for (int m = 0; m < NM; m++)
+#pragma unroll
+        for (int t = 0; t < 3; t++)
+            st.r[m][t] = *(const v4i*)(src[m] + (size_t)s * kP12Step + 256 * t);
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        // columns 128 s + 64 h + 16 (lane / 16) .. + 15 lie below the
+        // activations' padded width (a whole number of 128-column steps)
+        st.x0[h] = *(const v4u*)(xp + 128 * s + 64 * h);
+        st.x1[h] = *(const v4u*)(xp + 128 * s + 64 * h + 8);
+        if (EPI == EPI_STORE_NORM_IN) {
+            st.g0[h] = *(const v4u*)(gp + 128 * s + 64 * h);
+            st.g1[h] = *(const v4u*)(gp + 128 * s + 64 * h + 8);
+        }
+    }
+}
+
+template <int NM, int KS, int SM, int PDS, int EPI>
+__global__ __launch_bounds__(64 * KS) void proj_mfma12_kernel(ProjArgs a, uint32_t parts) {
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t c = blockIdx.x / parts, p = blockIdx.x % parts, S = a.steps, KQ = a.kq;
+    const uint32_t ps0 = p * S / parts, ps1 = (p + 1) * S / parts;
+    const uint32_t s0 = ps0 + wave * (ps1 - ps0) / KS;
+    const uint32_t s1 = ps0 + (wave + 1) * (ps1 - ps0) / KS;
+    const uint32_t n = s1 - s0;  // <= SM (the launcher's choice)
+    const uint32_t i = lane & 15, g = lane >> 4;
+    const bool hi_plane = i < 8;
+    const int16_t* xp = a.x + (size_t)(i & 7) * a.ldx + 16 * g;
+    const int16_t* gp = EPI == EPI_STORE_NORM_IN ? a.in_gamma + 16 * g : nullptr;
+    const MfEpi<NM, EPI> fe = mf_epi_fetch<NM, EPI>(a, c);
+    // load lanes: block 4c + lane / 16, clamped to the copy's last block
+    // (rows past n reach only outputs that are never written)
+    const uint32_t nblk = (a.n + kBlockRows - 1) / kBlockRows;
+    const uint32_t lb = min(4 * c + (lane >> 4), nblk - 1);
+    const uint8_t* src[NM];
+    src[0] = a.p0 + (size_t)lb * S * kP12Step + 16 * (lane & 15);
+    if (NM == 2) src[NM - 1] = a.p1 + (size_t)lb * S * kP12Step + 16 * (lane & 15);
+    __shared__ union {
+        P12Stage<NM> st[KS];
+        struct {
+            v4i red[KS][NM][2][64];
+            int32_t rsum[KS][64];
+        } fin;
+    } sm;
+    __shared__ uint32_t last;
+    P12Stage<NM>& my = sm.st[wave];
+    // where this lane's record bytes go: +0 low bytes of row (lane%16)/8,
+    // +256 of row 2 + (lane%16)/8, both at column 16 ((lane%16) % 8);
+    // +512 nibble words 4 (lane%16) .. + 3, row (lane%16)/4
+    const uint32_t o = lane & 15, bw = lane >> 4;
+    // where lane's operand is read: block i / 4, row i % 4
+    const uint32_t ob = i >> 2, orow = i & 3;
+    v4i c1[NM], c2[NM];
+#pragma unroll
+    for (int m = 0; m < NM; m++) c1[m] = c2[m] = v4i{0, 0, 0, 0};
+    int32_t rs = 0;
+    // Step u of this wavefront is s0 + u; loads past the last step repeat
+    // it (in bounds, its products add zero).  A wavefront with no step
+    // reads step ps0 and uses none.
+    auto step_s = [&](uint32_t u) -> uint32_t {
+        return n == 0 ? ps0 : s0 + (u < n ? u : n - 1);
+    };
+    P12Step<NM, EPI> ring[PDS];
+#pragma unroll
+    for (int u = 0; u < PDS; u++) p12_step_load<NM, EPI>(a, src, xp, gp, step_s(u), ring[u]);
+#pragma unroll
+    for (int u = 0; u < SM; u++) {
+        const P12Step<NM, EPI> cur = ring[u % PDS];
+        const uint32_t s = step_s(u);
+        if (u + PDS < SM) p12_step_load<NM, EPI>(a, src, xp, gp, step_s(u + PDS), ring[u % PDS]);
+#pragma unroll
+        for (int m = 0; m < NM; m++) {
+            *(v4i*)&my.lo[m][bw][o >> 3][16 * (o & 7)] = cur.r[m][0];
+            *(v4i*)&my.lo[m][bw][2 + (o >> 3)][16 * (o & 7)] = cur.r[m][1];
+            *(v4i*)&my.nb[m][bw][o >> 2][16 * (o & 3)] = cur.r[m][2];
+        }
+        // the reads below see other lanes' writes: the fences keep the
+        // compiler from moving LDS accesses across (no instruction)
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            MfChunk<NM, EPI> ch;
+#pragma unroll
+            for (int m = 0; m < NM; m++) {
+                const v4i lo = *(const v4i*)&my.lo[m][ob][orow][64 * h + 16 * g];
+                typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+                const v2u nw = *(const v2u*)&my.nb[m][ob][orow][32 * h + 8 * g];
+                const uint2 h0 = p12_high_bytes(nw.x), h1 = p12_high_bytes(nw.y);
+                ch.bh[m] = v4i{(int32_t)h0.x, (int32_t)h0.y, (int32_t)h1.x, (int32_t)h1.y};
+                ch.bl[m] = lo ^ v4i{(int32_t)0x80808080u, (int32_t)0x80808080u,
+                                    (int32_t)0x80808080u, (int32_t)0x80808080u};
+            }
+            ch.x0 = cur.x0[h];
+            ch.x1 = cur.x1[h];
+            ch.g0 = cur.g0[h];
+            ch.g1 = cur.g1[h];
+            // a half past the matrix's K chunks (odd kq) adds nothing
+            mf_compute<NM, EPI>(a, ch, hi_plane, (uint32_t)u < n && 2 * s + h < KQ, c1, c2, rs);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    }
+    __syncthreads();  // every wavefront's staging reads are done
+    mf_finish<NM, KS, EPI>(a, c, p, parts, c1, c2, rs, fe, sm.fin.red, sm.fin.rsum, &last);
 }
 
 // ---------------------------------------------------------------------
@@ -892,7 +1089,9 @@ static hipError_t launch_p12_rt(const ProjArgs& a, uint32_t blocks, hipStream_t 
 template <int EPI>
 static hipError_t launch_proj_epi(const ProjArgs& a, int L, uint32_t blocks,
                                   hipStream_t st) {
-    if (proj_uses_p12(a)) return launch_p12_rt<1, EPI>(a, blocks, st);
+    if (proj_uses_p12(a))
+        return a.rows <= 1 ? launch_p12_rt<1, EPI>(a, blocks, st)
+                           : launch_p12_rt<2, EPI>(a, blocks, st);
     if (a.rows <= 1) return launch_proj_rt<1, EPI>(a, L, blocks, st);
     if (a.rows <= 2) return launch_proj_rt<2, EPI>(a, L, blocks, st);
     if (a.rows <= 4) return launch_proj_rt<4, EPI>(a, L, blocks, st);
@@ -941,8 +1140,56 @@ static hipError_t launch_mfma_q(const ProjArgs& a, uint32_t parts, hipStream_t s
     return hipGetLastError();
 }
 
+// The 12-bit matrix-core kernel splits whole 128-column steps the same
+// way: wavefronts keep at least one step, at most LLM_MF_QMAX / 2; fewer
+// wavefronts per workgroup below 4 steps each (more workgroups resident:
+// measured faster for K = 2048, slower for K = 11008 with 4).
+MfSplit mf12_split(uint32_t nc, uint32_t steps) {
+    MfSplit s{LLM_MF12_KS, 1};
+    while (s.ks > 4 && steps < LLM_MF12_MIN_STEPS * s.ks) s.ks /= 2;
+    while (nc * s.parts < LLM_MF12_WG_TARGET && steps / (s.parts * 2) >= s.ks) s.parts *= 2;
+    while (mf_chunks_per_wave(steps, s.parts, s.ks) > LLM_MF_QMAX / 2) s.parts *= 2;
+    return s;
+}
+
+template <int NM, int KS, int SM, int EPI>
+static void launch_mfma12_k(const ProjArgs& a, uint32_t parts, hipStream_t st) {
+    // normalising on load holds the gammas too: one step in flight
+    constexpr int PD0 = NM == 2 ? LLM_MF12_PD2 : EPI == EPI_STORE_NORM_IN ? 1 : LLM_MF12_PD1;
+    constexpr int PD = PD0 < SM ? PD0 : SM;
+    proj_mfma12_kernel<NM, KS, SM, PD, EPI><<<a.nc * parts, 64 * KS, 0, st>>>(a, parts);
+}
+
+template <int NM, int KS, int EPI>
+static hipError_t launch_mfma12_s(const ProjArgs& a, uint32_t parts, hipStream_t st) {
+    const uint32_t sm = mf_chunks_per_wave(a.steps, parts, KS);
+    if (sm <= 1)
+        launch_mfma12_k<NM, KS, 1, EPI>(a, parts, st);
+    else if (sm <= 2)
+        launch_mfma12_k<NM, KS, 2, EPI>(a, parts, st);
+    else if (sm <= 3)
+        launch_mfma12_k<NM, KS, 3, EPI>(a, parts, st);
+    else if (sm <= 4)
+        launch_mfma12_k<NM, KS, 4, EPI>(a, parts, st);
+    else if (sm <= 6)
+        launch_mfma12_k<NM, KS, 6, EPI>(a, parts, st);
+    else
+        return hipErrorInvalidConfiguration;  // mf12_split keeps sm <= LLM_MF_QMAX / 2 <= 6
+    return hipGetLastError();
+}
+
+bool proj_mfma_reads_p12(const ProjArgs& a, int epi) {
+    return a.mf_p12 && a.p0 && (epi != EPI_SILU || a.p1);
+}
+
 template <int NM, int EPI>
 static hipError_t launch_mfma_epi(const ProjArgs& a, hipStream_t st) {
+    if (proj_mfma_reads_p12(a, EPI)) {
+        const MfSplit sp = mf12_split(a.nc, a.steps);
+        if (sp.ks >= 16) return launch_mfma12_s<NM, 16, EPI>(a, sp.parts, st);
+        if (sp.ks == 8) return launch_mfma12_s<NM, 8, EPI>(a, sp.parts, st);
+        return launch_mfma12_s<NM, 4, EPI>(a, sp.parts, st);
+    }
     const MfSplit sp = mf_split(a.nc, a.kq);
     if (sp.ks >= 16) return launch_mfma_q<NM, 16, EPI>(a, sp.parts, st);
     if (sp.ks == 8) return launch_mfma_q<NM, 8, EPI>(a, sp.parts, st);
@@ -959,7 +1206,7 @@ bool proj_uses_p12(const ProjArgs& a) {
     // wavefront with the launcher's wavefronts per block
     const uint32_t w = a.w1 ? LLM_PROJ_WPB_SILU
                      : (a.steps >= LLM_PROJ_LONG_STEPS ? 16u : (uint32_t)LLM_PROJ_WPB);
-    return a.rows == 1 && a.p0 && (a.w1 == nullptr || a.p1) && a.steps <= 8 * w;
+    return a.rows <= LLM_P12_MAX_ROWS && a.p0 && (a.w1 == nullptr || a.p1) && a.steps <= 8 * w;
 }
 
 hipError_t launch_proj(const ProjArgs& a, int epi, int L, uint32_t blocks,

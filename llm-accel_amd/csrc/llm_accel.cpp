@@ -158,6 +158,9 @@ struct llm_ctx {
     // 12-bit copies of the weight matrices for single decode rows (weights
     // in [-2048, 2047]); LLM_ACCEL_P12=0 keeps the 16-bit copies only
     bool p12 = true;
+    // the matrix-core path reads the 12-bit copies where every matrix of a
+    // launch has one; LLM_ACCEL_MF12=0 keeps it on the byte planes
+    bool mf12 = true;
     int32_t* s_tmax32 = nullptr;       // tile maxima published in that launch
     int32_t* s_gmax32 = nullptr;       // GQA path: tagged tile maxima
     uint32_t gqa_epoch = 0;            // epoch of the last GQA launch
@@ -583,7 +586,8 @@ int check_layer_loaded(llm_ctx* c, uint32_t layer, bool attn, bool ffn) {
 }
 
 // Matrix-core copies of the matrix (and of the up matrix for gate|up).
-void set_mf(llm::ProjArgs& a, const Matrix& m, const Matrix* m2 = nullptr) {
+void set_mf(const llm_ctx* c, llm::ProjArgs& a, const Matrix& m, const Matrix* m2 = nullptr) {
+    a.mf_p12 = c->mf12;
     a.mf_part = m.ctx_part;
     a.mf_count = m.ctx_count;
     a.mf0 = m.mf;
@@ -622,7 +626,7 @@ int enqueue_attention_sublayer(llm_ctx* c, uint32_t layer, uint32_t R,
     a.ldo = c->Nqkv;
     a.n = mq.n;
     a.rows = R;
-    set_mf(a, mq);
+    set_mf(c, a, mq);
     if (mq.p12_ok) a.p0 = mq.p12;  // single rows outside the fused launch
     if (norm_in) {
         a.in_gamma = c->norms + (size_t)(2 * layer) * c->H;
@@ -697,7 +701,7 @@ int enqueue_attention_sublayer(llm_ctx* c, uint32_t layer, uint32_t R,
     o.ldr = c->Hp;
     o.n = mo.n;
     o.rows = R;
-    set_mf(o, mo);
+    set_mf(c, o, mo);
     if (mo.p12_ok) o.p0 = mo.p12;
     if (c->const_gain > 0) {  // FFN norm of this sublayer's output
         o.norm_out = c->xn_ffn;
@@ -776,7 +780,7 @@ int enqueue_ffn_sublayer(llm_ctx* c, uint32_t layer, uint32_t R, int in_pair,
     a.n = mg.n;
     a.rows = R;
     a.exp8 = c->exp8;
-    set_mf(a, mg, &mu);
+    set_mf(c, a, mg, &mu);
     if (mg.p12_ok && mu.p12_ok) {
         a.p0 = mg.p12;
         a.p1 = mu.p12;
@@ -798,7 +802,7 @@ int enqueue_ffn_sublayer(llm_ctx* c, uint32_t layer, uint32_t R, int in_pair,
     dn.ldr = c->Hp;
     dn.n = md.n;
     dn.rows = R;
-    set_mf(dn, md);
+    set_mf(c, dn, md);
     if (md.p12_ok) dn.p0 = md.p12;
     const bool next = c->const_gain > 0 && layer + 1 < c->L;
     if (c->const_gain > 0) {
@@ -879,6 +883,7 @@ int llm_ctx_create(const llm_shape_t* shape, int device, uint32_t num_pairs,
 
     // weights
     if (const char* e = std::getenv("LLM_ACCEL_P12")) c->p12 = std::strcmp(e, "0") != 0;
+    if (const char* e = std::getenv("LLM_ACCEL_MF12")) c->mf12 = std::strcmp(e, "0") != 0;
     c->mats.resize((size_t)c->L * M_COUNT);
     c->loaded.assign((size_t)c->L * 7, false);
     size_t total = 0;
@@ -1031,9 +1036,11 @@ int llm_ctx_create(const llm_shape_t* shape, int device, uint32_t num_pairs,
         size_t words = 0, chunks = 0;
         for (uint32_t m = 0; m < M_COUNT; m++) {
             const Matrix& mt = c->mat(0, m);
-            const llm::MfSplit sp = llm::mf_split(mt.nc, mt.kq);
+            // either kernel of the matrix-core path
+            const uint32_t parts = std::max(llm::mf_split(mt.nc, mt.kq).parts,
+                                            llm::mf12_split(mt.nc, mt.steps).parts);
             const uint32_t nm = (m == M_GATE || m == M_UP) ? 2 : 1;
-            words = std::max(words, (size_t)mt.nc * sp.parts * llm::mf_part_words(nm));
+            words = std::max(words, (size_t)mt.nc * parts * llm::mf_part_words(nm));
             chunks = std::max(chunks, (size_t)mt.nc);
         }
         if ((rc = dev_alloc(c, (void**)&c->mf_part, words * 4)) ||
@@ -1482,7 +1489,7 @@ int enqueue_op_projection(llm_ctx* c, uint32_t layer, uint32_t proj, uint32_t T,
     a.rows = T;
     // the matrix-core records cover 16 outputs each
     if (row0 % llm::kMfRows == 0) {
-        set_mf(a, m);
+        set_mf(c, a, m);
         if (a.mf0) {
             a.mf0 += (size_t)(row0 / llm::kMfRows) * m.kq * llm::kMfRecord;
             a.ms0 += (size_t)2 * row0;
@@ -1788,7 +1795,7 @@ int llm_bench_projection(llm_ctx_t* c, uint32_t kernel, uint32_t rows,
             const Matrix& m = c->mat(layer, M_QKV);
             a.w0 = m.d; a.steps = m.steps; a.x = c->xn_attn; a.ldx = c->Hp;
             a.out = c->qkv; a.ldo = c->Nqkv; a.n = m.n; L = m.L; blocks = m.n_pad / 4;
-            set_mf(a, m);
+            set_mf(c, a, m);
             if (m.p12_ok) a.p0 = m.p12;
         } else if (kernel == LLM_K_OPROJ || kernel == LLM_K_DOWN) {
             const Matrix& m = c->mat(layer, kernel == LLM_K_OPROJ ? M_O : M_DOWN);
@@ -1798,7 +1805,7 @@ int llm_bench_projection(llm_ctx_t* c, uint32_t kernel, uint32_t rows,
             // output into a buffer the launch does not read
             a.out = c->qkv; a.ldo = c->Nqkv; a.res = c->xn_ffn; a.ldr = c->Hp;
             a.n = m.n; L = m.L; blocks = m.n_pad / 4; epi = llm::EPI_RESID;
-            set_mf(a, m);
+            set_mf(c, a, m);
             if (m.p12_ok) a.p0 = m.p12;
         } else {
             const Matrix& g = c->mat(layer, M_GATE);
@@ -1807,7 +1814,7 @@ int llm_bench_projection(llm_ctx_t* c, uint32_t kernel, uint32_t rows,
             a.ldx = c->Hp; a.out = c->act; a.ldo = c->Ip; a.n = g.n;
             a.exp8 = c->exp8; L = std::min(g.L, u.L); blocks = g.n_pad / 4;
             epi = llm::EPI_SILU;
-            set_mf(a, g, &u);
+            set_mf(c, a, g, &u);
             if (g.p12_ok && u.p12_ok) {
                 a.p0 = g.p12;
                 a.p1 = u.p12;
