@@ -215,6 +215,7 @@ def request_loop(llm_accel, workloads, spec, layers, prompt_len, gen, emb, lm_he
         prompt = [int(t) for t in synth.tokens(prompt_len)]
         del synth
         a.load_lm_head(lm_head)
+        weight_bytes, wide_matrices = a.weight_bytes()
         setup_s = time.perf_counter() - t0
         for _ in range(warmup):
             a.generate(emb, prompt, 8, layers, gen)
@@ -268,6 +269,8 @@ def request_loop(llm_accel, workloads, spec, layers, prompt_len, gen, emb, lm_he
         "kv_migrations": med["kv_migrations"],
         "first_tokens": toks[:4],
         "setup_s": round(setup_s, 1),
+        "weight_image_gb": round(weight_bytes / 1e9, 3),
+        "weight_matrices_16bit": wide_matrices,
         "decode_kernels_in_request": kernels,
     }
 

@@ -290,6 +290,15 @@ int llm_kernel_stats(llm_ctx_t* ctx, uint32_t kernel, uint64_t* launches,
 int llm_bench_projection(llm_ctx_t* ctx, uint32_t kernel, uint32_t rows,
                          uint32_t layers, uint32_t iters, float* avg_us);
 
+/* Device memory held by the decoder-layer weights, all layouts together
+ * (16-bit tiles, byte planes, 12-bit copies, per-output byte sums), and
+ * the number of layer matrices (Q|K|V, O, gate, up, down per layer) held
+ * in 16 bits.  A matrix whose weights all lie in [-2048, 2047] is held in
+ * 12 bits only; one with any weight outside keeps the 16-bit tiles and
+ * byte planes.  No counterpart in the reference (its weights are one
+ * packed image in device DDR); for capacity planning. */
+int llm_weight_bytes(llm_ctx_t* ctx, uint64_t* bytes, uint32_t* wide_matrices);
+
 /* A plain device-to-device copy of `bytes` repeated `iters` times on the
  * context stream (calibration reference for HBM counters and achievable
  * bandwidth); *ms is the average duration of one copy. */

@@ -133,6 +133,8 @@ constexpr uint32_t kSyncWords = kSyncAbort + kSyncStride;
 // for can always be dispatched).
 bool sublayer_fused_ok(const SublayerArgs& s, uint32_t rows, int qkv_epi, int L_qkv, int L_o,
                        int capacity);
+// Whether the fused launch reads the two projections' 12-bit copies.
+bool sublayer_reads_p12(const SublayerArgs& s);
 // QKV and O workgroups of the fused launch for `blocks` 4-row blocks.
 uint32_t sublayer_qkv_workgroups(uint32_t blocks);
 uint32_t sublayer_o_workgroups(uint32_t blocks);

@@ -724,6 +724,9 @@ __global__ __launch_bounds__(D * 2) void attention_split_head_kernel(AttnArgs a)
 // line for all 640 QKV blocks measured several microseconds of
 // serialised atomics).
 // ---------------------------------------------------------------------
+#ifndef LLM_SUB_P12
+#define LLM_SUB_P12 1  // fused sublayer: 12-bit copies where both matrices have one
+#endif
 #ifndef LLM_SUB_QKV_NB
 #define LLM_SUB_QKV_NB 1
 #endif
@@ -734,7 +737,8 @@ constexpr uint32_t kSubQkvBlocks = LLM_SUB_QKV_NB;
 // workgroups of one block each, at the same measured time)
 constexpr uint32_t kSubOBlocks = 2;
 
-template <int D, int RT, int QEPI, int LW>
+// P12: both projections read their 12-bit copies (qkv.p0, o.p0).
+template <int D, int RT, int QEPI, int LW, bool P12 = false>
 __global__ __launch_bounds__(D * 2) void attention_sublayer_kernel(SublayerArgs s) {
     constexpr int WPB = D / 32, SPW = 4;
     constexpr uint32_t NBR = kSubQkvBlocks > kSubOBlocks ? kSubQkvBlocks : kSubOBlocks;
@@ -744,8 +748,8 @@ __global__ __launch_bounds__(D * 2) void attention_sublayer_kernel(SublayerArgs 
     uint32_t* const sync = s.sync;
     const uint32_t idx = blockIdx.x;
     if (idx < s.nq) {
-        proj_block<RT, QEPI, WPB, SPW, false, true, LW, kSubQkvBlocks>(s.qkv, idx, red,
-                                                                      [] { return true; });
+        proj_block<RT, QEPI, WPB, SPW, false, true, LW, kSubQkvBlocks, P12>(
+            s.qkv, idx, red, [] { return true; });
         arrive(sync + kSyncStride * (idx % kSyncQkvLines));
         return;
     }
@@ -764,7 +768,7 @@ __global__ __launch_bounds__(D * 2) void attention_sublayer_kernel(SublayerArgs 
         return;
     }
     const uint32_t b = idx - s.nq - s.na;
-    proj_block<RT, EPI_RESID, WPB, SPW, true, false, LW, kSubOBlocks>(s.o, b, red, [&] {
+    proj_block<RT, EPI_RESID, WPB, SPW, true, false, LW, kSubOBlocks, P12>(s.o, b, red, [&] {
         return wait_counts(
             sync + kSyncAttn + kSyncStride * (b % kSyncAttnLines), 0, 1,
             [&](uint32_t) { return s.attn_base + s.na; }, s.wait_limit, sync + kSyncAbort, s.host_abort, &flag);
@@ -1605,18 +1609,21 @@ hipError_t launch_attention(const AttnArgs& a, uint32_t rows, uint32_t kv_heads,
 }
 
 
-// The smallest residency over the widening variants of the launch.
+// The smallest residency over the widening and 12-bit variants of the
+// launch.
 template <int D, int RT, int QEPI>
 static int sublayer_capacity_of(int cus) {
-    int per_cu[3] = {0, 0, 0};
+    int per_cu[4] = {0, 0, 0, 0};
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
             &per_cu[0], attention_sublayer_kernel<D, RT, QEPI, 4>, 2 * D, 0) != hipSuccess ||
         hipOccupancyMaxActiveBlocksPerMultiprocessor(
             &per_cu[1], attention_sublayer_kernel<D, RT, QEPI, 1>, 2 * D, 0) != hipSuccess ||
         hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &per_cu[2], attention_sublayer_kernel<D, RT, QEPI, 0>, 2 * D, 0) != hipSuccess)
+            &per_cu[2], attention_sublayer_kernel<D, RT, QEPI, 0>, 2 * D, 0) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &per_cu[3], attention_sublayer_kernel<D, RT, QEPI, 4, true>, 2 * D, 0) != hipSuccess)
         return 0;
-    return std::min({per_cu[0], per_cu[1], per_cu[2]}) * cus;
+    return std::min({per_cu[0], per_cu[1], per_cu[2], per_cu[3]}) * cus;
 }
 
 template <int D, int RT>
@@ -1654,25 +1661,37 @@ bool sublayer_fused_ok(const SublayerArgs& s, uint32_t rows, int qkv_epi, int L_
     (void)L_qkv;
     (void)L_o;
     if (s.qkv.steps > 4 * wpb || s.o.steps > 4 * wpb) return false;
+    // both projections from their 12-bit copies, or both from the 16-bit
+    if (!(sublayer_reads_p12(s) || (s.qkv.w0 && s.o.w0))) return false;
     if (!s.sync || !s.host_abort) return false;
     return (int64_t)s.na + s.no < capacity;
 }
 
-template <int D, int RT, int LW>
+template <int D, int RT, int LW, bool P12 = false>
 static void launch_sub_l(const SublayerArgs& s, int qkv_epi, hipStream_t st) {
     const uint32_t grid = s.nq + s.na + s.no;
     if (qkv_epi == EPI_STORE_NORM_IN)
-        attention_sublayer_kernel<D, RT, EPI_STORE_NORM_IN, LW><<<grid, 2 * D, 0, st>>>(s);
+        attention_sublayer_kernel<D, RT, EPI_STORE_NORM_IN, LW, P12><<<grid, 2 * D, 0, st>>>(s);
     else
-        attention_sublayer_kernel<D, RT, EPI_STORE, LW><<<grid, 2 * D, 0, st>>>(s);
+        attention_sublayer_kernel<D, RT, EPI_STORE, LW, P12><<<grid, 2 * D, 0, st>>>(s);
+}
+
+bool sublayer_reads_p12(const SublayerArgs& s) {
+#if LLM_SUB_P12
+    return s.qkv.p0 && s.o.p0;
+#else
+    return !(s.qkv.w0 && s.o.w0) && s.qkv.p0 && s.o.p0;
+#endif
 }
 
 // The int32 sums of the QKV and O roles (up to 4 k-steps per wavefront)
 // widen once when both matrices' widening intervals reach 4, after every
-// step when they are at least 1, and every product otherwise.
+// step when they are at least 1, and every product otherwise; from the
+// 12-bit copies they never need to.
 template <int D, int RT>
 static void launch_sub(const SublayerArgs& s, int qkv_epi, int L, hipStream_t st) {
-    if (L >= 4) launch_sub_l<D, RT, 4>(s, qkv_epi, st);
+    if (sublayer_reads_p12(s)) launch_sub_l<D, RT, 4, true>(s, qkv_epi, st);
+    else if (L >= 4) launch_sub_l<D, RT, 4>(s, qkv_epi, st);
     else if (L >= 1) launch_sub_l<D, RT, 1>(s, qkv_epi, st);
     else launch_sub_l<D, RT, 0>(s, qkv_epi, st);
 }

@@ -70,6 +70,8 @@ struct ProjArgs {
 };
 // Bytes of the p12 copy per 4-row block and k-step.
 constexpr uint32_t kP12Step = 768;
+// Sets every weight of a p12 copy of `records` records to 0.
+hipError_t launch_p12_zero(uint8_t* p, size_t records, hipStream_t st);
 
 // Matrix-core layout: record (c, q) of 2048 bytes holds outputs 16c..16c+15
 // and inputs 64q..64q+63: bytes [0, 1024) the high bytes w >> 8, bytes
@@ -118,9 +120,10 @@ bool proj_mfma_reads_p12(const ProjArgs& a, int epi);
 // int32 words of partial sums per (chunk, part) record.
 constexpr uint32_t mf_part_words(uint32_t nm) { return nm * 2 * 256 + 32; }
 bool proj_uses_mfma(const ProjArgs& a, int epi);
-// Single rows read the p12 copy when every matrix of the launch has one
-// (and a wavefront's share of K fits the kernel).
-bool proj_uses_p12(const ProjArgs& a);
+// Blocks of one or two rows read the p12 copy when every matrix of the
+// launch has one and K is at most kP12MaxSteps k-steps.
+constexpr uint32_t kP12MaxSteps = 128;
+bool proj_uses_p12(const ProjArgs& a, int epi);
 hipError_t launch_proj(const ProjArgs& a, int epi, int L, uint32_t blocks,
                        hipStream_t st);
 // RMSNorm of `rows` rows; const_gain > 0 selects the elementwise kernel

@@ -46,7 +46,7 @@
 #define LLM_MF_PD2 2        // the same for gate|up (two matrices)
 #endif
 #ifndef LLM_P12_MAX_ROWS
-#define LLM_P12_MAX_ROWS 1  // 12-bit VALU kernel: blocks of at most this many rows (1 or 2)
+#define LLM_P12_MAX_ROWS 2  // 12-bit VALU kernel: blocks of at most this many rows (1 or 2)
 #endif
 #ifndef LLM_MF12_KS
 #define LLM_MF12_KS 8       // 12-bit matrix-core kernel: wavefronts per workgroup
@@ -1061,10 +1061,11 @@ static hipError_t launch_proj_rt(const ProjArgs& a, int L, uint32_t blocks,
     return launch_proj_w<RT, EPI, LLM_PROJ_WPB>(a, L, blocks, st);
 }
 
-// The p12 kernel (one row): gate|up with 8 wavefronts per block, long
-// reductions (the down projection) with 16 and the others with 4, as the
-// 16-bit kernel; every wavefront's steps loaded at once; proj_uses_p12
-// bounds the steps per wavefront by 8.
+// The p12 kernel (one or two rows): gate|up with 8 wavefronts per block,
+// long reductions (the down projection) with 16 and the others with 4, as
+// the 16-bit kernel, and 16 wherever fewer would take more than 8 k-steps
+// each; every wavefront's steps loaded at once (proj_uses_p12 bounds the
+// steps by 16 x 8).
 template <int RT, int EPI, int W>
 static hipError_t launch_p12_w(const ProjArgs& a, uint32_t blocks, hipStream_t st) {
     const uint32_t spw = (a.steps + W - 1) / W;
@@ -1079,9 +1080,11 @@ static hipError_t launch_p12_w(const ProjArgs& a, uint32_t blocks, hipStream_t s
 template <int RT, int EPI>
 static hipError_t launch_p12_rt(const ProjArgs& a, uint32_t blocks, hipStream_t st) {
     if constexpr (EPI == EPI_SILU) {
+        if (a.steps > 8 * LLM_PROJ_WPB_SILU) return launch_p12_w<RT, EPI, 16>(a, blocks, st);
         return launch_p12_w<RT, EPI, LLM_PROJ_WPB_SILU>(a, blocks, st);
     } else {
-        if (a.steps >= LLM_PROJ_LONG_STEPS) return launch_p12_w<RT, EPI, 16>(a, blocks, st);
+        if (a.steps >= LLM_PROJ_LONG_STEPS || a.steps > 8 * LLM_PROJ_WPB)
+            return launch_p12_w<RT, EPI, 16>(a, blocks, st);
         return launch_p12_w<RT, EPI, LLM_PROJ_WPB>(a, blocks, st);
     }
 }
@@ -1089,9 +1092,11 @@ static hipError_t launch_p12_rt(const ProjArgs& a, uint32_t blocks, hipStream_t 
 template <int EPI>
 static hipError_t launch_proj_epi(const ProjArgs& a, int L, uint32_t blocks,
                                   hipStream_t st) {
-    if (proj_uses_p12(a))
+    if (proj_uses_p12(a, EPI))
         return a.rows <= 1 ? launch_p12_rt<1, EPI>(a, blocks, st)
                            : launch_p12_rt<2, EPI>(a, blocks, st);
+    // the 16-bit copy (absent for matrices held in 12 bits only)
+    if (!a.w0 || (EPI == EPI_SILU && !a.w1)) return hipErrorInvalidValue;
     if (a.rows <= 1) return launch_proj_rt<1, EPI>(a, L, blocks, st);
     if (a.rows <= 2) return launch_proj_rt<2, EPI>(a, L, blocks, st);
     if (a.rows <= 4) return launch_proj_rt<4, EPI>(a, L, blocks, st);
@@ -1184,7 +1189,8 @@ bool proj_mfma_reads_p12(const ProjArgs& a, int epi) {
 
 template <int NM, int EPI>
 static hipError_t launch_mfma_epi(const ProjArgs& a, hipStream_t st) {
-    if (proj_mfma_reads_p12(a, EPI)) {
+    if (proj_mfma_reads_p12(a, EPI) || !a.mf0 || (NM == 2 && !a.mf1)) {
+        if (!proj_mfma_reads_p12(a, EPI)) return hipErrorInvalidValue;
         const MfSplit sp = mf12_split(a.nc, a.steps);
         if (sp.ks >= 16) return launch_mfma12_s<NM, 16, EPI>(a, sp.parts, st);
         if (sp.ks == 8) return launch_mfma12_s<NM, 8, EPI>(a, sp.parts, st);
@@ -1197,16 +1203,15 @@ static hipError_t launch_mfma_epi(const ProjArgs& a, hipStream_t st) {
 }
 
 bool proj_uses_mfma(const ProjArgs& a, int epi) {
-    return a.rows >= kMfMinRows && a.mf0 && a.mf_part && a.kq * kMfCols <= 32768;
+    return a.rows >= kMfMinRows && (a.mf0 || proj_mfma_reads_p12(a, epi)) && a.mf_part &&
+           a.kq * kMfCols <= 32768;
 }
 
-bool proj_uses_p12(const ProjArgs& a) {
-    // one row (two rows measured slower than the 16-bit kernel: the
-    // unpacking is paid per activation row), at most 8 k-steps per
-    // wavefront with the launcher's wavefronts per block
-    const uint32_t w = a.w1 ? LLM_PROJ_WPB_SILU
-                     : (a.steps >= LLM_PROJ_LONG_STEPS ? 16u : (uint32_t)LLM_PROJ_WPB);
-    return a.rows <= LLM_P12_MAX_ROWS && a.p0 && (a.w1 == nullptr || a.p1) && a.steps <= 8 * w;
+bool proj_uses_p12(const ProjArgs& a, int epi) {
+    // blocks of one or two rows with every matrix of the launch in 12 bits
+    // and at most 8 k-steps per wavefront (launch_p12_rt's wavefronts)
+    return a.rows <= LLM_P12_MAX_ROWS && a.p0 && (epi != EPI_SILU || a.p1) &&
+           a.steps <= kP12MaxSteps;
 }
 
 hipError_t launch_proj(const ProjArgs& a, int epi, int L, uint32_t blocks,
@@ -1225,6 +1230,21 @@ hipError_t launch_proj(const ProjArgs& a, int epi, int L, uint32_t blocks,
     case EPI_STORE_NORM_IN: return launch_proj_epi<EPI_STORE_NORM_IN>(a, L, blocks, st);
     default: return launch_proj_epi<EPI_SILU>(a, L, blocks, st);
     }
+}
+
+// Every weight of a 12-bit copy set to 0 (h = 8, l = 0): the nibble words
+// of each 768-byte record to 0x88888888, the low bytes to 0.
+__global__ void p12_zero_kernel(uint32_t* p, size_t records) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= records * 192) return;
+    const size_t r = i / 192, w = i % 192;
+    p[r * 192 + w] = w < 128 ? 0u : 0x88888888u;
+}
+
+hipError_t launch_p12_zero(uint8_t* p, size_t records, hipStream_t st) {
+    const size_t words = records * 192;
+    p12_zero_kernel<<<(unsigned)((words + 255) / 256), 256, 0, st>>>((uint32_t*)p, records);
+    return hipGetLastError();
 }
 
 hipError_t launch_copy(const uint4* src, uint4* dst, size_t n16,

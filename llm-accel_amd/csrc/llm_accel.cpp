@@ -80,6 +80,13 @@ struct Matrix {
     uint8_t* p12 = nullptr;
     bool p12_fit[3] = {false, true, true};
     bool p12_ok = false;
+    // held in 12 bits only (no 16-bit copy, no byte planes) until a weight
+    // outside [-2048, 2047] arrives (widen_matrix)
+    bool p12_only = false;
+    // gate <-> up and Q|K|V <-> O: read together (gate|up in one launch,
+    // Q|K|V and O in the fused attention sublayer), so held in the same
+    // layout
+    Matrix* partner = nullptr;
     int L = 16;               // int32 widening interval in k-steps
     size_t elems() const { return (size_t)n_pad * k_pad; }
 };
@@ -418,10 +425,9 @@ void parallel_for(uint32_t n, F fn) {
     for (auto& x : th) x.join();
 }
 
-int upload_rows(llm_ctx* c, Matrix& m, uint32_t row0, uint32_t rows,
-                const int16_t* w, int which) {
-    if (row0 % llm::kBlockRows != 0)
-        return fail(LLM_E_ARG, "projection rows not aligned to 4");
+// Rows [0, rows) of w[rows][k] in the tile4x128 layout, rows padded to a
+// whole block; maxw receives the largest |w|.
+std::vector<int16_t> tile_rows(const Matrix& m, uint32_t rows, const int16_t* w, int* maxw) {
     const uint32_t rows_pad = round_up(rows, llm::kBlockRows);
     const uint32_t S = m.steps;
     std::vector<int16_t> buf((size_t)rows_pad * m.k_pad, 0);
@@ -438,74 +444,143 @@ int upload_rows(llm_ctx* c, Matrix& m, uint32_t row0, uint32_t rows,
         }
         row_max[n] = mx;
     });
-    int maxw = 0;
-    for (int v : row_max) maxw = std::max(maxw, v);
-    const size_t off = (size_t)(row0 / 4) * S * 512;
-    HIP_TRY(hipMemcpy(m.d + off, buf.data(), buf.size() * sizeof(int16_t),
-                      hipMemcpyHostToDevice));
-    if (m.p12) {
-        // the 12-bit copy (layout in kernels.hip, proj_p12_kernel) of these
-        // rows, built from the 16-bit tiles when every weight fits
-        bool fits = true;
-        for (size_t q = 0; fits && q < buf.size(); q++) fits = buf[q] >= -2048 && buf[q] <= 2047;
-        m.p12_fit[which] = fits;
-        m.p12_ok = m.p12_fit[0] && m.p12_fit[1] && m.p12_fit[2];
-        if (fits) {
-            const size_t nsteps = (size_t)(rows_pad / 4) * S;
-            std::vector<uint8_t> pk(nsteps * llm::kP12Step, 0);
-            parallel_for((uint32_t)nsteps, [&](uint32_t bs) {
-                const int16_t* t = &buf[(size_t)bs * 512];  // [4 rows][16 lanes][8]
-                uint8_t* o = &pk[(size_t)bs * llm::kP12Step];
-                for (uint32_t ln = 0; ln < 64; ln++) {
-                    uint32_t word = 0;
-                    for (uint32_t e = 0; e < 8; e++) {
-                        const uint32_t u = (uint32_t)(t[ln * 8 + e] + 2048);
-                        o[8 * ln + e] = (uint8_t)(u & 255);
-                        word |= (u >> 8) << ((e & 1) * 16 + (e >> 1) * 4);
-                    }
-                    std::memcpy(o + 512 + 4 * ln, &word, 4);
-                }
-            });
-            HIP_TRY(hipMemcpy(m.p12 + (size_t)(row0 / 4) * S * llm::kP12Step, pk.data(),
-                              pk.size(), hipMemcpyHostToDevice));
+    int mw = 0;
+    for (int v : row_max) mw = std::max(mw, v);
+    if (maxw) *maxw = mw;
+    return buf;
+}
+
+// The 12-bit copy (layout in kernels.hip, proj_p12_kernel) of the tile
+// rows buf, from row row0 on (every weight in [-2048, 2047]).
+int upload_p12(Matrix& m, uint32_t row0, const std::vector<int16_t>& buf) {
+    const uint32_t S = m.steps;
+    const size_t nsteps = buf.size() / 512;
+    std::vector<uint8_t> pk(nsteps * llm::kP12Step, 0);
+    parallel_for((uint32_t)nsteps, [&](uint32_t bs) {
+        const int16_t* t = &buf[(size_t)bs * 512];  // [4 rows][16 lanes][8]
+        uint8_t* o = &pk[(size_t)bs * llm::kP12Step];
+        for (uint32_t ln = 0; ln < 64; ln++) {
+            uint32_t word = 0;
+            for (uint32_t e = 0; e < 8; e++) {
+                const uint32_t u = (uint32_t)(t[ln * 8 + e] + 2048);
+                o[8 * ln + e] = (uint8_t)(u & 255);
+                word |= (u >> 8) << ((e & 1) * 16 + (e >> 1) * 4);
+            }
+            std::memcpy(o + 512 + 4 * ln, &word, 4);
         }
-    }
-    if (m.mf) {
-        // byte-plane records of the chunks these rows cover
-        if (row0 % llm::kMfRows != 0)
-            return fail(LLM_E_ARG, "projection rows not aligned to 16");
-        const uint32_t c0 = row0 / llm::kMfRows;
-        const uint32_t c1 = (uint32_t)cdiv(row0 + rows, llm::kMfRows);
-        const uint32_t KQ = m.kq;
-        std::vector<int8_t> rec((size_t)(c1 - c0) * KQ * llm::kMfRecord);
-        std::vector<int32_t> sums((size_t)(c1 - c0) * llm::kMfRows * 2, 0);
-        parallel_for(c1 - c0, [&](uint32_t ci) {
-            const uint32_t cc = c0 + ci;
-            for (uint32_t jj = 0; jj < llm::kMfRows; jj++) {
-                const uint32_t local = cc * llm::kMfRows + jj - row0;
-                const bool valid = local < rows;
-                int32_t* sm = &sums[((size_t)ci * llm::kMfRows + jj) * 2];
-                for (uint32_t q = 0; q < KQ; q++)
-                    for (uint32_t g = 0; g < 4; g++)
-                        for (uint32_t b = 0; b < 16; b++) {
-                            const uint32_t k = q * llm::kMfCols + 16 * g + b;
-                            const int32_t v = valid && k < m.k ? w[(size_t)local * m.k + k] : 0;
-                            const int8_t hi = (int8_t)(v >> 8);
-                            const int8_t lo = (int8_t)((v & 255) ^ 0x80);
+    });
+    HIP_TRY(hipMemcpy(m.p12 + (size_t)(row0 / 4) * S * llm::kP12Step, pk.data(), pk.size(),
+                      hipMemcpyHostToDevice));
+    return 0;
+}
+
+// Byte-plane records (when the matrix holds them) and the per-output byte
+// sums (always: the matrix-core kernels over either layout use them) of
+// the 16-output chunks that rows [row0, row0 + rows) cover.
+int upload_planes(Matrix& m, uint32_t row0, uint32_t rows, const int16_t* w) {
+    if (row0 % llm::kMfRows != 0) return fail(LLM_E_ARG, "projection rows not aligned to 16");
+    const uint32_t c0 = row0 / llm::kMfRows;
+    const uint32_t c1 = (uint32_t)cdiv(row0 + rows, llm::kMfRows);
+    const uint32_t KQ = m.kq;
+    std::vector<int8_t> rec(m.mf ? (size_t)(c1 - c0) * KQ * llm::kMfRecord : 0);
+    std::vector<int32_t> sums((size_t)(c1 - c0) * llm::kMfRows * 2, 0);
+    parallel_for(c1 - c0, [&](uint32_t ci) {
+        const uint32_t cc = c0 + ci;
+        for (uint32_t jj = 0; jj < llm::kMfRows; jj++) {
+            const uint32_t local = cc * llm::kMfRows + jj - row0;
+            const bool valid = local < rows;
+            int32_t* sm = &sums[((size_t)ci * llm::kMfRows + jj) * 2];
+            for (uint32_t q = 0; q < KQ; q++)
+                for (uint32_t g = 0; g < 4; g++)
+                    for (uint32_t b = 0; b < 16; b++) {
+                        const uint32_t k = q * llm::kMfCols + 16 * g + b;
+                        const int32_t v = valid && k < m.k ? w[(size_t)local * m.k + k] : 0;
+                        const int8_t hi = (int8_t)(v >> 8);
+                        const int8_t lo = (int8_t)((v & 255) ^ 0x80);
+                        if (m.mf) {
                             const size_t o = ((size_t)ci * KQ + q) * llm::kMfRecord +
                                              (16 * g + jj) * 16 + b;
                             rec[o] = hi;
                             rec[o + 1024] = lo;
-                            sm[0] += hi;
-                            sm[1] += lo;
                         }
-            }
-        });
-        HIP_TRY(hipMemcpy(m.mf + (size_t)c0 * KQ * llm::kMfRecord, rec.data(),
-                          rec.size(), hipMemcpyHostToDevice));
-        HIP_TRY(hipMemcpy(m.ms + (size_t)c0 * llm::kMfRows * 2, sums.data(),
-                          sums.size() * sizeof(int32_t), hipMemcpyHostToDevice));
+                        sm[0] += hi;
+                        sm[1] += lo;
+                    }
+        }
+    });
+    if (m.mf)
+        HIP_TRY(hipMemcpy(m.mf + (size_t)c0 * KQ * llm::kMfRecord, rec.data(), rec.size(),
+                          hipMemcpyHostToDevice));
+    HIP_TRY(hipMemcpy(m.ms + (size_t)c0 * llm::kMfRows * 2, sums.data(),
+                      sums.size() * sizeof(int32_t), hipMemcpyHostToDevice));
+    return 0;
+}
+
+int dev_free(llm_ctx* c, void* p) {
+    auto it = std::find(c->allocations.begin(), c->allocations.end(), p);
+    if (it != c->allocations.end()) c->allocations.erase(it);
+    HIP_TRY(hipFree(p));
+    return 0;
+}
+
+// A matrix held in 12 bits only gets a weight outside [-2048, 2047]: it
+// moves to the 16-bit copy and the byte planes, rebuilt for the rows loaded
+// so far from the 12-bit copy (which is exact for them), and the 12-bit
+// copy is released.
+int widen_matrix(llm_ctx* c, Matrix& m) {
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    const uint32_t S = m.steps;
+    std::vector<uint8_t> pk((size_t)(m.n_pad / 4) * S * llm::kP12Step);
+    HIP_TRY(hipMemcpy(pk.data(), m.p12, pk.size(), hipMemcpyDeviceToHost));
+    std::vector<int16_t> w((size_t)m.n * m.k);
+    parallel_for(m.n, [&](uint32_t n) {
+        const uint32_t b = n / 4, i = n % 4;
+        for (uint32_t k = 0; k < m.k; k++) {
+            const uint32_t s = k / 128, j = (k % 128) / 8, e = k % 8, ln = 16 * i + j;
+            const uint8_t* rec = &pk[((size_t)b * S + s) * llm::kP12Step];
+            uint32_t word;
+            std::memcpy(&word, rec + 512 + 4 * ln, 4);
+            const uint32_t h = (word >> ((e & 1) * 16 + (e >> 1) * 4)) & 15;
+            w[(size_t)n * m.k + k] = (int16_t)((int)(256 * h + rec[8 * ln + e]) - 2048);
+        }
+    });
+    int rc;
+    if ((rc = dev_alloc(c, (void**)&m.d, m.elems() * sizeof(int16_t))) ||
+        (rc = dev_alloc(c, (void**)&m.mf, (size_t)m.nc * m.kq * llm::kMfRecord)))
+        return rc;
+    const std::vector<int16_t> buf = tile_rows(m, m.n, w.data(), nullptr);
+    HIP_TRY(hipMemcpy(m.d, buf.data(), buf.size() * sizeof(int16_t), hipMemcpyHostToDevice));
+    if ((rc = upload_planes(m, 0, m.n, w.data()))) return rc;
+    if ((rc = dev_free(c, m.p12))) return rc;
+    m.p12 = nullptr;
+    m.p12_ok = false;
+    m.p12_only = false;
+    return 0;
+}
+
+int upload_rows(llm_ctx* c, Matrix& m, uint32_t row0, uint32_t rows,
+                const int16_t* w, int which) {
+    if (row0 % llm::kBlockRows != 0)
+        return fail(LLM_E_ARG, "projection rows not aligned to 4");
+    const uint32_t S = m.steps;
+    int maxw = 0;
+    const std::vector<int16_t> buf = tile_rows(m, rows, w, &maxw);
+    bool fits = true;
+    for (size_t q = 0; fits && q < buf.size(); q++) fits = buf[q] >= -2048 && buf[q] <= 2047;
+    int rc;
+    if (m.p12_only && !fits) {
+        if ((rc = widen_matrix(c, m))) return rc;
+        if (m.partner && m.partner->p12_only && (rc = widen_matrix(c, *m.partner))) return rc;
     }
+    if (m.d)
+        HIP_TRY(hipMemcpy(m.d + (size_t)(row0 / 4) * S * 512, buf.data(),
+                          buf.size() * sizeof(int16_t), hipMemcpyHostToDevice));
+    if (m.p12) {
+        m.p12_fit[which] = fits;
+        m.p12_ok = m.p12_fit[0] && m.p12_fit[1] && m.p12_fit[2];
+        if (fits && (rc = upload_p12(m, row0, buf))) return rc;
+    }
+    if (m.ms && (rc = upload_planes(m, row0, rows, w))) return rc;
     m.maxw[which] = maxw;
     m.L = widening_interval(std::max({m.maxw[0], m.maxw[1], m.maxw[2]}));
     return 0;
@@ -886,7 +961,6 @@ int llm_ctx_create(const llm_shape_t* shape, int device, uint32_t num_pairs,
     if (const char* e = std::getenv("LLM_ACCEL_MF12")) c->mf12 = std::strcmp(e, "0") != 0;
     c->mats.resize((size_t)c->L * M_COUNT);
     c->loaded.assign((size_t)c->L * 7, false);
-    size_t total = 0;
     for (uint32_t l = 0; l < c->L; l++) {
         const uint32_t dims[M_COUNT][2] = {{c->Nqkv, c->H}, {c->H, c->H},
                                            {c->I, c->H}, {c->I, c->H},
@@ -898,31 +972,70 @@ int llm_ctx_create(const llm_shape_t* shape, int device, uint32_t num_pairs,
             mt.n_pad = round_up(mt.n, llm::kBlockRows);
             mt.k_pad = round_up(mt.k, llm::kStepCols);
             mt.steps = mt.k_pad / llm::kStepCols;
-            total += mt.elems();
         }
     }
+    // A matrix whose shape every 12-bit kernel serves is held in 12 bits
+    // only (1.5 bytes per weight) until a weight outside [-2048, 2047]
+    // arrives; the others hold the 16-bit copy and the byte planes (and a
+    // 12-bit copy for as long as their weights fit).
+    auto p12_shape = [&](const Matrix& mt, int m) {
+        return c->p12 && c->mf12 && mt.steps <= llm::kP12MaxSteps &&
+               (m != M_QKV || (c->H % llm::kMfRows == 0 && c->Ckv % llm::kMfRows == 0));
+    };
+    for (uint32_t l = 0; l < c->L; l++) {
+        c->mat(l, M_GATE).partner = &c->mat(l, M_UP);
+        c->mat(l, M_UP).partner = &c->mat(l, M_GATE);
+        c->mat(l, M_QKV).partner = &c->mat(l, M_O);
+        c->mat(l, M_O).partner = &c->mat(l, M_QKV);
+    }
+    size_t wide_total = 0;
+    for (int idx = 0; idx < (int)c->mats.size(); idx++) {
+        Matrix& mt = c->mats[idx];
+        mt.p12_only = p12_shape(mt, idx % M_COUNT);
+        if (!mt.p12_only) wide_total += mt.elems();
+    }
     int rc;
-    if ((rc = dev_alloc(c, (void**)&c->arena, total * sizeof(int16_t))))
+    if (wide_total && (rc = dev_alloc(c, (void**)&c->arena, wide_total * sizeof(int16_t))))
         return cleanup(rc);
     size_t off = 0;
     for (int idx = 0; idx < (int)c->mats.size(); idx++) {
         Matrix& mt = c->mats[idx];
-        mt.d = c->arena + off;
-        off += mt.elems();
-        // 12-bit copy for single decode rows
+        if (!mt.p12_only) {
+            mt.d = c->arena + off;
+            off += mt.elems();
+        }
         if (idx % M_COUNT == M_QKV) mt.p12_fit[1] = mt.p12_fit[2] = false;
         if (c->p12)
             if ((rc = dev_alloc(c, (void**)&mt.p12, mt.elems() / 512 * llm::kP12Step)))
                 return cleanup(rc);
-        // byte-plane copy for multi-row blocks on the matrix cores
+        if (mt.p12_only) {
+            // weights not loaded yet are 0 in the 12-bit image, as in the
+            // 16-bit one
+            if (llm::launch_p12_zero(mt.p12, mt.elems() / 512, c->stream) != hipSuccess)
+                return cleanup(fail(LLM_E_HIP, "p12 initialisation"));
+            mt.p12_fit[0] = mt.p12_fit[1] = mt.p12_fit[2] = true;
+            mt.p12_ok = true;
+        }
+        // byte sums for both matrix-core layouts, byte planes for the
+        // matrices held in 16 bits
         mt.nc = (uint32_t)cdiv(mt.n, llm::kMfRows);
         mt.kq = (uint32_t)cdiv(mt.k, llm::kMfCols);
-        if ((rc = dev_alloc(c, (void**)&mt.mf, (size_t)mt.nc * mt.kq * llm::kMfRecord)) ||
-            (rc = dev_alloc(c, (void**)&mt.ms, (size_t)mt.nc * llm::kMfRows * 2 * 4)))
+        if (!mt.p12_only &&
+            (rc = dev_alloc(c, (void**)&mt.mf, (size_t)mt.nc * mt.kq * llm::kMfRecord)))
             return cleanup(rc);
-        if (hipMemset(mt.ms, 0, (size_t)mt.nc * llm::kMfRows * 2 * 4) != hipSuccess)
-            return cleanup(fail(LLM_E_HIP, "hipMemset failed"));
+        if ((rc = dev_alloc(c, (void**)&mt.ms, (size_t)mt.nc * llm::kMfRows * 2 * 4)))
+            return cleanup(rc);
+        if (mt.p12_only) {
+            // byte sums of all-zero rows: sum (w >> 8) = 0, sum ((w & 255) - 128)
+            // = -128 per input of the padded K
+            std::vector<int32_t> zs((size_t)mt.nc * llm::kMfRows * 2, 0);
+            for (size_t q = 1; q < zs.size(); q += 2) zs[q] = -128 * (int32_t)(mt.kq * llm::kMfCols);
+            if (hipMemcpy(mt.ms, zs.data(), zs.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
+                return cleanup(fail(LLM_E_HIP, "weight sums initialisation"));
+        }
     }
+    if (hipStreamSynchronize(c->stream) != hipSuccess)
+        return cleanup(fail(LLM_E_HIP, "weight image initialisation"));
     // tables
     // norm table + one k-step of padding: the fused-norm projections read
     // gammas in whole k-steps
@@ -1479,7 +1592,7 @@ int enqueue_op_projection(llm_ctx* c, uint32_t layer, uint32_t proj, uint32_t T,
     HIP_TRY(hipMemcpy2DAsync(c->op_stage, (size_t)m.k_pad * 2, in, (size_t)m.k * 2,
                              (size_t)m.k * 2, T, hipMemcpyDeviceToDevice, c->stream));
     llm::ProjArgs a{};
-    a.w0 = m.d + (size_t)row0 * m.k_pad;
+    a.w0 = m.d ? m.d + (size_t)row0 * m.k_pad : nullptr;
     a.steps = m.steps;
     a.x = c->op_stage;
     a.ldx = m.k_pad;
@@ -1487,14 +1600,14 @@ int enqueue_op_projection(llm_ctx* c, uint32_t layer, uint32_t proj, uint32_t T,
     a.ldo = n;
     a.n = n;
     a.rows = T;
-    // the matrix-core records cover 16 outputs each
+    if (m.p12_ok) a.p0 = m.p12 + (size_t)(row0 / llm::kBlockRows) * m.steps * llm::kP12Step;
+    // the matrix-core records and sums cover 16 outputs each (matrices held
+    // in 12 bits only have Q, K and V on 16-row boundaries)
     if (row0 % llm::kMfRows == 0) {
         set_mf(c, a, m);
-        if (a.mf0) {
-            a.mf0 += (size_t)(row0 / llm::kMfRows) * m.kq * llm::kMfRecord;
-            a.ms0 += (size_t)2 * row0;
-            a.nc = (uint32_t)cdiv(n, llm::kMfRows);
-        }
+        if (a.mf0) a.mf0 += (size_t)(row0 / llm::kMfRows) * m.kq * llm::kMfRecord;
+        a.ms0 += (size_t)2 * row0;
+        a.nc = (uint32_t)cdiv(n, llm::kMfRows);
     }
     HIP_TRY(llm::launch_proj(a, llm::EPI_STORE, m.L, (uint32_t)cdiv(n, 4), c->stream));
     return 0;
@@ -1838,6 +1951,21 @@ int llm_bench_projection(llm_ctx_t* c, uint32_t kernel, uint32_t rows,
     c->attn_cache.pair = c->ffn_cache.pair = -1;
     if (e != hipSuccess) return fail(LLM_E_HIP, hipGetErrorString(e));
     *avg_us = ms * 1000.0f / iters;
+    return 0;
+}
+
+int llm_weight_bytes(llm_ctx_t* c, uint64_t* bytes, uint32_t* wide_matrices) {
+    if (!c || !bytes || !wide_matrices) return fail(LLM_E_ARG, "null argument");
+    uint64_t b = 0;
+    uint32_t wide = 0;
+    for (const Matrix& m : c->mats) {
+        if (m.d) b += m.elems() * sizeof(int16_t), wide++;
+        if (m.p12) b += m.elems() / 512 * llm::kP12Step;
+        if (m.mf) b += (uint64_t)m.nc * m.kq * llm::kMfRecord;
+        if (m.ms) b += (uint64_t)m.nc * llm::kMfRows * 2 * sizeof(int32_t);
+    }
+    *bytes = b;
+    *wide_matrices = wide;
     return 0;
 }
 

@@ -155,10 +155,12 @@ __device__ __forceinline__ void silu_out_scalar(const ProjArgs& a, uint32_t r, u
 // use, so that no branch separates a load from its use.  red: LDS of
 // NB * WPB * 4 * RT int64.  LW: the int32 sums widen once at the end (4:
 // the matrix's widening interval covers SPW steps), after every step (1)
-// or every product is widened (0).  Returns false when wait() gave up
-// (uniform over the workgroup).
+// or every product is widened (0).  P12: the weights are read from the
+// 12-bit copy a.p0 instead (layout and sums as proj_p12_kernel; int32
+// sums, SPW <= 32).  Returns false when wait() gave up (uniform over the
+// workgroup).
 template <int RT, int EPI, int WPB, int SPW, bool XCOH, bool OCOH, int LW, int NB = 1,
-          typename Wait>
+          bool P12 = false, typename Wait>
 __device__ __forceinline__ bool proj_block(const ProjArgs& a, uint32_t b, int64_t* red,
                                            Wait&& wait) {
     static_assert(EPI != EPI_SILU, "one matrix per block");
@@ -175,15 +177,28 @@ __device__ __forceinline__ bool proj_block(const ProjArgs& a, uint32_t b, int64_
     const uint32_t s0 = wave * S / WPB, s1 = (wave + 1) * S / WPB;
     const uint32_t cnt = s1 - s0;  // <= SPW (the launcher's choice)
     const int16_t* xp = a.x + (size_t)s0 * 128 + j * 8;
+    static_assert(!P12 || SPW <= 32, "int32 sums of the 12-bit products");
     uint4 wv[NB][SPW], gv[SPW];
+    uint2 lv[NB][SPW];     // P12: low bytes of the lane's 8 columns
+    uint32_t hv[NB][SPW];  // P12: their high nibbles
 #pragma unroll
     for (int nb = 0; nb < NB; nb++) {
         const uint32_t bb = NB * b + nb < nblocks ? NB * b + nb : nblocks - 1;
-        const int16_t* wp = a.w0 + ((size_t)(bb * S + s0) * 4 + i) * 128 + j * 8;
+        if constexpr (P12) {
+            const uint8_t* pp = a.p0 + (size_t)(bb * S + s0) * kP12Step;
 #pragma unroll
-        for (int u = 0; u < SPW; u++) {
-            const uint32_t du = cnt == 0 ? 0 : ((uint32_t)u < cnt ? u : cnt - 1);
-            wv[nb][u] = *(const uint4*)(wp + (size_t)du * 512);
+            for (int u = 0; u < SPW; u++) {
+                const uint32_t du = cnt == 0 ? 0 : ((uint32_t)u < cnt ? u : cnt - 1);
+                lv[nb][u] = *(const uint2*)(pp + (size_t)du * kP12Step + 8 * lane);
+                hv[nb][u] = *(const uint32_t*)(pp + (size_t)du * kP12Step + 512 + 4 * lane);
+            }
+        } else {
+            const int16_t* wp = a.w0 + ((size_t)(bb * S + s0) * 4 + i) * 128 + j * 8;
+#pragma unroll
+            for (int u = 0; u < SPW; u++) {
+                const uint32_t du = cnt == 0 ? 0 : ((uint32_t)u < cnt ? u : cnt - 1);
+                wv[nb][u] = *(const uint4*)(wp + (size_t)du * 512);
+            }
         }
     }
     // EPI_STORE_NORM_IN: lane l normalises columns 2l, 2l + 1 of each of
@@ -244,26 +259,71 @@ __device__ __forceinline__ bool proj_block(const ProjArgs& a, uint32_t b, int64_
     for (int nb = 0; nb < NB; nb++)
 #pragma unroll
         for (int r = 0; r < RT; r++) part[nb][r] = 0, wide[nb][r] = 0;
-#pragma unroll
-    for (int u = 0; u < SPW; u++) {
-        const uint32_t keep = lane_mask((uint32_t)u < cnt);
+    if constexpr (P12) {
+        // w + 2048 = 256 h + l: sum w x = 256 sum h x + sum l x - 2048 sum x;
+        // steps past the wavefront's last carry zero activations
+        int32_t ph[NB][RT], sx[RT];
 #pragma unroll
         for (int r = 0; r < RT; r++) {
-            const uint4 x = xv[u][r];
+            sx[r] = 0;
 #pragma unroll
-            for (int nb = 0; nb < NB; nb++) {
-                const uint4 w = and4(wv[nb][u], keep);
-                if (LW == 0) {
-                    wide[nb][r] += dot2_wide(w.x, x.x) + dot2_wide(w.y, x.y) +
-                                   dot2_wide(w.z, x.z) + dot2_wide(w.w, x.w);
-                } else {
-                    int32_t p = part[nb][r];
-                    p = dot2(w.x, x.x, p);
-                    p = dot2(w.y, x.y, p);
-                    p = dot2(w.z, x.z, p);
-                    p = dot2(w.w, x.w, p);
+            for (int nb = 0; nb < NB; nb++) ph[nb][r] = 0;
+        }
+#pragma unroll
+        for (int u = 0; u < SPW; u++) {
+            const uint32_t keep = lane_mask((uint32_t)u < cnt);
+#pragma unroll
+            for (int r = 0; r < RT; r++) {
+                const uint4 x = and4(xv[u][r], keep);
+                sx[r] = dot2(0x00010001u, x.x, sx[r]);
+                sx[r] = dot2(0x00010001u, x.y, sx[r]);
+                sx[r] = dot2(0x00010001u, x.z, sx[r]);
+                sx[r] = dot2(0x00010001u, x.w, sx[r]);
+#pragma unroll
+                for (int nb = 0; nb < NB; nb++) {
+                    const uint2 l8 = lv[nb][u];
+                    const uint32_t h4 = hv[nb][u];
+                    int32_t p = part[nb][r], q = ph[nb][r];
+                    p = dot2(__builtin_amdgcn_perm(0u, l8.x, 0x0c010c00u), x.x, p);
+                    p = dot2(__builtin_amdgcn_perm(0u, l8.x, 0x0c030c02u), x.y, p);
+                    p = dot2(__builtin_amdgcn_perm(0u, l8.y, 0x0c010c00u), x.z, p);
+                    p = dot2(__builtin_amdgcn_perm(0u, l8.y, 0x0c030c02u), x.w, p);
+                    q = dot2(h4 & 0x000f000fu, x.x, q);
+                    q = dot2((h4 >> 4) & 0x000f000fu, x.y, q);
+                    q = dot2((h4 >> 8) & 0x000f000fu, x.z, q);
+                    q = dot2((h4 >> 12) & 0x000f000fu, x.w, q);
                     part[nb][r] = p;
-                    if (LW == 1) wide[nb][r] += p, part[nb][r] = 0;
+                    ph[nb][r] = q;
+                }
+            }
+        }
+#pragma unroll
+        for (int nb = 0; nb < NB; nb++)
+#pragma unroll
+            for (int r = 0; r < RT; r++)
+                wide[nb][r] = 256 * (int64_t)ph[nb][r] - 2048 * (int64_t)sx[r];
+    } else {
+#pragma unroll
+        for (int u = 0; u < SPW; u++) {
+            const uint32_t keep = lane_mask((uint32_t)u < cnt);
+#pragma unroll
+            for (int r = 0; r < RT; r++) {
+                const uint4 x = xv[u][r];
+#pragma unroll
+                for (int nb = 0; nb < NB; nb++) {
+                    const uint4 w = and4(wv[nb][u], keep);
+                    if (LW == 0) {
+                        wide[nb][r] += dot2_wide(w.x, x.x) + dot2_wide(w.y, x.y) +
+                                       dot2_wide(w.z, x.z) + dot2_wide(w.w, x.w);
+                    } else {
+                        int32_t p = part[nb][r];
+                        p = dot2(w.x, x.x, p);
+                        p = dot2(w.y, x.y, p);
+                        p = dot2(w.z, x.z, p);
+                        p = dot2(w.w, x.w, p);
+                        part[nb][r] = p;
+                        if (LW == 1) wide[nb][r] += p, part[nb][r] = 0;
+                    }
                 }
             }
         }

@@ -43,7 +43,7 @@ EXPORTS = (
     "llm_bench_projection", "llm_load_lm_head", "llm_lm_head_argmax",
     "llm_generate", "llm_lm_head_argmax_static", "llm_set_log",
     "llm_load_checkpoint_dir", "llm_op", "llm_port", "llm_port_write",
-    "llm_port_read",
+    "llm_port_read", "llm_weight_bytes",
 )
 CKPT_TIE_EMBEDDINGS = 1
 CKPT_REQUIRE_LM_HEAD = 2
@@ -166,6 +166,8 @@ def load_library(path=LIB_PATH):
                                     ctypes.POINTER(ctypes.c_size_t)]),
         "llm_port_write": (ctypes.c_int, [vp, _u32, _i16p, ctypes.c_size_t]),
         "llm_port_read": (ctypes.c_int, [vp, _u32, _i16p, ctypes.c_size_t]),
+        "llm_weight_bytes": (ctypes.c_int, [vp, ctypes.POINTER(ctypes.c_uint64),
+                                            ctypes.POINTER(ctypes.c_uint32)]),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)
@@ -506,6 +508,15 @@ class Accelerator:
                                                rows, layers, iters,
                                                ctypes.byref(us)), "bench_projection")
         return us.value
+
+    def weight_bytes(self):
+        """(device bytes of the decoder-layer weight images, matrices held
+        in 16 bits)."""
+        b = ctypes.c_uint64()
+        w = ctypes.c_uint32()
+        self._check(lib().llm_weight_bytes(self._ctx, ctypes.byref(b), ctypes.byref(w)),
+                    "weight_bytes")
+        return b.value, w.value
 
     def bench_copy(self, nbytes, iters):
         ms = ctypes.c_float()

@@ -103,3 +103,65 @@ def test_attention_mf12_matches_oracle(cfg, case):
                 assert rc == 0
                 got = acc.download(0, rows)
                 assert first_mismatch(got, want[rows]) is None, f"mf12={mf12} rows={rows}"
+
+
+@pytest.mark.parametrize("case", ["fits", "down_outlier", "v_outlier", "gate_outlier"])
+def test_single_weight_image(case):
+    """Matrices whose weights fit 12 bits hold only the 12-bit copy and the
+    byte sums; a weight past 12 bits moves its matrix and the one read
+    with it (gate with up, Q|K|V with O) to the 16-bit tiles and byte
+    planes, rebuilt from what was loaded (V arrives after Q and K of the
+    same Q|K|V matrix).  Task 18 + 19 of 1, 2 and 8 rows must still equal
+    the oracle."""
+    spec = workloads.CONFIG_A
+    synth = workloads.SyntheticModel(spec, layers=1)
+    edits = {(0, p): _extremes for p in range(7)}
+    if case == "down_outlier":
+        edits[(0, 6)] = _outlier
+    if case == "v_outlier":
+        edits[(0, 2)] = _outlier
+    if case == "gate_outlier":
+        edits[(0, 4)] = _outlier
+    model = _Edited(synth, edits)
+    om = oracle_from_synthetic(model, oracle_shape(spec, layers=1, max_seq=64))
+    dims = [spec.proj_dims(p) for p in range(7)]
+    qkv = (dims[0][0] + dims[1][0] + dims[2][0]) * spec.hidden
+    mats = {"qkv": qkv, "o": dims[3][0] * dims[3][1], "gate": dims[4][0] * dims[4][1],
+            "up": dims[5][0] * dims[5][1], "down": dims[6][0] * dims[6][1]}
+    kpad = {"qkv": 256, "o": 256, "gate": 256, "up": 256, "down": 768}
+    npad = {"qkv": 512, "o": 256, "gate": 688, "up": 688, "down": 256}
+    rng = np.random.default_rng(17)
+    with _accel(spec, {}, 64) as acc:
+        acc.load_model(model)
+        nbytes, wide = acc.weight_bytes()
+        wide_names = {"fits": [], "down_outlier": ["down"], "v_outlier": ["qkv", "o"],
+                      "gate_outlier": ["gate", "up"]}[case]
+        want_bytes = 0
+        for name in mats:
+            elems = npad[name] * kpad[name]
+            nc, kq = -(-npad[name] // 16), -(-kpad[name] // 64)
+            if name == "down":
+                kq = -(-688 // 64)
+            want_bytes += nc * 16 * 2 * 4
+            if name in wide_names:
+                want_bytes += elems * 2 + nc * kq * 2048
+            else:
+                want_bytes += elems // 512 * 768
+        _say(f"case single image {case}: {nbytes} bytes, {wide} wide")
+        assert wide == len(wide_names)
+        assert nbytes == want_bytes
+        for rows in (1, 2, 8):
+            h = rng.integers(-20000, 20000, (rows, spec.hidden)).astype(np.int16)
+            kc, vc = om.new_kv()
+            acc.kv_clear()
+            acc.upload(2, h)
+            rc, _ = acc.task(18, 0, rows, 0, 2, 0)
+            assert rc == 0
+            rc, _ = acc.task(19, 0, rows, 0, 0, 1)
+            assert rc == 0
+            got = acc.download(1, rows)
+            code, mid, _ = om.task((kc, vc), 18, 0, h, 0)
+            assert code == 0
+            code, want, _ = om.task((kc, vc), 19, 0, mid, 0)
+            assert code == 0
+            assert first_mismatch(got, want) is None, f"{case} rows={rows}"
