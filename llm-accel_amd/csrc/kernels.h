@@ -115,7 +115,7 @@ struct MfSplit {
 MfSplit mf_split(uint32_t nc, uint32_t kq);
 // The same for the matrix-core kernel over the 12-bit copy, in k-steps,
 // and whether a launch of the matrix-core path takes that kernel.
-MfSplit mf12_split(uint32_t nc, uint32_t steps);
+MfSplit mf12_split(uint32_t nc, uint32_t steps, uint32_t nm);
 bool proj_mfma_reads_p12(const ProjArgs& a, int epi);
 // int32 words of partial sums per (chunk, part) record.
 constexpr uint32_t mf_part_words(uint32_t nm) { return nm * 2 * 256 + 32; }

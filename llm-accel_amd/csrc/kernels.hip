@@ -1146,12 +1146,13 @@ static hipError_t launch_mfma_q(const ProjArgs& a, uint32_t parts, hipStream_t s
 }
 
 // The 12-bit matrix-core kernel splits whole 128-column steps the same
-// way: wavefronts keep at least one step, at most LLM_MF_QMAX / 2; fewer
-// wavefronts per workgroup below 4 steps each (more workgroups resident:
-// measured faster for K = 2048, slower for K = 11008 with 4).
-MfSplit mf12_split(uint32_t nc, uint32_t steps) {
+// way: wavefronts keep at least one step, at most LLM_MF_QMAX / 2.  Two
+// matrices (gate|up) take fewer wavefronts per workgroup below 4 steps
+// each: more workgroups resident (measured faster at K = 2048; slower for
+// one matrix, and for K = 11008).
+MfSplit mf12_split(uint32_t nc, uint32_t steps, uint32_t nm) {
     MfSplit s{LLM_MF12_KS, 1};
-    while (s.ks > 4 && steps < LLM_MF12_MIN_STEPS * s.ks) s.ks /= 2;
+    while (nm == 2 && s.ks > 4 && steps < LLM_MF12_MIN_STEPS * s.ks) s.ks /= 2;
     while (nc * s.parts < LLM_MF12_WG_TARGET && steps / (s.parts * 2) >= s.ks) s.parts *= 2;
     while (mf_chunks_per_wave(steps, s.parts, s.ks) > LLM_MF_QMAX / 2) s.parts *= 2;
     return s;
@@ -1191,7 +1192,7 @@ template <int NM, int EPI>
 static hipError_t launch_mfma_epi(const ProjArgs& a, hipStream_t st) {
     if (proj_mfma_reads_p12(a, EPI) || !a.mf0 || (NM == 2 && !a.mf1)) {
         if (!proj_mfma_reads_p12(a, EPI)) return hipErrorInvalidValue;
-        const MfSplit sp = mf12_split(a.nc, a.steps);
+        const MfSplit sp = mf12_split(a.nc, a.steps, NM);
         if (sp.ks >= 16) return launch_mfma12_s<NM, 16, EPI>(a, sp.parts, st);
         if (sp.ks == 8) return launch_mfma12_s<NM, 8, EPI>(a, sp.parts, st);
         return launch_mfma12_s<NM, 4, EPI>(a, sp.parts, st);

@@ -1150,9 +1150,9 @@ int llm_ctx_create(const llm_shape_t* shape, int device, uint32_t num_pairs,
         for (uint32_t m = 0; m < M_COUNT; m++) {
             const Matrix& mt = c->mat(0, m);
             // either kernel of the matrix-core path
-            const uint32_t parts = std::max(llm::mf_split(mt.nc, mt.kq).parts,
-                                            llm::mf12_split(mt.nc, mt.steps).parts);
             const uint32_t nm = (m == M_GATE || m == M_UP) ? 2 : 1;
+            const uint32_t parts = std::max(llm::mf_split(mt.nc, mt.kq).parts,
+                                            llm::mf12_split(mt.nc, mt.steps, nm).parts);
             words = std::max(words, (size_t)mt.nc * parts * llm::mf_part_words(nm));
             chunks = std::max(chunks, (size_t)mt.nc);
         }
