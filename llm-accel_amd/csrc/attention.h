@@ -63,6 +63,10 @@ struct AttnArgs {
     uint32_t* host_abort; // host-visible copy
     uint32_t wait_limit;  // bound of one wait (100 MHz ticks)
     uint32_t cus;
+    // one-launch tile path with the O projection in the same launch: the
+    // combining workgroups' arrival counters (kSyncAttnLines of them,
+    // kSyncStride words apart; null otherwise)
+    uint32_t* attn_arrive;
     // one-launch kernels go through hipLaunchCooperativeKernel, which
     // refuses a grid the device cannot hold at once (other work holding
     // compute units included); the launcher then takes the separate launches
@@ -135,6 +139,31 @@ bool sublayer_fused_ok(const SublayerArgs& s, uint32_t rows, int qkv_epi, int L_
                        int capacity);
 // Whether the fused launch reads the two projections' 12-bit copies.
 bool sublayer_reads_p12(const SublayerArgs& s);
+
+// The one-launch tile path (5-64 tiles, decode rows) and the O projection
+// in one launch: tile workgroups first, then O blocks that wait for every
+// (row, query head) of the attention (arrivals on the kSyncAttn counters,
+// which held attn_base before the launch; the host adds `arrivals` to its
+// copy after the launch).
+struct TileOArgs {
+    AttnArgs at;
+    ProjArgs o;
+    uint32_t ntile, no;     // tile workgroups (the tile grid), O workgroups
+    uint32_t arrivals;      // rows x query heads
+    uint32_t* sync;
+    uint32_t attn_base;
+    uint32_t* host_abort;
+    uint32_t wait_limit;
+};
+// Workgroups of the tile + O launch the device holds at once.
+int tile_o_capacity(uint32_t head_dim, uint32_t rows, int cus);
+// Fills the launch shape of s (grid, arrivals) and returns whether the
+// launch serves `rows` rows: head_dim 64 or 128, 1-2 rows, the attention
+// on the one-launch tile path (5-64 tiles, not the GQA path, not
+// cooperative), O within 4 k-steps per wavefront, the whole grid within
+// `capacity`.
+bool tile_o_prepare(TileOArgs& s, uint32_t rows, int capacity);
+hipError_t launch_attention_tile_o(const TileOArgs& s, uint32_t rows, int L, hipStream_t st);
 // QKV and O workgroups of the fused launch for `blocks` 4-row blocks.
 uint32_t sublayer_qkv_workgroups(uint32_t blocks);
 uint32_t sublayer_o_workgroups(uint32_t blocks);

@@ -1229,10 +1229,14 @@ __device__ __forceinline__ void slice_load_v(const AttnArgs& a, uint32_t h, uint
 // earlier tiles, publishes its PV values and then its flagged tile sum,
 // and the workgroup of the last tile polls the other tiles' sums and runs
 // the recurrence.
-template <int D, bool FUSED>
+// OARR (FUSED only): the output row slice is stored device-coherently and
+// the combining workgroup then arrives on a.attn_arrive (kSyncAttnLines
+// counters), for O blocks of the same launch.
+template <int D, bool FUSED, bool OARR = false>
 __device__ __forceinline__ void tile_pv_phase(const AttnArgs& a, const TileWg& wg,
                                               TilePvSmem<D>& sm, const int16_t* lsc,
                                               const int32_t* lmt) {
+    static_assert(!OARR || FUSED, "the O hand-off follows the one-launch combine");
     static_assert(D % 32 == 0, "tile path: head_dim a multiple of 32");
     constexpr uint32_t NTH = D * 2;
     constexpr int NE = (257 + NTH - 1) / NTH;    // exp table pieces per thread
@@ -1481,9 +1485,14 @@ __device__ __forceinline__ void tile_pv_phase(const AttnArgs& a, const TileWg& w
             }
         }
     }
-    if (tid < D)
-        a.out[(size_t)t * a.ldo + (size_t)g * D + tid] =
-            fx_sat16(fx_rnd((int64_t)acc * fx_inv_sum(sum), 16));
+    if (tid < D) {
+        const int16_t o = fx_sat16(fx_rnd((int64_t)acc * fx_inv_sum(sum), 16));
+        int16_t* op = &a.out[(size_t)t * a.ldo + (size_t)g * D + tid];
+        if (OARR)
+            st_coherent(op, o);
+        else
+            *op = o;
+    }
     if (FUSED) {
         // every tile of this (row, query head) has read the maxima and
         // published its sum: clear the flags for the next launch
@@ -1493,6 +1502,7 @@ __device__ __forceinline__ void tile_pv_phase(const AttnArgs& a, const TileWg& w
             st_coherent(&a.s_tsum[b], 0);
         }
     }
+    if (OARR) arrive(a.attn_arrive, kSyncAttnLines, kSyncStride);
 }
 
 template <int D>
@@ -1525,6 +1535,42 @@ __global__ __launch_bounds__(D * 2) void attention_tile_fused_kernel(AttnArgs a)
     tile_scores_phase<D, true>(a, wg, sm.s, lsc, &lmt);
     __syncthreads();  // phase 1's LDS use ends
     tile_pv_phase<D, true>(a, wg, sm.p, lsc, &lmt);
+}
+
+// The one-launch tile path and the O projection in one launch (decode
+// rows): tile workgroups as in attention_tile_fused_kernel, the combining
+// workgroup of each (row, query head) storing its slice coherently and
+// arriving on the attention counters; then O blocks (proj_block, two per
+// workgroup) that issue their weight loads, wait for every (row, query
+// head) and finish with the residual and FFN-norm epilogue.  Launched only
+// when the whole grid is resident at once.
+template <int D, int RT, int LW, bool P12>
+__global__ __launch_bounds__(D * 2) void attention_tile_o_kernel(TileOArgs s) {
+    constexpr int WPB = D / 32, SPW = 4;
+    __shared__ union {
+        TileScoresSmem<D> s;
+        TilePvSmem<D> p;
+    } sm;
+    __shared__ int16_t lsc[TILE];
+    __shared__ int32_t lmt;
+    __shared__ int64_t red[kSubOBlocks * WPB * 4 * RT];
+    __shared__ uint32_t flag;
+    if (blockIdx.x < s.ntile) {
+        const TileWg wg = tile_wg(s.at);
+        if (!wg.valid) return;                    // padding
+        if (wg.tile * TILE >= s.at.pos0 + wg.t + 1) return;  // beyond this row's context
+        tile_scores_phase<D, true>(s.at, wg, sm.s, lsc, &lmt);
+        __syncthreads();  // phase 1's LDS use ends
+        tile_pv_phase<D, true, true>(s.at, wg, sm.p, lsc, &lmt);
+        return;
+    }
+    const uint32_t b = blockIdx.x - s.ntile;
+    proj_block<RT, EPI_RESID, WPB, SPW, true, false, LW, kSubOBlocks, P12>(s.o, b, red, [&] {
+        return wait_counts(
+            s.sync + kSyncAttn + kSyncStride * (b % kSyncAttnLines), 0, 1,
+            [&](uint32_t) { return s.attn_base + s.arrivals; }, s.wait_limit, s.sync + kSyncAbort,
+            s.host_abort, &flag);
+    });
 }
 
 // Workgroups of the one-launch tile path the device holds at once.  The
@@ -1702,6 +1748,70 @@ hipError_t launch_attention_sublayer(const SublayerArgs& s, uint32_t rows, int q
         rows == 1 ? launch_sub<64, 1>(s, qkv_epi, L, st) : launch_sub<64, 2>(s, qkv_epi, L, st);
     else
         rows == 1 ? launch_sub<128, 1>(s, qkv_epi, L, st) : launch_sub<128, 2>(s, qkv_epi, L, st);
+    return hipGetLastError();
+}
+
+// The smallest residency over the variants of the tile + O launch.
+template <int D, int RT>
+static int tile_o_capacity_of(int cus) {
+    int pc[4] = {0, 0, 0, 0};
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &pc[0], attention_tile_o_kernel<D, RT, 4, false>, 2 * D, 0) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &pc[1], attention_tile_o_kernel<D, RT, 1, false>, 2 * D, 0) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &pc[2], attention_tile_o_kernel<D, RT, 0, false>, 2 * D, 0) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &pc[3], attention_tile_o_kernel<D, RT, 4, true>, 2 * D, 0) != hipSuccess)
+        return 0;
+    return std::min({pc[0], pc[1], pc[2], pc[3]}) * cus;
+}
+
+int tile_o_capacity(uint32_t head_dim, uint32_t rows, int cus) {
+    if (head_dim == 64) return rows == 1 ? tile_o_capacity_of<64, 1>(cus) : tile_o_capacity_of<64, 2>(cus);
+    if (head_dim == 128) return rows == 1 ? tile_o_capacity_of<128, 1>(cus) : tile_o_capacity_of<128, 2>(cus);
+    return 0;
+}
+
+bool tile_o_prepare(TileOArgs& s, uint32_t rows, int capacity) {
+    const AttnArgs& a = s.at;
+    const uint32_t D = a.head_dim;
+    if ((D != 64 && D != 128) || rows == 0 || rows > 2) return false;
+    const uint32_t tiles = (a.pos0 + rows + TILE - 1) / TILE;
+    // the attention launch would take the one-launch tile path
+    if (tiles <= kSplitHeadMaxTiles || tiles > kTileFusedMaxTiles) return false;
+    if (a.use_gqa && attention_gqa_ok(a, rows)) return false;
+    if (!a.tile_fused || !a.s_tmax32 || a.coop) return false;
+    // O: up to 4 k-steps per wavefront, from the 12-bit or the 16-bit copy
+    if (s.o.steps > 4 * (D / 32) || !(s.o.p0 || s.o.w0)) return false;
+    if (!s.sync || !s.host_abort) return false;
+    s.at.grid_rows = rows;
+    s.at.grid_tiles = tiles;
+    s.at.attn_arrive = s.sync + kSyncAttn;
+    s.ntile = tile_grid(rows, tiles, a.num_kv_heads, a.group);
+    s.no = (((s.o.n + 3) / 4) + kSubOBlocks - 1) / kSubOBlocks;
+    s.arrivals = rows * a.num_heads;
+    return (int64_t)s.ntile + s.no <= capacity;
+}
+
+template <int D, int RT>
+static void launch_tile_o_d(const TileOArgs& s, int L, hipStream_t st) {
+    const uint32_t grid = s.ntile + s.no;
+    if (s.o.p0)
+        attention_tile_o_kernel<D, RT, 4, true><<<grid, 2 * D, 0, st>>>(s);
+    else if (L >= 4)
+        attention_tile_o_kernel<D, RT, 4, false><<<grid, 2 * D, 0, st>>>(s);
+    else if (L >= 1)
+        attention_tile_o_kernel<D, RT, 1, false><<<grid, 2 * D, 0, st>>>(s);
+    else
+        attention_tile_o_kernel<D, RT, 0, false><<<grid, 2 * D, 0, st>>>(s);
+}
+
+hipError_t launch_attention_tile_o(const TileOArgs& s, uint32_t rows, int L, hipStream_t st) {
+    if (s.at.head_dim == 64)
+        rows == 1 ? launch_tile_o_d<64, 1>(s, L, st) : launch_tile_o_d<64, 2>(s, L, st);
+    else
+        rows == 1 ? launch_tile_o_d<128, 1>(s, L, st) : launch_tile_o_d<128, 2>(s, L, st);
     return hipGetLastError();
 }
 

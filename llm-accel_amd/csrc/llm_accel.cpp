@@ -193,6 +193,10 @@ struct llm_ctx {
     // residency of the fused launch per (rows - 1, QKV epilogue is the
     // input norm): -1 until first needed
     int sub_cap[2][2] = {{-1, -1}, {-1, -1}};
+    // the one-launch tile path and O in one launch for decode rows at 5-64
+    // tiles; LLM_ACCEL_TILE_O=0 keeps them two launches
+    bool tile_o = true;
+    int tile_o_cap[2] = {-1, -1};
     int cus = 0;
     // RMSNorm gain: > 0 when it is the same for every row (hidden >= 128:
     // fm_t(hidden) saturates, recip() returns 0, the mean square is 0 and
@@ -815,13 +819,32 @@ int enqueue_attention_sublayer(llm_ctx* c, uint32_t layer, uint32_t R,
             TimedScope ts(c, LLM_K_QKV);
             HIP_TRY(llm::launch_proj(a, qkv_epi, mq.L, mq.n_pad / 4, st));
         }
-        {
-            TimedScope ts(c, LLM_K_ATTENTION);
-            HIP_TRY(llm::launch_attention(at, R, c->Hkv, chunks, st));
+        llm::TileOArgs to{};
+        bool tile_o = false;
+        if (c->tile_o && R <= 2 && !llm::proj_uses_mfma(o, llm::EPI_RESID)) {
+            int& cc = c->tile_o_cap[R - 1];
+            if (cc < 0) cc = llm::tile_o_capacity(c->d, R, c->cus);
+            to.at = at;
+            to.o = o;
+            to.sync = c->sync;
+            to.attn_base = c->sync_attn;
+            to.host_abort = c->host_abort;
+            to.wait_limit = c->wait_limit;
+            tile_o = llm::tile_o_prepare(to, R, cc);
         }
-        {
-            TimedScope ts(c, LLM_K_OPROJ);
-            HIP_TRY(llm::launch_proj(o, llm::EPI_RESID, mo.L, mo.n_pad / 4, st));
+        if (tile_o) {
+            TimedScope ts(c, LLM_K_ATTENTION);
+            HIP_TRY(llm::launch_attention_tile_o(to, R, mo.L, st));
+            c->sync_attn += to.arrivals;  // counter values after this launch
+        } else {
+            {
+                TimedScope ts(c, LLM_K_ATTENTION);
+                HIP_TRY(llm::launch_attention(at, R, c->Hkv, chunks, st));
+            }
+            {
+                TimedScope ts(c, LLM_K_OPROJ);
+                HIP_TRY(llm::launch_proj(o, llm::EPI_RESID, mo.L, mo.n_pad / 4, st));
+            }
         }
     }
     invalidate_pair(c, out_pair);
@@ -959,6 +982,7 @@ int llm_ctx_create(const llm_shape_t* shape, int device, uint32_t num_pairs,
     // weights
     if (const char* e = std::getenv("LLM_ACCEL_P12")) c->p12 = std::strcmp(e, "0") != 0;
     if (const char* e = std::getenv("LLM_ACCEL_MF12")) c->mf12 = std::strcmp(e, "0") != 0;
+    if (const char* e = std::getenv("LLM_ACCEL_TILE_O")) c->tile_o = std::strcmp(e, "0") != 0;
     c->mats.resize((size_t)c->L * M_COUNT);
     c->loaded.assign((size_t)c->L * 7, false);
     for (uint32_t l = 0; l < c->L; l++) {
