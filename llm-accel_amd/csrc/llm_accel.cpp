@@ -340,15 +340,17 @@ int check_waits(llm_ctx* c) {
 // the case this covers.
 struct WaitFreeScope {
     llm_ctx* c;
-    bool fused, tile_fused, gqa_fused;
+    bool fused, tile_fused, gqa_fused, tile_o;
     explicit WaitFreeScope(llm_ctx* ctx)
-        : c(ctx), fused(ctx->fused), tile_fused(ctx->tile_fused), gqa_fused(ctx->gqa_fused) {
-        c->fused = c->tile_fused = c->gqa_fused = false;
+        : c(ctx), fused(ctx->fused), tile_fused(ctx->tile_fused), gqa_fused(ctx->gqa_fused),
+          tile_o(ctx->tile_o) {
+        c->fused = c->tile_fused = c->gqa_fused = c->tile_o = false;
     }
     ~WaitFreeScope() {
         c->fused = fused;
         c->tile_fused = tile_fused;
         c->gqa_fused = gqa_fused;
+        c->tile_o = tile_o;
     }
 };
 
