@@ -67,7 +67,14 @@ struct ProjArgs {
     // The matrix-core path reads p0 (and p1) instead of the byte planes
     // when set and present (proj_mfma12_kernel).
     uint32_t mf_p12;
+    // Sparse corrections of the 12-bit copies p0 / p1 (null: none): per
+    // output row kCorrSlots words (k << 16) | (uint16) delta, delta =
+    // w - clamp(w, -2048, 2047) for the row's weights outside 12 bits, whose
+    // copy holds the clamped value; unused words are 0.
+    const uint32_t* corr0;
+    const uint32_t* corr1;
 };
+constexpr uint32_t kCorrSlots = 4;
 // Bytes of the p12 copy per 4-row block and k-step.
 constexpr uint32_t kP12Step = 768;
 // Sets every weight of a p12 copy of `records` records to 0.

@@ -330,7 +330,11 @@ __global__ __launch_bounds__(64 * WPB) void proj_kernel(ProjArgs a) {
 // all loaded before the first product; partial sums stay in int32
 // (SPW <= 32: |sum l x| <= 8 SPW 255 2^15 < 2^31).
 // ---------------------------------------------------------------------
-template <int RT, int EPI, int WPB, int SPW>
+// CORR: the copies carry corrections (ProjArgs::corr0 / corr1; a separate
+// variant, so that the common one holds no registers for them): the slot
+// words are loaded when the kernel starts, a row's activations at its
+// correction columns in the epilogue, for rows that have any.
+template <int RT, int EPI, int WPB, int SPW, bool CORR = false>
 __global__ __launch_bounds__(64 * WPB) void proj_p12_kernel(ProjArgs a) {
     static_assert(SPW <= 32, "int32 partial sums");
     constexpr int NM = EPI == EPI_SILU ? 2 : 1;
@@ -342,6 +346,14 @@ __global__ __launch_bounds__(64 * WPB) void proj_p12_kernel(ProjArgs a) {
     const bool eout = et < 4 * RT && er < a.rows && en < a.n;
     EpiIn ei{0, 0, 0};
     if (eout) ei = epi_fetch<EPI>(a, er, en);
+    CorrIn cr[NM] = {};
+    if (CORR && eout) {
+#pragma unroll
+        for (int m = 0; m < NM; m++) {
+            const uint32_t* corr = m == 0 ? a.corr0 : a.corr1;
+            if (corr) corr_slots(corr, en, cr[m]);
+        }
+    }
     const uint32_t fn = b * 4 + (et >> 3), fr = et & 7;
     const bool efill = EPI == EPI_RESID && a.final_out && et < 32 && fr >= a.rows && fn < a.n;
     int16_t fill = 0;
@@ -456,6 +468,10 @@ __global__ __launch_bounds__(64 * WPB) void proj_p12_kernel(ProjArgs a) {
             tot[m] = 0;
 #pragma unroll
             for (int w = 0; w < WPB; w++) tot[m] += red[w][m][ii][er];
+            if (CORR && (cr[m].e[0] | cr[m].e[1] | cr[m].e[2] | cr[m].e[3]) != 0) {
+                corr_inputs<EPI, false>(a, er, cr[m]);
+                tot[m] += corr_sum(cr[m]);
+            }
         }
         if constexpr (EPI == EPI_SILU)
             silu_out_scalar<4 * RT>(a, er, en, tot[0], tot[NM - 1], et);
@@ -596,6 +612,7 @@ struct MfEpi {
     EpiIn ei;
     int32_t ems[NM][2];
     int16_t fill;
+    CorrIn cr[NM];  // correction slots of the 12-bit copies (zero without)
 };
 template <int NM, int EPI>
 __device__ __forceinline__ MfEpi<NM, EPI> mf_epi_fetch(const ProjArgs& a, uint32_t c) {
@@ -609,6 +626,8 @@ __device__ __forceinline__ MfEpi<NM, EPI> mf_epi_fetch(const ProjArgs& a, uint32
                 const int32_t* ms = m == 0 ? a.ms0 : a.ms1;
                 e.ems[m][0] = ms[2 * en];
                 e.ems[m][1] = ms[2 * en + 1];
+                const uint32_t* corr = m == 0 ? a.corr0 : a.corr1;
+                if (corr) corr_slots(corr, en, e.cr[m]);  // activations at the end
             }
         } else if (EPI == EPI_RESID && a.final_out && er < 8) {
             e.fill = a.res[(size_t)er * a.ldr + en];
@@ -710,6 +729,15 @@ __device__ __forceinline__ void mf_finish(const ProjArgs& a, uint32_t c, uint32_
                 const int32_t m0 = first ? fe.ems[m][0] : ms[2 * nn];
                 const int32_t m1 = first ? fe.ems[m][1] : ms[2 * nn + 1];
                 tot[m] = mf_total(s[m][0], s[m][1], s[m][2], s[m][3], m0, m1, sc, sd, k64);
+                const uint32_t* corr = m == 0 ? a.corr0 : a.corr1;
+                if (corr) {
+                    CorrIn c = fe.cr[m];
+                    if (!first) corr_slots(corr, nn, c);
+                    if ((c.e[0] | c.e[1] | c.e[2] | c.e[3]) != 0) {
+                        corr_inputs<EPI, false>(a, r, c);
+                        tot[m] += corr_sum(c);
+                    }
+                }
             }
             proj_out<EPI>(a, r, nn, tot[0], tot[NM - 1], e, a.exp8);
         } else if (EPI == EPI_RESID && a.final_out && r < 8) {
@@ -1066,15 +1094,22 @@ static hipError_t launch_proj_rt(const ProjArgs& a, int L, uint32_t blocks,
 // the 16-bit kernel, and 16 wherever fewer would take more than 8 k-steps
 // each; every wavefront's steps loaded at once (proj_uses_p12 bounds the
 // steps by 16 x 8).
-template <int RT, int EPI, int W>
-static hipError_t launch_p12_w(const ProjArgs& a, uint32_t blocks, hipStream_t st) {
+template <int RT, int EPI, int W, bool CORR>
+static void launch_p12_c(const ProjArgs& a, uint32_t blocks, hipStream_t st) {
     const uint32_t spw = (a.steps + W - 1) / W;
     // the smallest variant that holds the steps (registers decide how many
     // 16-wavefront blocks a compute unit holds)
-    if (spw <= 2) proj_p12_kernel<RT, EPI, W, 2><<<blocks, 64 * W, 0, st>>>(a);
-    else if (spw <= 4) proj_p12_kernel<RT, EPI, W, 4><<<blocks, 64 * W, 0, st>>>(a);
-    else if (spw <= 6) proj_p12_kernel<RT, EPI, W, 6><<<blocks, 64 * W, 0, st>>>(a);
-    else proj_p12_kernel<RT, EPI, W, 8><<<blocks, 64 * W, 0, st>>>(a);
+    if (spw <= 2) proj_p12_kernel<RT, EPI, W, 2, CORR><<<blocks, 64 * W, 0, st>>>(a);
+    else if (spw <= 4) proj_p12_kernel<RT, EPI, W, 4, CORR><<<blocks, 64 * W, 0, st>>>(a);
+    else if (spw <= 6) proj_p12_kernel<RT, EPI, W, 6, CORR><<<blocks, 64 * W, 0, st>>>(a);
+    else proj_p12_kernel<RT, EPI, W, 8, CORR><<<blocks, 64 * W, 0, st>>>(a);
+}
+template <int RT, int EPI, int W>
+static hipError_t launch_p12_w(const ProjArgs& a, uint32_t blocks, hipStream_t st) {
+    if (a.corr0 || a.corr1)
+        launch_p12_c<RT, EPI, W, true>(a, blocks, st);
+    else
+        launch_p12_c<RT, EPI, W, false>(a, blocks, st);
     return hipGetLastError();
 }
 template <int RT, int EPI>

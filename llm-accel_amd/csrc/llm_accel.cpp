@@ -83,6 +83,10 @@ struct Matrix {
     // held in 12 bits only (no 16-bit copy, no byte planes) until a weight
     // outside [-2048, 2047] arrives (widen_matrix)
     bool p12_only = false;
+    // corrections of the 12-bit copy (kCorrSlots words per output row,
+    // allocated with the first weight outside 12 bits; see ProjArgs)
+    uint32_t* corr = nullptr;
+    bool corr_any = false;
     // gate <-> up and Q|K|V <-> O: read together (gate|up in one launch,
     // Q|K|V and O in the fused attention sublayer), so held in the same
     // layout
@@ -538,6 +542,9 @@ int widen_matrix(llm_ctx* c, Matrix& m) {
     const uint32_t S = m.steps;
     std::vector<uint8_t> pk((size_t)(m.n_pad / 4) * S * llm::kP12Step);
     HIP_TRY(hipMemcpy(pk.data(), m.p12, pk.size(), hipMemcpyDeviceToHost));
+    std::vector<uint32_t> cw(m.corr_any ? (size_t)m.n_pad * llm::kCorrSlots : 0);
+    if (m.corr_any)
+        HIP_TRY(hipMemcpy(cw.data(), m.corr, cw.size() * 4, hipMemcpyDeviceToHost));
     std::vector<int16_t> w((size_t)m.n * m.k);
     parallel_for(m.n, [&](uint32_t n) {
         const uint32_t b = n / 4, i = n % 4;
@@ -548,6 +555,15 @@ int widen_matrix(llm_ctx* c, Matrix& m) {
             std::memcpy(&word, rec + 512 + 4 * ln, 4);
             const uint32_t h = (word >> ((e & 1) * 16 + (e >> 1) * 4)) & 15;
             w[(size_t)n * m.k + k] = (int16_t)((int)(256 * h + rec[8 * ln + e]) - 2048);
+        }
+        // the weights the copy holds clamped
+        for (uint32_t q = 0; q < (cw.empty() ? 0u : llm::kCorrSlots); q++) {
+            const uint32_t e = cw[(size_t)n * llm::kCorrSlots + q];
+            const int32_t d = (int16_t)(e & 0xffff);
+            if (d) {
+                int16_t& v = w[(size_t)n * m.k + (e >> 16)];
+                v = (int16_t)(v + d);
+            }
         }
     });
     int rc;
@@ -561,6 +577,9 @@ int widen_matrix(llm_ctx* c, Matrix& m) {
     m.p12 = nullptr;
     m.p12_ok = false;
     m.p12_only = false;
+    if (m.corr && (rc = dev_free(c, m.corr))) return rc;
+    m.corr = nullptr;
+    m.corr_any = false;
     return 0;
 }
 
@@ -570,13 +589,53 @@ int upload_rows(llm_ctx* c, Matrix& m, uint32_t row0, uint32_t rows,
         return fail(LLM_E_ARG, "projection rows not aligned to 4");
     const uint32_t S = m.steps;
     int maxw = 0;
-    const std::vector<int16_t> buf = tile_rows(m, rows, w, &maxw);
+    std::vector<int16_t> buf = tile_rows(m, rows, w, &maxw);
     bool fits = true;
     for (size_t q = 0; fits && q < buf.size(); q++) fits = buf[q] >= -2048 && buf[q] <= 2047;
     int rc;
+    // A matrix held in 12 bits keeps rows with at most kCorrSlots weights
+    // outside the range: the copy holds them clamped and the row's
+    // correction words the differences (exact: the kernels add
+    // x[k] * delta to the row's sum).  More, and the matrix is widened.
+    std::vector<int16_t> clamped;
+    std::vector<uint32_t> cw;
     if (m.p12_only && !fits) {
-        if ((rc = widen_matrix(c, m))) return rc;
-        if (m.partner && m.partner->p12_only && (rc = widen_matrix(c, *m.partner))) return rc;
+        cw.assign((size_t)rows * llm::kCorrSlots, 0);
+        bool sparse = true;
+        for (uint32_t n = 0; sparse && n < rows; n++) {
+            uint32_t q = 0;
+            for (uint32_t k = 0; k < m.k; k++) {
+                const int v = w[(size_t)n * m.k + k];
+                if (v >= -2048 && v <= 2047) continue;
+                if (q == llm::kCorrSlots) {
+                    sparse = false;
+                    break;
+                }
+                const int d = v - std::clamp(v, -2048, 2047);
+                cw[(size_t)n * llm::kCorrSlots + q++] = (k << 16) | (uint16_t)(int16_t)d;
+            }
+        }
+        if (sparse) {
+            clamped.assign(w, w + (size_t)rows * m.k);
+            for (auto& v : clamped) v = (int16_t)std::clamp((int)v, -2048, 2047);
+            w = clamped.data();
+            buf = tile_rows(m, rows, w, nullptr);
+            fits = true;
+            if (!m.corr && (rc = dev_alloc(c, (void**)&m.corr,
+                                           (size_t)m.n_pad * llm::kCorrSlots * 4)))
+                return rc;
+            m.corr_any = true;
+        } else {
+            cw.clear();
+            if ((rc = widen_matrix(c, m))) return rc;
+            if (m.partner && m.partner->p12_only && (rc = widen_matrix(c, *m.partner))) return rc;
+        }
+    }
+    if (m.corr) {
+        // this part's rows: their corrections, or none
+        if (cw.empty()) cw.assign((size_t)rows * llm::kCorrSlots, 0);
+        HIP_TRY(hipMemcpy(m.corr + (size_t)row0 * llm::kCorrSlots, cw.data(), cw.size() * 4,
+                          hipMemcpyHostToDevice));
     }
     if (m.d)
         HIP_TRY(hipMemcpy(m.d + (size_t)(row0 / 4) * S * 512, buf.data(),
@@ -669,6 +728,8 @@ int check_layer_loaded(llm_ctx* c, uint32_t layer, bool attn, bool ffn) {
 // Matrix-core copies of the matrix (and of the up matrix for gate|up).
 void set_mf(const llm_ctx* c, llm::ProjArgs& a, const Matrix& m, const Matrix* m2 = nullptr) {
     a.mf_p12 = c->mf12;
+    a.corr0 = m.corr_any ? m.corr : nullptr;
+    if (m2) a.corr1 = m2->corr_any ? m2->corr : nullptr;
     a.mf_part = m.ctx_part;
     a.mf_count = m.ctx_count;
     a.mf0 = m.mf;
@@ -1635,6 +1696,7 @@ int enqueue_op_projection(llm_ctx* c, uint32_t layer, uint32_t proj, uint32_t T,
         a.ms0 += (size_t)2 * row0;
         a.nc = (uint32_t)cdiv(n, llm::kMfRows);
     }
+    if (m.corr_any) a.corr0 = m.corr + (size_t)row0 * llm::kCorrSlots;
     HIP_TRY(llm::launch_proj(a, llm::EPI_STORE, m.L, (uint32_t)cdiv(n, 4), c->stream));
     return 0;
 }
@@ -1989,6 +2051,7 @@ int llm_weight_bytes(llm_ctx_t* c, uint64_t* bytes, uint32_t* wide_matrices) {
         if (m.p12) b += m.elems() / 512 * llm::kP12Step;
         if (m.mf) b += (uint64_t)m.nc * m.kq * llm::kMfRecord;
         if (m.ms) b += (uint64_t)m.nc * llm::kMfRows * 2 * sizeof(int32_t);
+        if (m.corr) b += (uint64_t)m.n_pad * llm::kCorrSlots * 4;
     }
     *bytes = b;
     *wide_matrices = wide;

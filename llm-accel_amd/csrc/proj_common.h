@@ -87,6 +87,39 @@ __device__ __forceinline__ EpiIn epi_fetch(const ProjArgs& a, uint32_t r, uint32
     return e;
 }
 
+// Corrections of output (r, n) of a 12-bit copy with out-of-range weights
+// (ProjArgs::corr0 / corr1): the row's slot words, and the activations at
+// their columns -- as the kernel uses them: normalised on load for
+// EPI_STORE_NORM_IN.  corr_slots runs when the kernel starts; corr_inputs
+// in the epilogue, for rows that have a correction (XCOH: activations
+// written by other workgroups of the same launch, read device-coherently).
+struct CorrIn {
+    uint32_t e[kCorrSlots];
+    int32_t x[kCorrSlots];
+};
+__device__ __forceinline__ void corr_slots(const uint32_t* corr, uint32_t n, CorrIn& c) {
+    const uint4 s = *(const uint4*)(corr + (size_t)kCorrSlots * n);
+    c.e[0] = s.x, c.e[1] = s.y, c.e[2] = s.z, c.e[3] = s.w;
+}
+template <int EPI, bool XCOH>
+__device__ __forceinline__ void corr_inputs(const ProjArgs& a, uint32_t r, CorrIn& c) {
+#pragma unroll
+    for (int j = 0; j < (int)kCorrSlots; j++) {
+        const uint32_t k = c.e[j] >> 16;
+        const int16_t* px = a.x + (size_t)r * a.ldx + k;
+        int32_t x = XCOH ? ld_coherent(px) : *px;
+        if (EPI == EPI_STORE_NORM_IN) x = norm1(x, a.in_gain * a.in_gamma[k]);
+        c.x[j] = x;
+    }
+}
+// The exact correction sum_j x_j * delta_j (0 for unused words).
+__device__ __forceinline__ int64_t corr_sum(const CorrIn& c) {
+    int64_t s = 0;
+#pragma unroll
+    for (int j = 0; j < (int)kCorrSlots; j++) s += (int64_t)c.x[j] * (int16_t)(c.e[j] & 0xffffu);
+    return s;
+}
+
 // Output (r, n) of a projection from its exact sums (gate and up for
 // EPI_SILU): the reference's narrowing, then the epilogue.
 // COH: the output is read by other workgroups of the same launch, so it is
@@ -173,6 +206,8 @@ __device__ __forceinline__ bool proj_block(const ProjArgs& a, uint32_t b, int64_
     const bool eout = et < 4 * RT * NB && er < a.rows && en < a.n;
     EpiIn ei{0, 0, 0};
     if (eout) ei = epi_fetch<EPI>(a, er, en);
+    CorrIn cr = {};  // correction slots of a 12-bit copy (zero without)
+    if (P12 && a.corr0 && eout) corr_slots(a.corr0, en, cr);
     const uint32_t S = a.steps;
     const uint32_t s0 = wave * S / WPB, s1 = (wave + 1) * S / WPB;
     const uint32_t cnt = s1 - s0;  // <= SPW (the launcher's choice)
@@ -342,6 +377,11 @@ __device__ __forceinline__ bool proj_block(const ProjArgs& a, uint32_t b, int64_
         int64_t tot = 0;
 #pragma unroll
         for (int w = 0; w < WPB; w++) tot += red[((nb * WPB + w) * 4 + ii) * RT + er];
+        if (P12 && (cr.e[0] | cr.e[1] | cr.e[2] | cr.e[3]) != 0) {
+            // this row's activations at its correction columns
+            corr_inputs<EPI, XCOH>(a, er, cr);
+            tot += corr_sum(cr);
+        }
         proj_out<EPI, OCOH>(a, er, en, tot, tot, ei, nullptr);
     }
     return true;

@@ -105,48 +105,62 @@ def test_attention_mf12_matches_oracle(cfg, case):
                 assert first_mismatch(got, want[rows]) is None, f"mf12={mf12} rows={rows}"
 
 
-@pytest.mark.parametrize("case", ["fits", "down_outlier", "v_outlier", "gate_outlier"])
+def _dense(w):
+    """Five weights past 12 bits in one row: more than a row's corrections
+    hold."""
+    _extremes(w)
+    w[w.shape[0] // 3, 1:6] = 3000
+
+
+# case: (edits, matrices held in 16 bits, matrices with corrections)
+_IMAGE_CASES = {
+    "fits": ({}, [], []),
+    "down_outlier": ({6: _outlier}, [], ["down"]),
+    "v_outlier": ({2: _outlier}, [], ["qkv"]),
+    "gate_outlier": ({4: _outlier}, [], ["gate"]),
+    "dense_down": ({6: _dense}, ["down"], []),
+    "dense_v_after_q_outlier": ({0: _outlier, 2: _dense}, ["qkv", "o"], []),
+    "dense_up": ({5: _dense}, ["gate", "up"], []),
+}
+
+
+@pytest.mark.parametrize("case", list(_IMAGE_CASES))
 def test_single_weight_image(case):
     """Matrices whose weights fit 12 bits hold only the 12-bit copy and the
-    byte sums; a weight past 12 bits moves its matrix and the one read
-    with it (gate with up, Q|K|V with O) to the 16-bit tiles and byte
-    planes, rebuilt from what was loaded (V arrives after Q and K of the
-    same Q|K|V matrix).  Task 18 + 19 of 1, 2 and 8 rows must still equal
-    the oracle."""
+    byte sums.  Rows with at most 4 weights past 12 bits keep the image:
+    the copy holds the weights clamped and the row's correction words the
+    differences, which every 12-bit kernel adds exactly.  More in a row
+    moves the matrix and the one read with it (gate with up, Q|K|V with O)
+    to the 16-bit tiles and byte planes, rebuilt from what was loaded --
+    corrections included (V arrives after Q and K of the same Q|K|V
+    matrix).  Task 18 + 19 of 1, 2 and 8 rows must still equal the
+    oracle."""
     spec = workloads.CONFIG_A
     synth = workloads.SyntheticModel(spec, layers=1)
+    edits_p, wide_names, corr_names = _IMAGE_CASES[case]
     edits = {(0, p): _extremes for p in range(7)}
-    if case == "down_outlier":
-        edits[(0, 6)] = _outlier
-    if case == "v_outlier":
-        edits[(0, 2)] = _outlier
-    if case == "gate_outlier":
-        edits[(0, 4)] = _outlier
+    for p, fn in edits_p.items():
+        edits[(0, p)] = fn
     model = _Edited(synth, edits)
     om = oracle_from_synthetic(model, oracle_shape(spec, layers=1, max_seq=64))
-    dims = [spec.proj_dims(p) for p in range(7)]
-    qkv = (dims[0][0] + dims[1][0] + dims[2][0]) * spec.hidden
-    mats = {"qkv": qkv, "o": dims[3][0] * dims[3][1], "gate": dims[4][0] * dims[4][1],
-            "up": dims[5][0] * dims[5][1], "down": dims[6][0] * dims[6][1]}
     kpad = {"qkv": 256, "o": 256, "gate": 256, "up": 256, "down": 768}
     npad = {"qkv": 512, "o": 256, "gate": 688, "up": 688, "down": 256}
+    kq = {"qkv": 4, "o": 4, "gate": 4, "up": 4, "down": 11}
     rng = np.random.default_rng(17)
     with _accel(spec, {}, 64) as acc:
         acc.load_model(model)
         nbytes, wide = acc.weight_bytes()
-        wide_names = {"fits": [], "down_outlier": ["down"], "v_outlier": ["qkv", "o"],
-                      "gate_outlier": ["gate", "up"]}[case]
         want_bytes = 0
-        for name in mats:
+        for name in npad:
             elems = npad[name] * kpad[name]
-            nc, kq = -(-npad[name] // 16), -(-kpad[name] // 64)
-            if name == "down":
-                kq = -(-688 // 64)
+            nc = -(-npad[name] // 16)
             want_bytes += nc * 16 * 2 * 4
             if name in wide_names:
-                want_bytes += elems * 2 + nc * kq * 2048
+                want_bytes += elems * 2 + nc * kq[name] * 2048
             else:
                 want_bytes += elems // 512 * 768
+            if name in corr_names:
+                want_bytes += npad[name] * 4 * 4
         _say(f"case single image {case}: {nbytes} bytes, {wide} wide")
         assert wide == len(wide_names)
         assert nbytes == want_bytes

@@ -68,6 +68,37 @@ def test_projections_match_oracle(ctx, rows):
         assert err is None, f"projection op {op}: {err}"
 
 
+@pytest.mark.parametrize("rows", [1, 2, 5, 8])
+def test_projections_with_sparse_corrections(rows):
+    """Every projection with a few weights past 12 bits per matrix (at most
+    four in a row): the 12-bit images hold them clamped and the corrections
+    of their rows add the difference -- K and V as row ranges of the
+    Q|K|V matrix, so their corrections sit at an offset -- bit-exact
+    against the oracle's full-range projection."""
+    import llm_accel
+    spec = CONFIG_A_OPS
+    synth = workloads.SyntheticModel(spec, layers=1)
+    rng = np.random.default_rng(300 + rows)
+    for proj in range(7):
+        w = synth.weight(0, proj)
+        n, k = w.shape
+        for r in (0, n // 2, n - 1):
+            cols = rng.choice(k, size=4, replace=False)
+            w[r, cols] = rng.choice([-32768, -2049, 2048, 30000], size=4)
+    with llm_accel.Accelerator(accel_shape(spec, layers=1)) as acc:
+        acc.load_model(synth)
+        assert acc.weight_bytes()[1] == 0  # every matrix still in 12 bits
+        for proj in range(7):
+            op = llm_accel.OP_Q_PROJECTION + proj
+            out_dim, in_dim = spec.proj_dims(proj)
+            x = _ints(rng, (rows, in_dim), -32768, 32767)
+            _say(f"case corrections op={op} rows={rows}")
+            got = acc.run_feature(op, x)
+            want = orc.projection(x, synth.weight(0, proj))
+            err = first_mismatch(got, want)
+            assert err is None, f"projection op {op}: {err}"
+
+
 def test_projection_saturates_and_full_range(ctx):
     import llm_accel
     spec, synth, acc = ctx

@@ -9,7 +9,10 @@ every step, and from 8192 raw (2.0) up every product is widened.  A real
 checkpoint with one outlier takes the slower intervals, so this runs a P8
 block, two decode forwards and the LM head of a Qwen2.5-3B-shaped layer
 whose every matrix holds such weights, against the oracle, and checks that
-decode rows still take the fused attention sublayer.
+decode rows still take the fused attention sublayer -- on the 16-bit
+layout (LLM_ACCEL_P12=0: the widening intervals) and on the 12-bit images,
+where these few weights per row stay in the image clamped and their rows'
+sparse corrections add the difference.
 """
 import sys
 
@@ -38,10 +41,13 @@ def _plant(w, rng, value):
         w[rng.integers(0, n), rng.integers(0, k)] = value if rng.integers(0, 2) else -value
 
 
+@pytest.mark.parametrize("layout", ["16-bit", "12-bit"])
 @pytest.mark.parametrize("value,interval", [(32767, "per product"), (4095, "per step"),
                                             (1500, "four steps")])
-def test_outlier_weights_p8_decode_lm_head(value, interval):
+def test_outlier_weights_p8_decode_lm_head(value, interval, layout, monkeypatch):
     import llm_accel
+    if layout == "16-bit":
+        monkeypatch.setenv("LLM_ACCEL_P12", "0")
     spec = workloads.CONFIG_B
     max_seq = 64
     synth = workloads.SyntheticModel(spec, layers=1)
@@ -56,8 +62,10 @@ def test_outlier_weights_p8_decode_lm_head(value, interval):
     with llm_accel.Accelerator(accel_shape(spec, layers=1, max_seq=max_seq)) as acc:
         acc.load_model(synth)
         acc.load_lm_head(head)
+        if layout == "12-bit" and value > 2047:  # every matrix stays in 12 bits
+            assert acc.weight_bytes()[1] == 0
         for pos, rows in ((0, 8), (8, 1), (9, 1)):
-            _say(f"case outliers {value} ({interval}) pos={pos} rows={rows}")
+            _say(f"case outliers {value} ({interval}) {layout} pos={pos} rows={rows}")
             cur = hidden[pos:pos + rows]
             acc.upload(1, cur)
             acc.kernel_timing(True)
