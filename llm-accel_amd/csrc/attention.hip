@@ -737,8 +737,9 @@ constexpr uint32_t kSubQkvBlocks = LLM_SUB_QKV_NB;
 // workgroups of one block each, at the same measured time)
 constexpr uint32_t kSubOBlocks = 2;
 
-// P12: both projections read their 12-bit copies (qkv.p0, o.p0).
-template <int D, int RT, int QEPI, int LW, bool P12 = false>
+// P12: both projections read their 12-bit copies (qkv.p0, o.p0); CORR:
+// with their corrections.
+template <int D, int RT, int QEPI, int LW, bool P12 = false, bool CORR = false>
 __global__ __launch_bounds__(D * 2) void attention_sublayer_kernel(SublayerArgs s) {
     constexpr int WPB = D / 32, SPW = 4;
     constexpr uint32_t NBR = kSubQkvBlocks > kSubOBlocks ? kSubQkvBlocks : kSubOBlocks;
@@ -748,7 +749,7 @@ __global__ __launch_bounds__(D * 2) void attention_sublayer_kernel(SublayerArgs 
     uint32_t* const sync = s.sync;
     const uint32_t idx = blockIdx.x;
     if (idx < s.nq) {
-        proj_block<RT, QEPI, WPB, SPW, false, true, LW, kSubQkvBlocks, P12>(
+        proj_block<RT, QEPI, WPB, SPW, false, true, LW, kSubQkvBlocks, P12, CORR>(
             s.qkv, idx, red, [] { return true; });
         arrive(sync + kSyncStride * (idx % kSyncQkvLines));
         return;
@@ -768,7 +769,7 @@ __global__ __launch_bounds__(D * 2) void attention_sublayer_kernel(SublayerArgs 
         return;
     }
     const uint32_t b = idx - s.nq - s.na;
-    proj_block<RT, EPI_RESID, WPB, SPW, true, false, LW, kSubOBlocks, P12>(s.o, b, red, [&] {
+    proj_block<RT, EPI_RESID, WPB, SPW, true, false, LW, kSubOBlocks, P12, CORR>(s.o, b, red, [&] {
         return wait_counts(
             sync + kSyncAttn + kSyncStride * (b % kSyncAttnLines), 0, 1,
             [&](uint32_t) { return s.attn_base + s.na; }, s.wait_limit, sync + kSyncAbort, s.host_abort, &flag);
@@ -1544,7 +1545,7 @@ __global__ __launch_bounds__(D * 2) void attention_tile_fused_kernel(AttnArgs a)
 // workgroup) that issue their weight loads, wait for every (row, query
 // head) and finish with the residual and FFN-norm epilogue.  Launched only
 // when the whole grid is resident at once.
-template <int D, int RT, int LW, bool P12>
+template <int D, int RT, int LW, bool P12, bool CORR = false>
 __global__ __launch_bounds__(D * 2) void attention_tile_o_kernel(TileOArgs s) {
     constexpr int WPB = D / 32, SPW = 4;
     __shared__ union {
@@ -1565,7 +1566,7 @@ __global__ __launch_bounds__(D * 2) void attention_tile_o_kernel(TileOArgs s) {
         return;
     }
     const uint32_t b = blockIdx.x - s.ntile;
-    proj_block<RT, EPI_RESID, WPB, SPW, true, false, LW, kSubOBlocks, P12>(s.o, b, red, [&] {
+    proj_block<RT, EPI_RESID, WPB, SPW, true, false, LW, kSubOBlocks, P12, CORR>(s.o, b, red, [&] {
         return wait_counts(
             s.sync + kSyncAttn + kSyncStride * (b % kSyncAttnLines), 0, 1,
             [&](uint32_t) { return s.attn_base + s.arrivals; }, s.wait_limit, s.sync + kSyncAbort,
@@ -1659,7 +1660,7 @@ hipError_t launch_attention(const AttnArgs& a, uint32_t rows, uint32_t kv_heads,
 // launch.
 template <int D, int RT, int QEPI>
 static int sublayer_capacity_of(int cus) {
-    int per_cu[4] = {0, 0, 0, 0};
+    int per_cu[5] = {0, 0, 0, 0, 0};
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
             &per_cu[0], attention_sublayer_kernel<D, RT, QEPI, 4>, 2 * D, 0) != hipSuccess ||
         hipOccupancyMaxActiveBlocksPerMultiprocessor(
@@ -1667,9 +1668,12 @@ static int sublayer_capacity_of(int cus) {
         hipOccupancyMaxActiveBlocksPerMultiprocessor(
             &per_cu[2], attention_sublayer_kernel<D, RT, QEPI, 0>, 2 * D, 0) != hipSuccess ||
         hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &per_cu[3], attention_sublayer_kernel<D, RT, QEPI, 4, true>, 2 * D, 0) != hipSuccess)
+            &per_cu[3], attention_sublayer_kernel<D, RT, QEPI, 4, true>, 2 * D, 0) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &per_cu[4], attention_sublayer_kernel<D, RT, QEPI, 4, true, true>, 2 * D, 0) !=
+            hipSuccess)
         return 0;
-    return std::min({per_cu[0], per_cu[1], per_cu[2], per_cu[3]}) * cus;
+    return std::min({per_cu[0], per_cu[1], per_cu[2], per_cu[3], per_cu[4]}) * cus;
 }
 
 template <int D, int RT>
@@ -1713,13 +1717,13 @@ bool sublayer_fused_ok(const SublayerArgs& s, uint32_t rows, int qkv_epi, int L_
     return (int64_t)s.na + s.no < capacity;
 }
 
-template <int D, int RT, int LW, bool P12 = false>
+template <int D, int RT, int LW, bool P12 = false, bool CORR = false>
 static void launch_sub_l(const SublayerArgs& s, int qkv_epi, hipStream_t st) {
     const uint32_t grid = s.nq + s.na + s.no;
     if (qkv_epi == EPI_STORE_NORM_IN)
-        attention_sublayer_kernel<D, RT, EPI_STORE_NORM_IN, LW, P12><<<grid, 2 * D, 0, st>>>(s);
+        attention_sublayer_kernel<D, RT, EPI_STORE_NORM_IN, LW, P12, CORR><<<grid, 2 * D, 0, st>>>(s);
     else
-        attention_sublayer_kernel<D, RT, EPI_STORE, LW, P12><<<grid, 2 * D, 0, st>>>(s);
+        attention_sublayer_kernel<D, RT, EPI_STORE, LW, P12, CORR><<<grid, 2 * D, 0, st>>>(s);
 }
 
 bool sublayer_reads_p12(const SublayerArgs& s) {
@@ -1736,7 +1740,10 @@ bool sublayer_reads_p12(const SublayerArgs& s) {
 // 12-bit copies they never need to.
 template <int D, int RT>
 static void launch_sub(const SublayerArgs& s, int qkv_epi, int L, hipStream_t st) {
-    if (sublayer_reads_p12(s)) launch_sub_l<D, RT, 4, true>(s, qkv_epi, st);
+    if (sublayer_reads_p12(s) && (s.qkv.corr0 || s.o.corr0))
+        launch_sub_l<D, RT, 4, true, true>(s, qkv_epi, st);
+    else if (sublayer_reads_p12(s))
+        launch_sub_l<D, RT, 4, true>(s, qkv_epi, st);
     else if (L >= 4) launch_sub_l<D, RT, 4>(s, qkv_epi, st);
     else if (L >= 1) launch_sub_l<D, RT, 1>(s, qkv_epi, st);
     else launch_sub_l<D, RT, 0>(s, qkv_epi, st);
@@ -1754,7 +1761,7 @@ hipError_t launch_attention_sublayer(const SublayerArgs& s, uint32_t rows, int q
 // The smallest residency over the variants of the tile + O launch.
 template <int D, int RT>
 static int tile_o_capacity_of(int cus) {
-    int pc[4] = {0, 0, 0, 0};
+    int pc[5] = {0, 0, 0, 0, 0};
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
             &pc[0], attention_tile_o_kernel<D, RT, 4, false>, 2 * D, 0) != hipSuccess ||
         hipOccupancyMaxActiveBlocksPerMultiprocessor(
@@ -1762,9 +1769,11 @@ static int tile_o_capacity_of(int cus) {
         hipOccupancyMaxActiveBlocksPerMultiprocessor(
             &pc[2], attention_tile_o_kernel<D, RT, 0, false>, 2 * D, 0) != hipSuccess ||
         hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &pc[3], attention_tile_o_kernel<D, RT, 4, true>, 2 * D, 0) != hipSuccess)
+            &pc[3], attention_tile_o_kernel<D, RT, 4, true>, 2 * D, 0) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &pc[4], attention_tile_o_kernel<D, RT, 4, true, true>, 2 * D, 0) != hipSuccess)
         return 0;
-    return std::min({pc[0], pc[1], pc[2], pc[3]}) * cus;
+    return std::min({pc[0], pc[1], pc[2], pc[3], pc[4]}) * cus;
 }
 
 int tile_o_capacity(uint32_t head_dim, uint32_t rows, int cus) {
@@ -1797,7 +1806,9 @@ bool tile_o_prepare(TileOArgs& s, uint32_t rows, int capacity) {
 template <int D, int RT>
 static void launch_tile_o_d(const TileOArgs& s, int L, hipStream_t st) {
     const uint32_t grid = s.ntile + s.no;
-    if (s.o.p0)
+    if (s.o.p0 && s.o.corr0)
+        attention_tile_o_kernel<D, RT, 4, true, true><<<grid, 2 * D, 0, st>>>(s);
+    else if (s.o.p0)
         attention_tile_o_kernel<D, RT, 4, true><<<grid, 2 * D, 0, st>>>(s);
     else if (L >= 4)
         attention_tile_o_kernel<D, RT, 4, false><<<grid, 2 * D, 0, st>>>(s);

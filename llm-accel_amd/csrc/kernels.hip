@@ -180,8 +180,8 @@ __global__ __launch_bounds__(64 * WPB) void proj_kernel(ProjArgs a) {
             __shared__ uint32_t xs[WPB][SPW][RT][64];
 #pragma unroll
             for (int u = 0; u < SPW; u++) {
-                const int32_t glo = a.in_gain * (int16_t)(g2[u] & 0xffff);
-                const int32_t ghi = a.in_gain * (int16_t)(g2[u] >> 16);
+                const int32_t glo = __mul24(a.in_gain, (int16_t)(g2[u] & 0xffff));
+                const int32_t ghi = __mul24(a.in_gain, (int16_t)(g2[u] >> 16));
 #pragma unroll
                 for (int r = 0; r < RT; r++) {
                     const int32_t lo16 = norm1((int16_t)(x2[u][r] & 0xffff), glo);
@@ -398,8 +398,8 @@ __global__ __launch_bounds__(64 * WPB) void proj_p12_kernel(ProjArgs a) {
         __shared__ uint32_t xs[WPB][SPW][64];
 #pragma unroll
         for (int u = 0; u < SPW; u++) {
-            const int32_t lo16 = norm1((int16_t)(x2[u] & 0xffff), a.in_gain * (int16_t)(g2[u] & 0xffff));
-            const int32_t hi16 = norm1((int16_t)(x2[u] >> 16), a.in_gain * (int16_t)(g2[u] >> 16));
+            const int32_t lo16 = norm1((int16_t)(x2[u] & 0xffff), __mul24(a.in_gain, (int16_t)(g2[u] & 0xffff)));
+            const int32_t hi16 = norm1((int16_t)(x2[u] >> 16), __mul24(a.in_gain, (int16_t)(g2[u] >> 16)));
             xs[wave][u][lane] = (uint32_t)(uint16_t)lo16 | ((uint32_t)hi16 << 16);
         }
 #pragma unroll
@@ -561,12 +561,21 @@ __device__ __forceinline__ void mf_compute(const ProjArgs& a, const MfChunk<NM, 
                                            int32_t& rs) {
     v4u x0 = ch.x0, x1 = ch.x1;
     if (EPI == EPI_STORE_NORM_IN) {
-        const uint4 n0 = norm8(make_uint4(x0.x, x0.y, x0.z, x0.w),
-                               make_uint4(ch.g0.x, ch.g0.y, ch.g0.z, ch.g0.w), a.in_gain);
-        const uint4 n1 = norm8(make_uint4(x1.x, x1.y, x1.z, x1.w),
-                               make_uint4(ch.g1.x, ch.g1.y, ch.g1.z, ch.g1.w), a.in_gain);
-        x0 = v4u{n0.x, n0.y, n0.z, n0.w};
-        x1 = v4u{n1.x, n1.y, n1.z, n1.w};
+        // lanes i and i + 8 of a 16-lane row hold the same 16 inputs (the
+        // two byte planes of one activation row): lane i < 8 normalises the
+        // first 8, lane i + 8 the last 8, and they swap results (DPP row
+        // rotation by 8) -- half the normalisation work per lane
+        const v4u mx = hi_plane ? x0 : x1, mg = hi_plane ? ch.g0 : ch.g1;
+        const uint4 nm = norm8(make_uint4(mx.x, mx.y, mx.z, mx.w),
+                               make_uint4(mg.x, mg.y, mg.z, mg.w), a.in_gain);
+        const v4u mine = v4u{nm.x, nm.y, nm.z, nm.w};
+        v4u other;
+        other.x = (uint32_t)__builtin_amdgcn_update_dpp(0, (int32_t)mine.x, 0x128, 0xf, 0xf, false);
+        other.y = (uint32_t)__builtin_amdgcn_update_dpp(0, (int32_t)mine.y, 0x128, 0xf, 0xf, false);
+        other.z = (uint32_t)__builtin_amdgcn_update_dpp(0, (int32_t)mine.z, 0x128, 0xf, 0xf, false);
+        other.w = (uint32_t)__builtin_amdgcn_update_dpp(0, (int32_t)mine.w, 0x128, 0xf, 0xf, false);
+        x0 = hi_plane ? mine : other;
+        x1 = hi_plane ? other : mine;
     }
     // chunks past the wavefront's last (ok false) contribute zero
     // activations; the caller computes them anyway, so that no branch

@@ -1255,6 +1255,9 @@ int llm_ctx_create(const llm_shape_t* shape, int device, uint32_t num_pairs,
     }
     if (fx_recip(fx_sat16((int64_t)c->H * 256)) == 0)
         c->const_gain = fx_rmsnorm_gain(0, c->H);
+    // the fused norms form gain * gamma with 24-bit multiplies (the gain is
+    // 6623 raw); a gain beyond that keeps the separate norm kernel
+    if (c->const_gain >= (1 << 23)) c->const_gain = 0;
     *out = c;
     return 0;
 }

@@ -35,21 +35,24 @@ __device__ __forceinline__ uint4 and4(uint4 v, uint32_t m) {
 // One input normalised with a constant gain: rnd(x * gg, 16), gg = gain *
 // gamma (int32), in 32-bit arithmetic: with gg = 2^16 gh + gl (0 <= gl <
 // 2^16), floor((x gg + 2^15) / 2^16) = x gh + floor((x gl + 2^15) / 2^16)
-// exactly, |x gl + 2^15| < 2^31 for int16 x and |x gh| <= 2^30.
+// exactly, |x gl + 2^15| < 2^31 for int16 x and |x gh| <= 2^30.  Both
+// products have 24-bit operands (x 16 bits, gh and gl within 17), so they
+// use the full-rate 24-bit multiply.
 __device__ __forceinline__ int32_t norm1(int32_t x, int32_t gg) {
     const int32_t gh = gg >> 16, gl = gg & 0xffff;
-    const int32_t y = x * gh + ((x * gl + 32768) >> 16);
+    const int32_t y = __mul24(x, gh) + ((__mul24(x, gl) + 32768) >> 16);
     return y < -32768 ? -32768 : (y > 32767 ? 32767 : y);
 }
 // Eight inputs normalised with a constant gain: rnd(x * gain * gamma, 16);
-// columns >= cols have gamma 0 (the caller zeroes g there).
+// columns >= cols have gamma 0 (the caller zeroes g there).  The gain is
+// below 2^23 (the host guarantees it), so gain * gamma is a 24-bit product.
 __device__ __forceinline__ uint4 norm8(uint4 x, uint4 g, int32_t gain) {
     uint32_t w[4] = {x.x, x.y, x.z, x.w};
     const uint32_t gw[4] = {g.x, g.y, g.z, g.w};
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const int32_t lo = norm1((int16_t)(w[i] & 0xffff), gain * (int16_t)(gw[i] & 0xffff));
-        const int32_t hi = norm1((int16_t)(w[i] >> 16), gain * (int16_t)(gw[i] >> 16));
+        const int32_t lo = norm1((int16_t)(w[i] & 0xffff), __mul24(gain, (int16_t)(gw[i] & 0xffff)));
+        const int32_t hi = norm1((int16_t)(w[i] >> 16), __mul24(gain, (int16_t)(gw[i] >> 16)));
         w[i] = (uint32_t)(uint16_t)lo | ((uint32_t)hi << 16);
     }
     return make_uint4(w[0], w[1], w[2], w[3]);
@@ -108,7 +111,7 @@ __device__ __forceinline__ void corr_inputs(const ProjArgs& a, uint32_t r, CorrI
         const uint32_t k = c.e[j] >> 16;
         const int16_t* px = a.x + (size_t)r * a.ldx + k;
         int32_t x = XCOH ? ld_coherent(px) : *px;
-        if (EPI == EPI_STORE_NORM_IN) x = norm1(x, a.in_gain * a.in_gamma[k]);
+        if (EPI == EPI_STORE_NORM_IN) x = norm1(x, __mul24(a.in_gain, a.in_gamma[k]));
         c.x[j] = x;
     }
 }
@@ -190,10 +193,12 @@ __device__ __forceinline__ void silu_out_scalar(const ProjArgs& a, uint32_t r, u
 // the matrix's widening interval covers SPW steps), after every step (1)
 // or every product is widened (0).  P12: the weights are read from the
 // 12-bit copy a.p0 instead (layout and sums as proj_p12_kernel; int32
-// sums, SPW <= 32).  Returns false when wait() gave up (uniform over the
+// sums, SPW <= 32); CORR: that copy carries corrections (a.corr0; a
+// variant of its own, so that the common one holds no code or registers
+// for them).  Returns false when wait() gave up (uniform over the
 // workgroup).
 template <int RT, int EPI, int WPB, int SPW, bool XCOH, bool OCOH, int LW, int NB = 1,
-          bool P12 = false, typename Wait>
+          bool P12 = false, bool CORR = false, typename Wait>
 __device__ __forceinline__ bool proj_block(const ProjArgs& a, uint32_t b, int64_t* red,
                                            Wait&& wait) {
     static_assert(EPI != EPI_SILU, "one matrix per block");
@@ -207,7 +212,8 @@ __device__ __forceinline__ bool proj_block(const ProjArgs& a, uint32_t b, int64_
     EpiIn ei{0, 0, 0};
     if (eout) ei = epi_fetch<EPI>(a, er, en);
     CorrIn cr = {};  // correction slots of a 12-bit copy (zero without)
-    if (P12 && a.corr0 && eout) corr_slots(a.corr0, en, cr);
+    static_assert(!CORR || P12, "corrections belong to a 12-bit copy");
+    if (CORR && a.corr0 && eout) corr_slots(a.corr0, en, cr);  // a role's matrix may have none
     const uint32_t S = a.steps;
     const uint32_t s0 = wave * S / WPB, s1 = (wave + 1) * S / WPB;
     const uint32_t cnt = s1 - s0;  // <= SPW (the launcher's choice)
@@ -264,8 +270,8 @@ __device__ __forceinline__ bool proj_block(const ProjArgs& a, uint32_t b, int64_
         __shared__ uint32_t xs[WPB][SPW][RT][64];
 #pragma unroll
         for (int u = 0; u < SPW; u++) {
-            const int32_t glo = a.in_gain * (int16_t)(g2[u] & 0xffff);
-            const int32_t ghi = a.in_gain * (int16_t)(g2[u] >> 16);
+            const int32_t glo = __mul24(a.in_gain, (int16_t)(g2[u] & 0xffff));
+            const int32_t ghi = __mul24(a.in_gain, (int16_t)(g2[u] >> 16));
 #pragma unroll
             for (int r = 0; r < RT; r++) {
                 const int32_t lo16 = norm1((int16_t)(x2[u][r] & 0xffff), glo);
@@ -377,7 +383,7 @@ __device__ __forceinline__ bool proj_block(const ProjArgs& a, uint32_t b, int64_
         int64_t tot = 0;
 #pragma unroll
         for (int w = 0; w < WPB; w++) tot += red[((nb * WPB + w) * 4 + ii) * RT + er];
-        if (P12 && (cr.e[0] | cr.e[1] | cr.e[2] | cr.e[3]) != 0) {
+        if (CORR && (cr.e[0] | cr.e[1] | cr.e[2] | cr.e[3]) != 0) {
             // this row's activations at its correction columns
             corr_inputs<EPI, XCOH>(a, er, cr);
             tot += corr_sum(cr);
