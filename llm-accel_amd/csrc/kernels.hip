@@ -899,14 +899,33 @@ __global__ __launch_bounds__(64 * KS) void proj_mfma12_kernel(ProjArgs a, uint32
     for (int u = 0; u < PDS; u++) p12_step_load<NM, EPI>(a, src, xp, gp, step_s(u), ring[u]);
 #pragma unroll
     for (int u = 0; u < SM; u++) {
-        const P12Step<NM, EPI> cur = ring[u % PDS];
         const uint32_t s = step_s(u);
-        if (u + PDS < SM) p12_step_load<NM, EPI>(a, src, xp, gp, step_s(u + PDS), ring[u % PDS]);
+        P12Step<NM, EPI>& rg = ring[u % PDS];
+        P12Step<NM, EPI> cur;
+        // One matrix: step u's records into the slice first, so that the
+        // next step's loads reuse their registers (only the activations are
+        // kept; measured faster for down and Q|K|V).  Two (gate|up): the
+        // next step's loads first, while step u's are still in flight.
+        if (NM == 2) {
+            cur = rg;
+            if (u + PDS < SM) p12_step_load<NM, EPI>(a, src, xp, gp, step_s(u + PDS), rg);
+        }
 #pragma unroll
         for (int m = 0; m < NM; m++) {
-            *(v4i*)&my.lo[m][bw][o >> 3][16 * (o & 7)] = cur.r[m][0];
-            *(v4i*)&my.lo[m][bw][2 + (o >> 3)][16 * (o & 7)] = cur.r[m][1];
-            *(v4i*)&my.nb[m][bw][o >> 2][16 * (o & 3)] = cur.r[m][2];
+            const P12Step<NM, EPI>& sr = NM == 2 ? cur : rg;
+            *(v4i*)&my.lo[m][bw][o >> 3][16 * (o & 7)] = sr.r[m][0];
+            *(v4i*)&my.lo[m][bw][2 + (o >> 3)][16 * (o & 7)] = sr.r[m][1];
+            *(v4i*)&my.nb[m][bw][o >> 2][16 * (o & 3)] = sr.r[m][2];
+        }
+        if (NM == 1) {
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                cur.x0[h] = rg.x0[h];
+                cur.x1[h] = rg.x1[h];
+                cur.g0[h] = rg.g0[h];
+                cur.g1[h] = rg.g1[h];
+            }
+            if (u + PDS < SM) p12_step_load<NM, EPI>(a, src, xp, gp, step_s(u + PDS), rg);
         }
         // the reads below see other lanes' writes: the fences keep the
         // compiler from moving LDS accesses across (no instruction)
