@@ -57,6 +57,9 @@
 #ifndef LLM_MF12_WG_TARGET
 #define LLM_MF12_WG_TARGET 128  // 12-bit matrix-core kernel: split K below this many workgroups
 #endif
+#ifndef LLM_MF12_LONG_STEPS
+#define LLM_MF12_LONG_STEPS 64  // 12-bit matrix-core kernel: one matrix with at least this many
+#endif                          // k-steps (down) takes 16 wavefronts and >= 256 workgroups
 #ifndef LLM_MF12_PD1
 #define LLM_MF12_PD1 2      // 12-bit matrix-core kernel: k-steps of loads in flight, one matrix
 #endif
@@ -506,17 +509,23 @@ __global__ __launch_bounds__(64 * WPB) void proj_p12_kernel(ProjArgs a) {
 // ---------------------------------------------------------------------
 typedef int32_t v4i __attribute__((ext_vector_type(4)));
 
-// 16 int16 activations (two 16-byte loads) -> high bytes (hi_plane) or
-// biased low bytes, element e in byte e.
-__device__ __forceinline__ v4i split16(const v4u& x0, const v4u& x1, bool hi_plane) {
-    const uint32_t sel = hi_plane ? 0x07050301u : 0x06040200u;
-    const uint32_t bias = hi_plane ? 0u : 0x80808080u;
-    v4i r;
-    r.x = (int32_t)(__builtin_amdgcn_perm(x0.y, x0.x, sel) ^ bias);
-    r.y = (int32_t)(__builtin_amdgcn_perm(x0.w, x0.z, sel) ^ bias);
-    r.z = (int32_t)(__builtin_amdgcn_perm(x1.y, x1.x, sel) ^ bias);
-    r.w = (int32_t)(__builtin_amdgcn_perm(x1.w, x1.z, sel) ^ bias);
-    return r;
+// The A operand of lane i (< 16) of a row of lanes: 16 inputs of
+// activation row i & 7, its high bytes (i < 8) or biased low bytes
+// (i >= 8), element e in byte e.  Lane i holds inputs 0-7 of the 16, lane
+// i + 8 inputs 8-15 (one 16-byte load each): each lane forms both byte
+// planes of its 8 inputs and passes its partner's plane across (DPP row
+// rotation by 8 pairs lanes i and i + 8).
+__device__ __forceinline__ v4i plane16(const v4u& x, bool hi_plane) {
+    const uint32_t h0 = __builtin_amdgcn_perm(x.y, x.x, 0x07050301u);
+    const uint32_t h1 = __builtin_amdgcn_perm(x.w, x.z, 0x07050301u);
+    const uint32_t l0 = __builtin_amdgcn_perm(x.y, x.x, 0x06040200u) ^ 0x80808080u;
+    const uint32_t l1 = __builtin_amdgcn_perm(x.w, x.z, 0x06040200u) ^ 0x80808080u;
+    const int32_t r0 = __builtin_amdgcn_update_dpp(0, (int32_t)(hi_plane ? l0 : h0), 0x128, 0xf,
+                                                   0xf, false);
+    const int32_t r1 = __builtin_amdgcn_update_dpp(0, (int32_t)(hi_plane ? l1 : h1), 0x128, 0xf,
+                                                   0xf, false);
+    return hi_plane ? v4i{(int32_t)h0, (int32_t)h1, r0, r1}
+                    : v4i{r0, r1, (int32_t)l0, (int32_t)l1};
 }
 __device__ __forceinline__ int32_t byte_sum(const v4i& v, int32_t acc) {
     acc = __builtin_amdgcn_sdot4(v.x, 0x01010101, acc, false);
@@ -526,12 +535,13 @@ __device__ __forceinline__ int32_t byte_sum(const v4i& v, int32_t acc) {
 }
 
 // Operands of one K chunk as loaded: both weight planes per matrix, the
-// lane's 16 activations and, for EPI_STORE_NORM_IN, their 16 gammas.
+// lane's 8 activations (its half of the 16 of its A row) and, for
+// EPI_STORE_NORM_IN, their 8 gammas.
 template <int NM, int EPI>
 struct MfChunk {
     v4i bh[NM], bl[NM];
-    v4u x0, x1;
-    v4u g0, g1;
+    v4u xh;
+    v4u gh;
 };
 
 template <int NM, int EPI>
@@ -543,13 +553,11 @@ __device__ __forceinline__ void mf_load(const ProjArgs& a, const int8_t* const* 
         ch.bh[m] = *(const v4i*)(bp[m] + (size_t)q * kMfRecord);
         ch.bl[m] = *(const v4i*)(bp[m] + (size_t)q * kMfRecord + 1024);
     }
-    ch.x0 = *(const v4u*)(xp + 64 * q);
-    ch.x1 = *(const v4u*)(xp + 64 * q + 8);
+    ch.xh = *(const v4u*)(xp + 64 * q);
     if (EPI == EPI_STORE_NORM_IN) {
         // unconditional: the norm table is padded by a whole k-step, and
         // past in_cols the activations are 0 and so is the normalised value
-        ch.g0 = *(const v4u*)(gp + 64 * q);
-        ch.g1 = *(const v4u*)(gp + 64 * q + 8);
+        ch.gh = *(const v4u*)(gp + 64 * q);
     }
 }
 
@@ -559,29 +567,19 @@ template <int NM, int EPI>
 __device__ __forceinline__ void mf_compute(const ProjArgs& a, const MfChunk<NM, EPI>& ch,
                                            bool hi_plane, bool ok, v4i* c1, v4i* c2,
                                            int32_t& rs) {
-    v4u x0 = ch.x0, x1 = ch.x1;
+    v4u x = ch.xh;
     if (EPI == EPI_STORE_NORM_IN) {
-        // lanes i and i + 8 of a 16-lane row hold the same 16 inputs (the
-        // two byte planes of one activation row): lane i < 8 normalises the
-        // first 8, lane i + 8 the last 8, and they swap results (DPP row
-        // rotation by 8) -- half the normalisation work per lane
-        const v4u mx = hi_plane ? x0 : x1, mg = hi_plane ? ch.g0 : ch.g1;
-        const uint4 nm = norm8(make_uint4(mx.x, mx.y, mx.z, mx.w),
-                               make_uint4(mg.x, mg.y, mg.z, mg.w), a.in_gain);
-        const v4u mine = v4u{nm.x, nm.y, nm.z, nm.w};
-        v4u other;
-        other.x = (uint32_t)__builtin_amdgcn_update_dpp(0, (int32_t)mine.x, 0x128, 0xf, 0xf, false);
-        other.y = (uint32_t)__builtin_amdgcn_update_dpp(0, (int32_t)mine.y, 0x128, 0xf, 0xf, false);
-        other.z = (uint32_t)__builtin_amdgcn_update_dpp(0, (int32_t)mine.z, 0x128, 0xf, 0xf, false);
-        other.w = (uint32_t)__builtin_amdgcn_update_dpp(0, (int32_t)mine.w, 0x128, 0xf, 0xf, false);
-        x0 = hi_plane ? mine : other;
-        x1 = hi_plane ? other : mine;
+        // each lane normalises its own 8 inputs; lanes i and i + 8 then
+        // exchange byte planes of the normalised values
+        const uint4 nm = norm8(make_uint4(x.x, x.y, x.z, x.w),
+                               make_uint4(ch.gh.x, ch.gh.y, ch.gh.z, ch.gh.w), a.in_gain);
+        x = v4u{nm.x, nm.y, nm.z, nm.w};
     }
     // chunks past the wavefront's last (ok false) contribute zero
     // activations; the caller computes them anyway, so that no branch
     // separates a load from its use
     const int32_t keep = (int32_t)lane_mask(ok);
-    const v4i av = split16(x0, x1, hi_plane) & v4i{keep, keep, keep, keep};
+    const v4i av = plane16(x, hi_plane) & v4i{keep, keep, keep, keep};
     rs = byte_sum(av, rs);
 #pragma unroll
     for (int m = 0; m < NM; m++) {
@@ -766,9 +764,10 @@ __global__ __launch_bounds__(64 * KS) void proj_mfma_kernel(ProjArgs a, uint32_t
     const uint32_t n = q1 - q0;  // <= QM (the launcher's choice)
     const uint32_t i = lane & 15, g = lane >> 4;
     const bool hi_plane = i < 8;
-    // every activation buffer holds 8 rows: row i & 7 is always in bounds
-    const int16_t* xp = a.x + (size_t)(i & 7) * a.ldx + 16 * g;
-    const int16_t* gp = EPI == EPI_STORE_NORM_IN ? a.in_gamma + 16 * g : nullptr;
+    // every activation buffer holds 8 rows: row i & 7 is always in bounds;
+    // lane i holds inputs 8 (i / 8) .. + 7 of its 16
+    const int16_t* xp = a.x + (size_t)(i & 7) * a.ldx + 16 * g + 8 * (i >> 3);
+    const int16_t* gp = EPI == EPI_STORE_NORM_IN ? a.in_gamma + 16 * g + 8 * (i >> 3) : nullptr;
     const MfEpi<NM, EPI> fe = mf_epi_fetch<NM, EPI>(a, c);
     const int8_t* bp[NM];
     bp[0] = a.mf0 + (size_t)c * KQ * kMfRecord + lane * 16;
@@ -822,9 +821,9 @@ struct __attribute__((aligned(16))) P12Stage {
 
 template <int NM, int EPI>
 struct P12Step {
-    v4i r[NM][3];         // record bytes 16 (lane % 16) + {0, 256, 512}
-    v4u x0[2], x1[2];     // activations of the step's two K chunks
-    v4u g0[2], g1[2];     // their gammas (EPI_STORE_NORM_IN)
+    v4i r[NM][3];  // record bytes 16 (lane % 16) + {0, 256, 512}
+    v4u xh[2];     // the lane's 8 activations of the step's two K chunks
+    v4u gh[2];     // their gammas (EPI_STORE_NORM_IN)
 };
 
 template <int NM, int EPI>
@@ -840,12 +839,8 @@ __device__ __forceinline__ void p12_step_load(const ProjArgs& a, const uint8_t* 
     for (int h = 0; h < 2; h++) {
         // columns 128 s + 64 h + 16 (lane / 16) .. + 15 lie below the
         // activations' padded width (a whole number of 128-column steps)
-        st.x0[h] = *(const v4u*)(xp + 128 * s + 64 * h);
-        st.x1[h] = *(const v4u*)(xp + 128 * s + 64 * h + 8);
-        if (EPI == EPI_STORE_NORM_IN) {
-            st.g0[h] = *(const v4u*)(gp + 128 * s + 64 * h);
-            st.g1[h] = *(const v4u*)(gp + 128 * s + 64 * h + 8);
-        }
+        st.xh[h] = *(const v4u*)(xp + 128 * s + 64 * h);
+        if (EPI == EPI_STORE_NORM_IN) st.gh[h] = *(const v4u*)(gp + 128 * s + 64 * h);
     }
 }
 
@@ -859,8 +854,8 @@ __global__ __launch_bounds__(64 * KS) void proj_mfma12_kernel(ProjArgs a, uint32
     const uint32_t n = s1 - s0;  // <= SM (the launcher's choice)
     const uint32_t i = lane & 15, g = lane >> 4;
     const bool hi_plane = i < 8;
-    const int16_t* xp = a.x + (size_t)(i & 7) * a.ldx + 16 * g;
-    const int16_t* gp = EPI == EPI_STORE_NORM_IN ? a.in_gamma + 16 * g : nullptr;
+    const int16_t* xp = a.x + (size_t)(i & 7) * a.ldx + 16 * g + 8 * (i >> 3);
+    const int16_t* gp = EPI == EPI_STORE_NORM_IN ? a.in_gamma + 16 * g + 8 * (i >> 3) : nullptr;
     const MfEpi<NM, EPI> fe = mf_epi_fetch<NM, EPI>(a, c);
     // load lanes: block 4c + lane / 16, clamped to the copy's last block
     // (rows past n reach only outputs that are never written)
@@ -920,10 +915,8 @@ __global__ __launch_bounds__(64 * KS) void proj_mfma12_kernel(ProjArgs a, uint32
         if (NM == 1) {
 #pragma unroll
             for (int h = 0; h < 2; h++) {
-                cur.x0[h] = rg.x0[h];
-                cur.x1[h] = rg.x1[h];
-                cur.g0[h] = rg.g0[h];
-                cur.g1[h] = rg.g1[h];
+                cur.xh[h] = rg.xh[h];
+                cur.gh[h] = rg.gh[h];
             }
             if (u + PDS < SM) p12_step_load<NM, EPI>(a, src, xp, gp, step_s(u + PDS), rg);
         }
@@ -943,10 +936,8 @@ __global__ __launch_bounds__(64 * KS) void proj_mfma12_kernel(ProjArgs a, uint32
                 ch.bl[m] = lo ^ v4i{(int32_t)0x80808080u, (int32_t)0x80808080u,
                                     (int32_t)0x80808080u, (int32_t)0x80808080u};
             }
-            ch.x0 = cur.x0[h];
-            ch.x1 = cur.x1[h];
-            ch.g0 = cur.g0[h];
-            ch.g1 = cur.g1[h];
+            ch.xh = cur.xh[h];
+            ch.gh = cur.gh[h];
             // a half past the matrix's K chunks (odd kq) adds nothing
             mf_compute<NM, EPI>(a, ch, hi_plane, (uint32_t)u < n && 2 * s + h < KQ, c1, c2, rs);
         }
@@ -1212,11 +1203,19 @@ static hipError_t launch_mfma_q(const ProjArgs& a, uint32_t parts, hipStream_t s
 // way: wavefronts keep at least one step, at most LLM_MF_QMAX / 2.  Two
 // matrices (gate|up) take fewer wavefronts per workgroup below 4 steps
 // each: more workgroups resident (measured faster at K = 2048; slower for
-// one matrix, and for K = 11008).
+// one matrix, and for K = 11008).  One matrix with a long K (down, K =
+// 11008) takes 16 wavefronts of ~3 steps over at least 256 workgroups
+// (P8 down 11.5 -> 11.1 us against 8 wavefronts of ~6 steps over 128
+// chunks x 2; Q|K|V and O, K = 2048, are slower so).
 MfSplit mf12_split(uint32_t nc, uint32_t steps, uint32_t nm) {
     MfSplit s{LLM_MF12_KS, 1};
+    uint32_t target = LLM_MF12_WG_TARGET;
     while (nm == 2 && s.ks > 4 && steps < LLM_MF12_MIN_STEPS * s.ks) s.ks /= 2;
-    while (nc * s.parts < LLM_MF12_WG_TARGET && steps / (s.parts * 2) >= s.ks) s.parts *= 2;
+    if (nm == 1 && steps >= LLM_MF12_LONG_STEPS) {
+        s.ks = 16;
+        target = 256;
+    }
+    while (nc * s.parts < target && steps / (s.parts * 2) >= s.ks) s.parts *= 2;
     while (mf_chunks_per_wave(steps, s.parts, s.ks) > LLM_MF_QMAX / 2) s.parts *= 2;
     return s;
 }

@@ -1238,9 +1238,13 @@ int llm_ctx_create(const llm_shape_t* shape, int device, uint32_t num_pairs,
             const Matrix& mt = c->mat(0, m);
             // either kernel of the matrix-core path
             const uint32_t nm = (m == M_GATE || m == M_UP) ? 2 : 1;
-            const uint32_t parts = std::max(llm::mf_split(mt.nc, mt.kq).parts,
-                                            llm::mf12_split(mt.nc, mt.steps, nm).parts);
-            words = std::max(words, (size_t)mt.nc * parts * llm::mf_part_words(nm));
+            // the operator-level commands launch row ranges of a matrix,
+            // whose fewer chunks may split K into more parts
+            for (uint32_t n2 = 1; n2 <= mt.nc; n2++) {
+                const uint32_t parts = std::max(llm::mf_split(n2, mt.kq).parts,
+                                                llm::mf12_split(n2, mt.steps, nm).parts);
+                words = std::max(words, (size_t)n2 * parts * llm::mf_part_words(nm));
+            }
             chunks = std::max(chunks, (size_t)mt.nc);
         }
         if ((rc = dev_alloc(c, (void**)&c->mf_part, words * 4)) ||
