@@ -1011,11 +1011,14 @@ struct __attribute__((aligned(16))) TileScoresSmem {
 template <int D>
 struct __attribute__((aligned(16))) TilePvSmem {
     static constexpr int NWH = D / 32;
+    static constexpr int NTH = 2 * D;
     int16_t kv[8][D];                     // the block's V rows
     int16_t p[NWH][TILE], cp[NWH][TILE];  // per wavefront: probabilities, c(p)
     int16_t e14[2056];                    // Q2.14 exp table
     uint32_t last;
     int32_t m0;                           // one-launch path: running max before the tile
+    int32_t rsum;                         // the recurrence's final sum
+    int32_t fac[NTH / 64][64];            // per wavefront: a piece's rescale factors
     union __attribute__((aligned(16))) {
         int16_t scr[NWH][SLICE_SCRATCH];  // per wavefront: slice transposes
         struct {                          // then the recurrence operands of up
@@ -1395,11 +1398,11 @@ __device__ __forceinline__ void tile_pv_phase(const AttnArgs& a, const TileWg& w
         if (!arrive_last(top + (1 + grp) * kCounterStride, in_grp, &sm.last)) return;
         if (!arrive_last(top, tile_groups(ntiles), &sm.last)) return;
     }
-    // A tile whose maximum does not raise the running max has factor
-    // exp(0) = 1.0 (rnd(v * 2^16, 16) = v): sum and acc take saturating
-    // 32-bit additions of exact int32 terms.  Steps padded with (maximum
-    // -128, sum 0, value 0) change nothing.
+    // Steps padded with (maximum INT16_MIN, sum 0, value 0) change
+    // nothing.
     int32_t m = INT16_MIN, sum = 0, acc = 0;
+    constexpr uint32_t kElemWaves = (D + 63) / 64;         // wavefronts holding elements
+    constexpr bool kSumWave = NTH / 64 > kElemWaves;       // one more for the sum
     constexpr int PL = 64 * D / 4 / NTH;  // 4-value groups per thread per piece
     // A piece's operands are loaded while the previous piece is computed.
     struct Piece {
@@ -1444,47 +1447,73 @@ __device__ __forceinline__ void tile_pv_phase(const AttnArgs& a, const TileWg& w
         }
         if (j0 + 64 < ntiles) load_piece(j0 + 64, cur);
         lds_barrier();
+        // The same for every element, formed by every wavefront with all
+        // its lanes: lane j holds tile j0 + j's maximum, the running
+        // max before it (the max of m and the earlier maxima) and the
+        // tile's rescale factor: exp(before - after) << 2 where the tile
+        // raises the max, else 65536 (1.0), under which rnd(v * 2^16, 16) =
+        // v leaves sum and acc as they are.
+        const int32_t tmj = sm.tmax[lane];
+        const int32_t before = wave_prefix_max_excl(tmj, m);
+        const bool rise = tmj > before;
+        // (lanes that do not rise look up exp(0): the table holds x <= 0)
+        const int32_t pj = (int32_t)prob(sm.e14, rise ? before - tmj : 0) << 2;
+        const int32_t fj = rise ? pj : 65536;
+        m = max(m, wave_max(tmj));
+        // Every tile the same straight-line step, the reference's per-tile
+        // order and rounding, in full-rate 24-bit products: with v = 2^16 h
+        // + l (l the low 16 bits) and f <= 2^16, rnd(v f, 16) = h f +
+        // ((l f + 2^15) >> 16) exactly, |h f| <= 2^31 and l f < 2^32 - 2^15;
+        // the rescaled acc stays within int32 (|v f / 2^16| <= |v|), and
+        // every term of sum is non-negative, so its saturation is that of
+        // nested saturating additions.  The factors go through LDS (a
+        // wavefront's own copy: its LDS operations complete in order).  The
+        // sum, the same for every element, is carried by the first
+        // wavefront past the element lanes where the workgroup has one.
+        sm.fac[w][lane] = fj;
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        auto rescale = [](int32_t v, int32_t f) -> int32_t {
+            const uint32_t lo = (__umul24((uint32_t)v & 0xffffu, (uint32_t)f) + 32768u) >> 16;
+            return __mul24(v >> 16, f) + (int32_t)lo;
+        };
+        auto sum_step = [&](int32_t sv, int32_t f, int32_t tk) -> int32_t {
+            const uint32_t lo = (__umul24((uint32_t)sv & 0xffffu, (uint32_t)f) + 32768u) >> 16;
+            return __builtin_elementwise_add_sat(
+                __builtin_elementwise_add_sat(__mul24(sv >> 16, f), tk << 2), (int32_t)lo);
+        };
         if (tid < D) {
             for (uint32_t j = 0; j < nj; j += 8) {
-                int32_t tmv[8], tsk[8], tvv[8];
+                int32_t tvv[8], fv[8], tk[8];
 #pragma unroll
                 for (int u = 0; u < 8; u++) {
-                    tmv[u] = sm.tmax[j + u];
-                    tsk[u] = sm.tsum[j + u];
                     tvv[u] = sm.tv[j + u][tid];
-                }
-                // Eight tiles none of which raises the running max, with sum
-                // and every lane's acc far enough from the int32 bounds that
-                // eight terms (sum: tile sums << 2 <= 2^22 each; acc: tile
-                // values << 8 <= 2^23 each) cannot saturate: one addition.
-                int32_t mx8 = tmv[0];
-#pragma unroll
-                for (int u = 1; u < 8; u++) mx8 = tmv[u] > mx8 ? tmv[u] : mx8;
-                const bool flat = __builtin_amdgcn_readfirstlane(mx8) <= m &&
-                                  sum <= INT32_MAX - (8 << 22) &&
-                                  __all(acc <= INT32_MAX - (8 << 23) && acc >= INT32_MIN + (8 << 23));
-                if (flat) {
-                    int32_t ts = 0, tvs = 0;
-#pragma unroll
-                    for (int u = 0; u < 8; u++) ts += tsk[u], tvs += tvv[u];
-                    sum += ts << 2;
-                    acc += tvs * 256;
-                    continue;
+                    fv[u] = sm.fac[w][j + u];
+                    if (!kSumWave) tk[u] = sm.tsum[j + u];
                 }
 #pragma unroll
                 for (int u = 0; u < 8; u++) {
-                    if (tmv[u] > m) {  // the running max moves: rescale
-                        const int64_t old = (int64_t)prob(sm.e14, m - tmv[u]) << 2;
-                        sum = fx_sat32(fx_rnd((int64_t)sum * old + ((int64_t)tsk[u] << 18), 16));
-                        acc = fx_sat32(fx_rnd((int64_t)acc * old, 16));
-                        m = tmv[u];
-                    } else {
-                        sum = __builtin_elementwise_add_sat(sum, tsk[u] << 2);
-                    }
-                    acc = __builtin_elementwise_add_sat(acc, tvv[u] * 256);
+                    if (!kSumWave) sum = sum_step(sum, fv[u], tk[u]);
+                    acc = __builtin_elementwise_add_sat(rescale(acc, fv[u]), tvv[u] * 256);
                 }
             }
+        } else if (kSumWave && w == kElemWaves) {
+            for (uint32_t j = 0; j < nj; j += 8) {
+                int32_t fv[8], tk[8];
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    fv[u] = sm.fac[w][j + u];
+                    tk[u] = sm.tsum[j + u];
+                }
+#pragma unroll
+                for (int u = 0; u < 8; u++) sum = sum_step(sum, fv[u], tk[u]);
+            }
         }
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");  // fac read before the next piece
+    }
+    if (kSumWave) {
+        if (w == kElemWaves && lane == 0) sm.rsum = sum;
+        lds_barrier();
+        sum = sm.rsum;
     }
     if (tid < D) {
         const int16_t o = fx_sat16(fx_rnd((int64_t)acc * fx_inv_sum(sum), 16));

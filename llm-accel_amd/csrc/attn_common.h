@@ -113,6 +113,20 @@ __device__ __forceinline__ int32_t wave_sum(int32_t v) {
     v += dpp<0x143, 0xc>(0, v);
     return __builtin_amdgcn_readlane(v, 63);
 }
+// Maximum of `first` and the values of the lanes below each lane (lane 0:
+// first alone): the lanes shifted up by one (wave_shr:1, lane 0 takes
+// `first`), then an inclusive scan within rows of 16 (row_shr 1, 2, 4, 8;
+// lanes without a source keep INT32_MIN) and across them (row_bcast).
+__device__ __forceinline__ int32_t wave_prefix_max_excl(int32_t v, int32_t first) {
+    v = __builtin_amdgcn_update_dpp(first, v, 0x138, 0xf, 0xf, false);  // wave_shr:1
+    v = max(v, dpp<0x111, 0xf>(INT32_MIN, v));  // row_shr:1
+    v = max(v, dpp<0x112, 0xf>(INT32_MIN, v));  // row_shr:2
+    v = max(v, dpp<0x114, 0xf>(INT32_MIN, v));  // row_shr:4
+    v = max(v, dpp<0x118, 0xf>(INT32_MIN, v));  // row_shr:8
+    v = max(v, dpp<0x142, 0xa>(INT32_MIN, v));  // row_bcast:15 -> rows 1, 3
+    v = max(v, dpp<0x143, 0xc>(INT32_MIN, v));  // row_bcast:31 -> rows 2, 3
+    return v;
+}
 
 // (x0, x1) rotated by the Q8.8 table entry (c, s) (host:4765-4788).  The
 // table holds quantised cos / sin, |c|, |s| <= 256, so the sums fit int32.
