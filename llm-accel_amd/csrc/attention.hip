@@ -1017,7 +1017,7 @@ struct __attribute__((aligned(16))) TilePvSmem {
     int16_t e14[2056];                    // Q2.14 exp table
     uint32_t last;
     int32_t m0;                           // one-launch path: running max before the tile
-    int32_t rsum;                         // the recurrence's final sum
+    int32_t rinv;                         // 1 / the recurrence's final sum
     int32_t fac[NTH / 64][64];            // per wavefront: a piece's rescale factors
     union __attribute__((aligned(16))) {
         int16_t scr[NWH][SLICE_SCRATCH];  // per wavefront: slice transposes
@@ -1185,8 +1185,8 @@ __device__ __forceinline__ void tile_scores_phase(const AttnArgs& a, const TileW
                             ((int32_t)s2 == INT32_MIN ? INT32_MAX : (int32_t)s2) +
                             ((int32_t)s3 == INT32_MIN ? INT32_MAX : (int32_t)s3);
         int32_t ts = fx_sat32(t64);
-        ts = fx_sat32(fx_rnd((int64_t)ts * scale, 16));
-        const int32_t s = valid ? fx_sat16(fx_rnd(ts, 8)) : INT16_MIN;
+        ts = rnd16_mul(ts, (int32_t)scale);  // scale = qk_scale << 8 <= 2^16
+        const int32_t s = valid ? sat16_32(rnd32(ts, 8)) : INT16_MIN;
         const size_t base = (((size_t)t * a.num_kv_heads + h) * a.max_tiles + tile) * G + gi;
         const int32_t mx = wave_max(s);
         if (FUSED) {
@@ -1363,8 +1363,7 @@ __device__ __forceinline__ void tile_pv_phase(const AttnArgs& a, const TileWg& w
     b2 += __shfl_xor(b2, 32, 64);
     b3 += __shfl_xor(b3, 32, 64);
     int32_t tv = fx_sat32((int64_t)b0 + b1 + b2 + b3);
-    tv = fx_sat32(fx_rnd((int64_t)tv * 1024, 16));
-    tv = fx_sat16(fx_rnd(tv, 8));
+    tv = sat16_32(rnd32(rnd32(tv, 6), 8));  // rnd(tv 2^10, 16) = rnd(tv, 6)
     {  // elements e..e+3 in one 8-byte store (lane % 4 == 0 of each half-wave)
         const uint32_t t1 = (uint16_t)__shfl_down(tv, 1, 64), t2 = (uint16_t)__shfl_down(tv, 2, 64),
                        t3 = (uint16_t)__shfl_down(tv, 3, 64);
@@ -1472,10 +1471,6 @@ __device__ __forceinline__ void tile_pv_phase(const AttnArgs& a, const TileWg& w
         // wavefront past the element lanes where the workgroup has one.
         sm.fac[w][lane] = fj;
         __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-        auto rescale = [](int32_t v, int32_t f) -> int32_t {
-            const uint32_t lo = (__umul24((uint32_t)v & 0xffffu, (uint32_t)f) + 32768u) >> 16;
-            return __mul24(v >> 16, f) + (int32_t)lo;
-        };
         auto sum_step = [&](int32_t sv, int32_t f, int32_t tk) -> int32_t {
             const uint32_t lo = (__umul24((uint32_t)sv & 0xffffu, (uint32_t)f) + 32768u) >> 16;
             return __builtin_elementwise_add_sat(
@@ -1493,7 +1488,7 @@ __device__ __forceinline__ void tile_pv_phase(const AttnArgs& a, const TileWg& w
 #pragma unroll
                 for (int u = 0; u < 8; u++) {
                     if (!kSumWave) sum = sum_step(sum, fv[u], tk[u]);
-                    acc = __builtin_elementwise_add_sat(rescale(acc, fv[u]), tvv[u] * 256);
+                    acc = __builtin_elementwise_add_sat(rnd16_mul(acc, fv[u]), tvv[u] * 256);
                 }
             }
         } else if (kSumWave && w == kElemWaves) {
@@ -1510,13 +1505,18 @@ __device__ __forceinline__ void tile_pv_phase(const AttnArgs& a, const TileWg& w
         }
         __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");  // fac read before the next piece
     }
+    // 1 / sum (a division) on the sum's wavefront, beside the elements'
+    // chains
+    int32_t inv;
     if (kSumWave) {
-        if (w == kElemWaves && lane == 0) sm.rsum = sum;
+        if (w == kElemWaves && lane == 0) sm.rinv = fx_inv_sum(sum);
         lds_barrier();
-        sum = sm.rsum;
+        inv = sm.rinv;
+    } else {
+        inv = fx_inv_sum(sum);
     }
     if (tid < D) {
-        const int16_t o = fx_sat16(fx_rnd((int64_t)acc * fx_inv_sum(sum), 16));
+        const int16_t o = sat16_32(rnd16_mul(acc, inv));  // 0 <= inv < 2^15
         int16_t* op = &a.out[(size_t)t * a.ldo + (size_t)g * D + tid];
         if (OARR)
             st_coherent(op, o);

@@ -231,8 +231,8 @@ __device__ __forceinline__ void gqa_scores_body(const AttnArgs& a, const GqaWg& 
                             (b2 == INT32_MIN ? INT32_MAX : b2) +
                             (b3 == INT32_MIN ? INT32_MAX : b3);
         int32_t ts = fx_sat32(t64);
-        ts = fx_sat32(fx_rnd((int64_t)ts * scale, 16));
-        const int32_t s = valid ? fx_sat16(fx_rnd(ts, 8)) : INT16_MIN;
+        ts = rnd16_mul(ts, (int32_t)scale);  // scale = qk_scale << 8 <= 2^16
+        const int32_t s = valid ? sat16_32(rnd32(ts, 8)) : INT16_MIN;
         const size_t base = (((size_t)t * a.num_kv_heads + h) * a.max_tiles + tile) * G + gi;
         const int32_t mx = wave_max(s);
         if (FUSED) {
@@ -480,8 +480,7 @@ __device__ __forceinline__ bool gqa_pv_body(const AttnArgs& a, const GqaWg& wg,
             }
         }
         int32_t tv = fx_sat32((int64_t)b0 + b1 + b2 + b3);
-        tv = fx_sat32(fx_rnd((int64_t)tv * 1024, 16));
-        tv = fx_sat16(fx_rnd(tv, 8));
+        tv = sat16_32(rnd32(rnd32(tv, 6), 8));  // rnd(tv 2^10, 16) = rnd(tv, 6)
         if (SCAN)
             sm.tv[gi][e] = (int16_t)tv;
         else
@@ -875,7 +874,7 @@ __device__ __forceinline__ void gqa_scan_body(const AttnArgs& a, GqaScanSmem& sm
     lds_barrier();  // the sum
     if (tid < GSE)
         a.out[(size_t)t * a.ldo + (size_t)g * D + GSE * es + tid] =
-            fx_sat16(fx_rnd((int64_t)acc * fx_inv_sum(sm.sum), 16));
+            sat16_32(rnd16_mul(acc, fx_inv_sum(sm.sum)));
 }
 
 template <int D>

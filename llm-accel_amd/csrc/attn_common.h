@@ -75,6 +75,23 @@ __device__ __forceinline__ v4u clamp4(v4u v, uint32_t& any) {
     return r;
 }
 
+// rnd(v * f, 16) for 0 <= f <= 2^16, exactly, in full-rate 24-bit
+// products: with v = 2^16 h + l (l the low 16 bits), rnd(v f, 16) = h f +
+// ((l f + 2^15) >> 16); |h f| <= 2^31, l f + 2^15 < 2^32, and the result
+// lies within |v| (a dependent 64-bit multiply-add costs ~100 cycles).
+__device__ __forceinline__ int32_t rnd16_mul(int32_t v, int32_t f) {
+    const uint32_t lo = (__umul24((uint32_t)v & 0xffffu, (uint32_t)f) + 32768u) >> 16;
+    return __mul24(v >> 16, f) + (int32_t)lo;
+}
+// rnd(v, s) of an int32 in 32-bit arithmetic: floor(v / 2^s) plus the
+// carry of the dropped bits and the half.
+__device__ __forceinline__ int32_t rnd32(int32_t v, int s) {
+    return (v >> s) + (int32_t)((((uint32_t)v & ((1u << s) - 1u)) + (1u << (s - 1))) >> s);
+}
+__device__ __forceinline__ int16_t sat16_32(int32_t v) {
+    return (int16_t)(v < INT16_MIN ? INT16_MIN : (v > INT16_MAX ? INT16_MAX : v));
+}
+
 __device__ __forceinline__ int16_t prob(const int16_t* exp14, int32_t x) {
     x = fx_sat16(x);
     x = x < -2048 ? -2048 : x;

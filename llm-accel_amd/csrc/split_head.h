@@ -274,8 +274,8 @@ __device__ __forceinline__ bool split_head_body(const AttnArgs& a, uint32_t t, u
                             ((int32_t)s2 == INT32_MIN ? INT32_MAX : (int32_t)s2) +
                             ((int32_t)s3 == INT32_MIN ? INT32_MAX : (int32_t)s3);
         int32_t ts32 = fx_sat32(t64);
-        ts32 = fx_sat32(fx_rnd((int64_t)ts32 * scale, 16));
-        const int32_t s = valid ? fx_sat16(fx_rnd(ts32, 8)) : INT16_MIN;
+        ts32 = rnd16_mul(ts32, (int32_t)scale);  // scale = qk_scale << 8 <= 2^16
+        const int32_t s = valid ? sat16_32(rnd32(ts32, 8)) : INT16_MIN;
         // ---- softmax state (the same in every wavefront) ----
         const int32_t wm = wave_max(s);
         const int32_t mn = wm > m ? wm : m;
@@ -284,9 +284,11 @@ __device__ __forceinline__ bool split_head_body(const AttnArgs& a, uint32_t t, u
         sm.p[w][paired(lane)] = (int16_t)pr;
         sm.cp[w][paired(lane)] = (int16_t)sat_corr(pr);
         const int32_t tsum = wave_sum(pr);  // <= 64 * 16384
-        sum = fx_sat32(fx_rnd((int64_t)sum * ((int64_t)old << 2) + ((int64_t)tsum << 18), 16));
+        // (old << 2 <= 2^16; sum and its terms are non-negative, so the
+        // saturation of the rounded sum is that of nested saturating adds)
+        sum = __builtin_elementwise_add_sat(rnd16_mul(sum, old << 2), tsum << 2);
         m = mn;
-        if (old != 16384) acc = fx_sat32(fx_rnd((int64_t)acc * ((int64_t)old << 2), 16));
+        if (old != 16384) acc = rnd16_mul(acc, old << 2);
         // ---- PV over half hh of the tile for element e ----
         v4u vr[4];
         slice_v_rows(sm.scr[w], cur, lane, vr);
@@ -333,13 +335,12 @@ __device__ __forceinline__ bool split_head_body(const AttnArgs& a, uint32_t t, u
         b2 += __shfl_xor(b2, 32, 64);
         b3 += __shfl_xor(b3, 32, 64);
         int32_t tv = fx_sat32((int64_t)b0 + b1 + b2 + b3);
-        tv = fx_sat32(fx_rnd((int64_t)tv * 1024, 16));
-        tv = fx_sat16(fx_rnd(tv, 8));
-        acc = fx_sat32((int64_t)acc + ((int64_t)tv << 8));
+        tv = sat16_32(rnd32(rnd32(tv, 6), 8));  // rnd(tv 2^10, 16) = rnd(tv, 6)
+        acc = __builtin_elementwise_add_sat(acc, tv * 256);
     }
-    const int64_t inv = fx_inv_sum(sum);
+    const int32_t inv = fx_inv_sum(sum);
     if (hh == 0) {
-        const int16_t y = fx_sat16(fx_rnd((int64_t)acc * inv, 16));
+        const int16_t y = sat16_32(rnd16_mul(acc, inv));  // 0 <= inv < 2^15
         int16_t* po = a.out + (size_t)t * a.ldo + (size_t)g * D + e;
         if (FUSED)
             st_coherent(po, y);
