@@ -155,8 +155,10 @@ struct TileOArgs {
     uint32_t* host_abort;
     uint32_t wait_limit;
 };
-// Workgroups of the tile + O launch the device holds at once.
-int tile_o_capacity(uint32_t head_dim, uint32_t rows, int cus);
+// The variant of the tile + O launch for an O projection of widening
+// interval L, and the workgroups of a variant the device holds at once.
+int tile_o_variant(const ProjArgs& o, int L);
+int tile_o_capacity(uint32_t head_dim, uint32_t rows, int variant, int cus);
 // Fills the launch shape of s (grid, arrivals) and returns whether the
 // launch serves `rows` rows: head_dim 64 or 128, 1-2 rows, the attention
 // on the one-launch tile path (5-64 tiles, not the GQA path, not

@@ -1787,27 +1787,36 @@ hipError_t launch_attention_sublayer(const SublayerArgs& s, uint32_t rows, int q
     return hipGetLastError();
 }
 
-// The smallest residency over the variants of the tile + O launch.
-template <int D, int RT>
-static int tile_o_capacity_of(int cus) {
-    int pc[5] = {0, 0, 0, 0, 0};
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &pc[0], attention_tile_o_kernel<D, RT, 4, false>, 2 * D, 0) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &pc[1], attention_tile_o_kernel<D, RT, 1, false>, 2 * D, 0) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &pc[2], attention_tile_o_kernel<D, RT, 0, false>, 2 * D, 0) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &pc[3], attention_tile_o_kernel<D, RT, 4, true>, 2 * D, 0) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &pc[4], attention_tile_o_kernel<D, RT, 4, true, true>, 2 * D, 0) != hipSuccess)
-        return 0;
-    return std::min({pc[0], pc[1], pc[2], pc[3], pc[4]}) * cus;
+// The variant of the tile + O launch for an O projection: 12-bit with
+// corrections, 12-bit, or 16-bit at widening interval 4 / 1 / every
+// product.
+int tile_o_variant(const ProjArgs& o, int L) {
+    if (o.p0 && o.corr0) return 4;
+    if (o.p0) return 3;
+    return L >= 4 ? 0 : (L >= 1 ? 1 : 2);
 }
 
-int tile_o_capacity(uint32_t head_dim, uint32_t rows, int cus) {
-    if (head_dim == 64) return rows == 1 ? tile_o_capacity_of<64, 1>(cus) : tile_o_capacity_of<64, 2>(cus);
-    if (head_dim == 128) return rows == 1 ? tile_o_capacity_of<128, 1>(cus) : tile_o_capacity_of<128, 2>(cus);
+// Workgroups of one variant of the tile + O launch the device holds at
+// once.
+template <int D, int RT>
+static int tile_o_capacity_of(int variant, int cus) {
+    int pc = 0;
+    hipError_t e;
+    switch (variant) {
+    case 0: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&pc, attention_tile_o_kernel<D, RT, 4, false>, 2 * D, 0); break;
+    case 1: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&pc, attention_tile_o_kernel<D, RT, 1, false>, 2 * D, 0); break;
+    case 2: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&pc, attention_tile_o_kernel<D, RT, 0, false>, 2 * D, 0); break;
+    case 3: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&pc, attention_tile_o_kernel<D, RT, 4, true>, 2 * D, 0); break;
+    default: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&pc, attention_tile_o_kernel<D, RT, 4, true, true>, 2 * D, 0); break;
+    }
+    return e == hipSuccess ? pc * cus : 0;
+}
+
+int tile_o_capacity(uint32_t head_dim, uint32_t rows, int variant, int cus) {
+    if (head_dim == 64)
+        return rows == 1 ? tile_o_capacity_of<64, 1>(variant, cus) : tile_o_capacity_of<64, 2>(variant, cus);
+    if (head_dim == 128)
+        return rows == 1 ? tile_o_capacity_of<128, 1>(variant, cus) : tile_o_capacity_of<128, 2>(variant, cus);
     return 0;
 }
 
@@ -1835,16 +1844,13 @@ bool tile_o_prepare(TileOArgs& s, uint32_t rows, int capacity) {
 template <int D, int RT>
 static void launch_tile_o_d(const TileOArgs& s, int L, hipStream_t st) {
     const uint32_t grid = s.ntile + s.no;
-    if (s.o.p0 && s.o.corr0)
-        attention_tile_o_kernel<D, RT, 4, true, true><<<grid, 2 * D, 0, st>>>(s);
-    else if (s.o.p0)
-        attention_tile_o_kernel<D, RT, 4, true><<<grid, 2 * D, 0, st>>>(s);
-    else if (L >= 4)
-        attention_tile_o_kernel<D, RT, 4, false><<<grid, 2 * D, 0, st>>>(s);
-    else if (L >= 1)
-        attention_tile_o_kernel<D, RT, 1, false><<<grid, 2 * D, 0, st>>>(s);
-    else
-        attention_tile_o_kernel<D, RT, 0, false><<<grid, 2 * D, 0, st>>>(s);
+    switch (tile_o_variant(s.o, L)) {
+    case 4: attention_tile_o_kernel<D, RT, 4, true, true><<<grid, 2 * D, 0, st>>>(s); break;
+    case 3: attention_tile_o_kernel<D, RT, 4, true><<<grid, 2 * D, 0, st>>>(s); break;
+    case 0: attention_tile_o_kernel<D, RT, 4, false><<<grid, 2 * D, 0, st>>>(s); break;
+    case 1: attention_tile_o_kernel<D, RT, 1, false><<<grid, 2 * D, 0, st>>>(s); break;
+    default: attention_tile_o_kernel<D, RT, 0, false><<<grid, 2 * D, 0, st>>>(s); break;
+    }
 }
 
 hipError_t launch_attention_tile_o(const TileOArgs& s, uint32_t rows, int L, hipStream_t st) {

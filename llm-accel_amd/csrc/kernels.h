@@ -29,7 +29,8 @@ struct ProjArgs {
     uint32_t ldr;
     uint32_t n;         // valid output columns
     uint32_t rows;      // active rows (1..8)
-    const int16_t* exp8;  // Q8.8 exp table, x = -2048..0 (EPI_SILU)
+    const int16_t* exp8;    // Q8.8 exp table, x = -2048..0
+    const uint32_t* silu8;  // EPI_SILU: per exp-table entry e, e | recip(256 + e) << 16
     // EPI_RESID only, optional: RMSNorm of the output rows with a constant
     // gain (norm_out[r][n] = rnd(out * gain * gamma[n], 16)).
     int16_t* norm_out;

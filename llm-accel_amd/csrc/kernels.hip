@@ -135,9 +135,6 @@ __global__ __launch_bounds__(64 * WPB) void proj_kernel(ProjArgs a) {
     const bool efill = EPI == EPI_RESID && a.final_out && et < 32 && fr >= a.rows && fn < a.n;
     int16_t fill = 0;
     if (efill) fill = a.res[(size_t)fr * a.ldr + fn];
-    // SiLU reads its 4 * RT table entries from the (L2-resident) table:
-    // staging the 4 KiB table in LDS per workgroup measured slower
-    const int16_t* e8s = a.exp8;
     const uint32_t S = a.steps;
     const uint32_t s0 = wave * S / WPB, s1 = (wave + 1) * S / WPB;
 
@@ -308,14 +305,12 @@ __global__ __launch_bounds__(64 * WPB) void proj_kernel(ProjArgs a) {
         int64_t tot[NM];
 #pragma unroll
         for (int m = 0; m < NM; m++) {
-            tot[m] = 0;
-#pragma unroll
-            for (int w = 0; w < WPB; w++) tot[m] += red[w][m][ii][er];
+            tot[m] = tree_sum64<WPB>([&](int w) { return red[w][m][ii][er]; });
         }
         if constexpr (EPI == EPI_SILU && RT <= 2)
             silu_out_scalar<4 * RT>(a, er, en, tot[0], tot[NM - 1], et);
         else
-            proj_out<EPI>(a, er, en, tot[0], tot[NM - 1], ei, e8s);
+            proj_out<EPI>(a, er, en, tot[0], tot[NM - 1], ei);
     }
     if (efill) a.final_out[(size_t)fr * a.ldn + fn] = fill;
 }
@@ -468,9 +463,7 @@ __global__ __launch_bounds__(64 * WPB) void proj_p12_kernel(ProjArgs a) {
         int64_t tot[NM];
 #pragma unroll
         for (int m = 0; m < NM; m++) {
-            tot[m] = 0;
-#pragma unroll
-            for (int w = 0; w < WPB; w++) tot[m] += red[w][m][ii][er];
+            tot[m] = tree_sum64<WPB>([&](int w) { return red[w][m][ii][er]; });
             if (CORR && (cr[m].e[0] | cr[m].e[1] | cr[m].e[2] | cr[m].e[3]) != 0) {
                 corr_inputs<EPI, false>(a, er, cr[m]);
                 tot[m] += corr_sum(cr[m]);
@@ -479,7 +472,7 @@ __global__ __launch_bounds__(64 * WPB) void proj_p12_kernel(ProjArgs a) {
         if constexpr (EPI == EPI_SILU)
             silu_out_scalar<4 * RT>(a, er, en, tot[0], tot[NM - 1], et);
         else
-            proj_out<EPI>(a, er, en, tot[0], tot[NM - 1], ei, a.exp8);
+            proj_out<EPI>(a, er, en, tot[0], tot[NM - 1], ei);
     }
     if (efill) a.final_out[(size_t)fr * a.ldn + fn] = fill;
 }
@@ -746,7 +739,7 @@ __device__ __forceinline__ void mf_finish(const ProjArgs& a, uint32_t c, uint32_
                     }
                 }
             }
-            proj_out<EPI>(a, r, nn, tot[0], tot[NM - 1], e, a.exp8);
+            proj_out<EPI>(a, r, nn, tot[0], tot[NM - 1], e);
         } else if (EPI == EPI_RESID && a.final_out && r < 8) {
             a.final_out[(size_t)r * a.ldn + nn] =
                 t == et ? fe.fill : a.res[(size_t)r * a.ldr + nn];
@@ -1279,6 +1272,7 @@ bool proj_uses_p12(const ProjArgs& a, int epi) {
 
 hipError_t launch_proj(const ProjArgs& a, int epi, int L, uint32_t blocks,
                        hipStream_t st) {
+    if (epi == EPI_SILU && !a.silu8) return hipErrorInvalidValue;  // the SiLU epilogue's table
     if (proj_uses_mfma(a, epi)) {
         switch (epi) {
         case EPI_STORE: return launch_mfma_epi<1, EPI_STORE>(a, st);

@@ -126,6 +126,7 @@ struct llm_ctx {
     int16_t* norms = nullptr;
     int16_t* rope = nullptr;
     int16_t* exp8 = nullptr;
+    uint32_t* silu8 = nullptr;  // per exp8 entry e: e | fx_recip(256 + e) << 16
     int16_t* exp14 = nullptr;
     int16_t* kcache = nullptr;
     int16_t* vcache = nullptr;
@@ -200,7 +201,7 @@ struct llm_ctx {
     // the one-launch tile path and O in one launch for decode rows at 5-64
     // tiles; LLM_ACCEL_TILE_O=0 keeps them two launches
     bool tile_o = true;
-    int tile_o_cap[2] = {-1, -1};
+    int tile_o_cap[2][5] = {{-1, -1, -1, -1, -1}, {-1, -1, -1, -1, -1}};  // rows x variant
     int cus = 0;
     // RMSNorm gain: > 0 when it is the same for every row (hidden >= 128:
     // fm_t(hidden) saturates, recip() returns 0, the mean square is 0 and
@@ -885,8 +886,9 @@ int enqueue_attention_sublayer(llm_ctx* c, uint32_t layer, uint32_t R,
         llm::TileOArgs to{};
         bool tile_o = false;
         if (c->tile_o && R <= 2 && !llm::proj_uses_mfma(o, llm::EPI_RESID)) {
-            int& cc = c->tile_o_cap[R - 1];
-            if (cc < 0) cc = llm::tile_o_capacity(c->d, R, c->cus);
+            const int var = llm::tile_o_variant(o, mo.L);
+            int& cc = c->tile_o_cap[R - 1][var];
+            if (cc < 0) cc = llm::tile_o_capacity(c->d, R, var, c->cus);
             to.at = at;
             to.o = o;
             to.sync = c->sync;
@@ -941,6 +943,7 @@ int enqueue_ffn_sublayer(llm_ctx* c, uint32_t layer, uint32_t R, int in_pair,
     a.n = mg.n;
     a.rows = R;
     a.exp8 = c->exp8;
+    a.silu8 = c->silu8;
     set_mf(c, a, mg, &mu);
     if (mg.p12_ok && mu.p12_ok) {
         a.p0 = mg.p12;
@@ -1131,6 +1134,7 @@ int llm_ctx_create(const llm_shape_t* shape, int device, uint32_t num_pairs,
         (rc = dev_alloc(c, (void**)&c->rope,
                         (size_t)c->max_seq * d * sizeof(int16_t))) ||
         (rc = dev_alloc(c, (void**)&c->exp8, 2056 * sizeof(int16_t))) ||
+        (rc = dev_alloc(c, (void**)&c->silu8, 2056 * sizeof(uint32_t))) ||
         (rc = dev_alloc(c, (void**)&c->exp14, 2056 * sizeof(int16_t))))
         return cleanup(rc);
     {
@@ -1150,7 +1154,13 @@ int llm_ctx_create(const llm_shape_t* shape, int device, uint32_t num_pairs,
             return cleanup(fail(LLM_E_HIP, "rope upload"));
         int16_t e8[2049], e14[2049];
         build_exp_tables(e8, e14);
+        // the SiLU epilogues' reciprocal recip(256 + e), formed here by the
+        // same Newton steps instead of per output on the device
+        uint32_t s8[2049];
+        for (int i = 0; i < 2049; i++)
+            s8[i] = (uint32_t)(uint16_t)e8[i] | (uint32_t)(uint16_t)fx_recip(256 + e8[i]) << 16;
         if (hipMemcpy(c->exp8, e8, sizeof(e8), hipMemcpyHostToDevice) ||
+            hipMemcpy(c->silu8, s8, sizeof(s8), hipMemcpyHostToDevice) ||
             hipMemcpy(c->exp14, e14, sizeof(e14), hipMemcpyHostToDevice))
             return cleanup(fail(LLM_E_HIP, "exp table upload"));
     }
@@ -2020,7 +2030,8 @@ int llm_bench_projection(llm_ctx_t* c, uint32_t kernel, uint32_t rows,
             const Matrix& u = c->mat(layer, M_UP);
             a.w0 = g.d; a.w1 = u.d; a.steps = g.steps; a.x = c->xn_ffn;
             a.ldx = c->Hp; a.out = c->act; a.ldo = c->Ip; a.n = g.n;
-            a.exp8 = c->exp8; L = std::min(g.L, u.L); blocks = g.n_pad / 4;
+            a.exp8 = c->exp8; a.silu8 = c->silu8;
+            L = std::min(g.L, u.L); blocks = g.n_pad / 4;
             epi = llm::EPI_SILU;
             set_mf(c, a, g, &u);
             if (g.p12_ok && u.p12_ok) {

@@ -123,27 +123,52 @@ __device__ __forceinline__ int64_t corr_sum(const CorrIn& c) {
     return s;
 }
 
+// fx_narrow_projection with its second rounding in 32-bit arithmetic.
+__device__ __forceinline__ int16_t narrow16(int64_t acc) {
+    return sat16_32(rnd32(fx_sat32(fx_rnd(acc, 4)), 8));
+}
+// fx_silu_entry from a packed table word w = e | recip(256 + e) << 16 (the
+// reciprocal formed on the host by the same Newton steps), its products in
+// 32-bit arithmetic: x r <= 2^15 * 2^14, and x e r as norm1(r, x e) with
+// |x e| <= 2^23 (e <= 256).
+__device__ __forceinline__ int16_t silu_packed(int32_t x, uint32_t w) {
+    const int32_t e = (int32_t)(w & 0xffffu), r = (int32_t)(w >> 16);
+    if (x >= 0) return sat16_32(rnd32(x * r, 8));
+    return (int16_t)norm1(r, x * e);
+}
+// Sum of N int64 values as a tree (depth log2 N instead of a chain of N
+// dependent 64-bit additions).
+template <int N, typename F>
+__device__ __forceinline__ int64_t tree_sum64(F get) {
+    int64_t v[N];
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] = get(i);
+#pragma unroll
+    for (int n = N; n > 1; n = (n + 1) / 2)
+#pragma unroll
+        for (int i = 0; i < n / 2; i++) v[i] += v[n - 1 - i];
+    return v[0];
+}
+
 // Output (r, n) of a projection from its exact sums (gate and up for
 // EPI_SILU): the reference's narrowing, then the epilogue.
 // COH: the output is read by other workgroups of the same launch, so it is
 // written with a device-coherent store.
 template <int EPI, bool COH = false>
 __device__ __forceinline__ void proj_out(const ProjArgs& a, uint32_t r, uint32_t n,
-                                         int64_t t0, int64_t t1, const EpiIn& ei,
-                                         const int16_t* e8) {
-    int16_t y = fx_narrow_projection(t0);
+                                         int64_t t0, int64_t t1, const EpiIn& ei) {
+    int16_t y = narrow16(t0);
     if (EPI == EPI_RESID) {
-        y = fx_sat16((int32_t)y + ei.res);
+        y = sat16_32((int32_t)y + ei.res);
+        // rnd(y gain gamma, 16) with the (int16) gain: norm1's exact split
         if (a.norm_out)
-            a.norm_out[(size_t)r * a.ldn + n] = fx_sat16(fx_rnd(
-                (int64_t)y * a.norm_gain * ei.g0, 16));
+            a.norm_out[(size_t)r * a.ldn + n] = (int16_t)norm1(y, __mul24(a.norm_gain, ei.g0));
         if (a.final_out)
-            a.final_out[(size_t)r * a.ldn + n] = fx_sat16(fx_rnd(
-                (int64_t)y * a.norm_gain * ei.g1, 16));
+            a.final_out[(size_t)r * a.ldn + n] = (int16_t)norm1(y, __mul24(a.norm_gain, ei.g1));
     } else if (EPI == EPI_SILU) {
-        const int16_t up = fx_narrow_projection(t1);
-        const int16_t sg = fx_silu(y, e8);
-        y = fx_sat16(fx_rnd((int64_t)sg * up, 8));
+        const int16_t up = narrow16(t1);
+        const int16_t sg = silu_packed(y, a.silu8[fx_silu_index(y)]);
+        y = sat16_32(rnd32((int32_t)sg * up, 8));
     }
     if (COH)
         st_coherent(&a.out[(size_t)r * a.ldo + n], y);
@@ -160,22 +185,21 @@ template <int NL>
 __device__ __forceinline__ void silu_out_scalar(const ProjArgs& a, uint32_t r, uint32_t n,
                                                 int64_t t0, int64_t t1, int et) {
     static_assert(NL <= 64, "lanes of wavefront 0");
-    const int16_t y = fx_narrow_projection(t0);
-    const int16_t up = fx_narrow_projection(t1);
+    const int16_t y = narrow16(t0);
+    const int16_t up = narrow16(t1);
     const int32_t ix = fx_silu_index(y);  // 0..2048
     typedef const __attribute__((address_space(4))) uint32_t* ctab;
-    const ctab tab = (ctab)(const void*)a.exp8;
-    int32_t e = 0;
+    const ctab tab = (ctab)(const void*)a.silu8;
+    uint32_t w = 0;
 #pragma unroll
     for (int l = 0; l < NL; l++) {
         uint32_t il = __builtin_amdgcn_readlane(ix, l);
         il = il > 2048u ? 2048u : il;  // a lane past the matrix holds anything
-        const uint32_t wd = tab[il >> 1];
-        const int32_t el = (int32_t)((wd >> (16 * (il & 1))) & 0xffffu);
-        e = et == l ? el : e;
+        const uint32_t wl = tab[il];
+        w = et == l ? wl : w;
     }
-    const int16_t sg = fx_silu_entry(y, e);
-    a.out[(size_t)r * a.ldo + n] = fx_sat16(fx_rnd((int64_t)sg * up, 8));
+    const int16_t sg = silu_packed(y, w);
+    a.out[(size_t)r * a.ldo + n] = sat16_32(rnd32((int32_t)sg * up, 8));
 }
 
 // NB consecutive 4-row blocks NB b .. NB b + NB - 1 of a projection inside
@@ -380,15 +404,14 @@ __device__ __forceinline__ bool proj_block(const ProjArgs& a, uint32_t b, int64_
     lds_barrier();
     if (eout) {
         const int nb = et / (4 * RT), ii = (et % (4 * RT)) / RT;
-        int64_t tot = 0;
-#pragma unroll
-        for (int w = 0; w < WPB; w++) tot += red[((nb * WPB + w) * 4 + ii) * RT + er];
+        int64_t tot = tree_sum64<WPB>(
+            [&](int w) { return red[((nb * WPB + w) * 4 + ii) * RT + er]; });
         if (CORR && (cr.e[0] | cr.e[1] | cr.e[2] | cr.e[3]) != 0) {
             // this row's activations at its correction columns
             corr_inputs<EPI, XCOH>(a, er, cr);
             tot += corr_sum(cr);
         }
-        proj_out<EPI, OCOH>(a, er, en, tot, tot, ei, nullptr);
+        proj_out<EPI, OCOH>(a, er, en, tot, tot, ei);
     }
     return true;
 }
