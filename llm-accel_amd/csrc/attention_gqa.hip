@@ -563,9 +563,8 @@ __device__ __forceinline__ int32_t acc_tiles_seq(const AttnArgs& a, const GqaSca
             const uint32_t j = jb + u;
             if (j < j1) {
                 const int32_t tmv = sm.tm[j];
-                if (tmv > m) {
-                    acc = fx_sat32(
-                        fx_rnd((int64_t)acc * ((int64_t)prob(sm.e14, m - tmv) << 2), 16));
+                if (tmv > m) {  // (the factor is at most 2^16)
+                    acc = rnd16_mul(acc, (int32_t)prob(sm.e14, m - tmv) << 2);
                     m = tmv;
                 }
                 acc = __builtin_elementwise_add_sat(acc, tvv[u] * 256);
@@ -579,9 +578,9 @@ __device__ __forceinline__ int32_t sum_tiles_seq(const GqaScanSmem& sm, uint32_t
                                                  uint32_t j1, int32_t m, int32_t sum) {
     for (uint32_t j = j0; j < j1; j++) {
         const int32_t tmv = sm.tm[j], tsk = sm.ts[j];
-        if (tmv > m) {
-            const int64_t old = (int64_t)prob(sm.e14, m - tmv) << 2;
-            sum = fx_sat32(fx_rnd((int64_t)sum * old + ((int64_t)tsk << 18), 16));
+        if (tmv > m) {  // non-negative terms: nested saturating additions
+            const int32_t old = (int32_t)prob(sm.e14, m - tmv) << 2;
+            sum = __builtin_elementwise_add_sat(rnd16_mul(sum, old), tsk << 2);
             m = tmv;
         } else {
             sum = __builtin_elementwise_add_sat(sum, tsk << 2);
@@ -828,7 +827,7 @@ __device__ __forceinline__ void gqa_scan_body(const AttnArgs& a, GqaScanSmem& sm
                 nx = sm.ri[rn];
                 tsn = sm.rts[rn];
                 if (cu.len == 0) continue;
-                const int64_t sumr = r ? fx_rnd((int64_t)sum * cu.old, 16) : sum;
+                const int64_t sumr = r ? rnd16_mul(sum, (int32_t)cu.old) : sum;
                 const int64_t t4 = (int64_t)ts << 2;
                 if (sumr + t4 <= INT32_MAX)
                     sum = (int32_t)(sumr + t4);
@@ -862,7 +861,7 @@ __device__ __forceinline__ void gqa_scan_body(const AttnArgs& a, GqaScanSmem& sm
                 nx = sm.ri[rn];
                 rsn = sm.rsum[rn][tid];
                 if (cu.len == 0) continue;
-                const int32_t accr = r ? fx_sat32(fx_rnd((int64_t)acc * cu.old, 16)) : acc;
+                const int32_t accr = r ? rnd16_mul(acc, (int32_t)cu.old) : acc;
                 const int64_t aa = accr < 0 ? -(int64_t)accr : accr;
                 if (aa + ((int64_t)cu.len << 23) <= INT32_MAX)
                     acc = accr + rs * 256;
