@@ -1243,8 +1243,6 @@ __device__ __forceinline__ void tile_pv_phase(const AttnArgs& a, const TileWg& w
     static_assert(!OARR || FUSED, "the O hand-off follows the one-launch combine");
     static_assert(D % 32 == 0, "tile path: head_dim a multiple of 32");
     constexpr uint32_t NTH = D * 2;
-    constexpr int NE = (257 + NTH - 1) / NTH;    // exp table pieces per thread
-    constexpr int NV = (8 * D + NTH - 1) / NTH;  // block V elements per thread
     constexpr int NM = 4;                        // tile maxima per lane (tiles < 256)
     const uint32_t t = wg.t, g = wg.g, tile = wg.tile, tid = threadIdx.x;
     const uint32_t n = a.pos0 + t + 1, own = n - 1;
@@ -1255,22 +1253,44 @@ __device__ __forceinline__ void tile_pv_phase(const AttnArgs& a, const TileWg& w
     const size_t base = (rh * a.max_tiles + tile) * G + gi;
 
     // ---- staging loads (indices clamped: every load is issued), this
-    // tile's V slice, then the staging writes ----
-    v4u ex[NE];
-#pragma unroll
-    for (int u = 0; u < NE; u++) {
-        const uint32_t c = tid + NTH * u;
-        ex[u] = *(const v4u*)(a.exp14 + 8 * (c < 257 ? c : 256));
-    }
+    // tile's V slice, then the staging writes.  One launch with more than
+    // one wavefront: the wavefronts past the first load and stage the exp
+    // table and the block's V rows while the first polls the maxima ----
+    constexpr bool SPLIT = FUSED && NTH > 64;
+    constexpr uint32_t SW = SPLIT ? NTH - 64 : NTH;  // staging threads
+    constexpr int NE2 = (257 + SW - 1) / SW, NV2 = (8 * D + SW - 1) / SW;
+    const uint32_t sid = SPLIT ? tid - 64 : tid;     // index among them
+    const bool stager = !SPLIT || tid >= 64;
     const TileRows tr = tile_rows(a, tile, own);
     const uint32_t nv = tr.nrow * D;
-    int16_t vx[NV];
+    v4u ex[NE2];
+    int16_t vx[NV2];
+    auto stage_load = [&] {
 #pragma unroll
-    for (int u = 0; u < NV; u++) {
-        const uint32_t i = tid + NTH * u < nv ? tid + NTH * u : 0;
-        vx[u] = a.qkv[(size_t)(tr.r0 + i / D) * a.ldqkv +
-                      (size_t)(a.num_heads + a.num_kv_heads) * D + (size_t)h * D + i % D];
-    }
+        for (int u = 0; u < NE2; u++) {
+            const uint32_t c = sid + SW * u;
+            ex[u] = *(const v4u*)(a.exp14 + 8 * (c < 257 ? c : 256));
+        }
+#pragma unroll
+        for (int u = 0; u < NV2; u++) {
+            const uint32_t i = sid + SW * u < nv ? sid + SW * u : 0;
+            vx[u] = a.qkv[(size_t)(tr.r0 + i / D) * a.ldqkv +
+                          (size_t)(a.num_heads + a.num_kv_heads) * D + (size_t)h * D + i % D];
+        }
+    };
+    auto stage_write = [&] {
+#pragma unroll
+        for (int u = 0; u < NE2; u++) {
+            const uint32_t c = sid + SW * u;
+            if (c < 257) *(v4u*)(sm.e14 + 8 * c) = ex[u];
+        }
+#pragma unroll
+        for (int u = 0; u < NV2; u++) {
+            const uint32_t i = sid + SW * u;
+            if (i < nv) sm.kv[tr.r0 + i / D][i % D] = vx[u];
+        }
+    };
+    if (stager) stage_load();
     int32_t sc = 0, mt = 0, mprev = INT16_MIN;  // mprev: maxima of the earlier tiles
     if (!FUSED) {
         sc = a.s_scores[base * TILE + lane];
@@ -1288,31 +1308,27 @@ __device__ __forceinline__ void tile_pv_phase(const AttnArgs& a, const TileWg& w
     }
     SplitRegs regs;
     slice_load_v<D>(a, h, tile, w, lane, regs);
+    if (SPLIT && stager) stage_write();  // before the poll's barrier
     if (FUSED) {
         // lane j < tile of wavefront 0 polls tile j's maximum
         // (tile < kTileFusedMaxTiles); their maximum goes through LDS
+        // before the poll's barrier
         uint32_t v = 0;
         if (!poll_flags((const uint32_t*)&a.s_tmax32[rh * a.max_tiles * G + gi], G, tile,
-                        kMaxValid, &v, a.wait_limit, a.abort, a.host_abort, &sm.last))
+                        kMaxValid, &v, a.wait_limit, a.abort, a.host_abort, &sm.last,
+                        [&](uint32_t vl) {
+                            const int32_t mx = wave_max(
+                                lane < tile ? (int32_t)(int16_t)(vl & 0xffffu) : INT16_MIN);
+                            if (lane == 0) sm.m0 = mx;
+                        }))
             return;
         sc = lsc[lane];
         mt = *lmt;
-        if (w == 0) {
-            const int32_t mx = wave_max(lane < tile ? (int32_t)(int16_t)(v & 0xffffu) : INT16_MIN);
-            if (lane == 0) sm.m0 = mx;
-        }
     }
-#pragma unroll
-    for (int u = 0; u < NE; u++) {
-        const uint32_t c = tid + NTH * u;
-        if (c < 257) *(v4u*)(sm.e14 + 8 * c) = ex[u];
+    if (!SPLIT) {
+        stage_write();
+        lds_barrier();
     }
-#pragma unroll
-    for (int u = 0; u < NV; u++) {
-        const uint32_t i = tid + NTH * u;
-        if (i < nv) sm.kv[tr.r0 + i / D][i % D] = vx[u];
-    }
-    lds_barrier();
     // ---- probabilities under the running max after this tile ----
     const int32_t m0 = FUSED ? sm.m0 : wave_max(mprev);  // running max before the tile
     const int32_t mn = mt > m0 ? mt : m0;      // and after it

@@ -168,10 +168,14 @@ struct TagWait {
 // the flag and the value: no separate arrival).  Bounded as wait_counts:
 // returns (uniformly) false when the wait gave up or another workgroup
 // did.  Progress needs the workgroups that write the words to be running.
+// `done(v)` runs in wavefront 0 with each lane's word once every flag is
+// set, before the workgroup barrier (results it writes to LDS are visible
+// to every wavefront on return).
+template <typename Done>
 __device__ __forceinline__ bool poll_flags(const uint32_t* p, uint32_t stride, uint32_t n,
                                            uint32_t valid, uint32_t* val, uint32_t limit,
                                            uint32_t* abort, uint32_t* host_abort,
-                                           uint32_t* lds_flag) {
+                                           uint32_t* lds_flag, Done done) {
     if (threadIdx.x < 64) {
         const uint32_t l = threadIdx.x;
         const bool mine = l < n;
@@ -198,10 +202,18 @@ __device__ __forceinline__ bool poll_flags(const uint32_t* p, uint32_t stride, u
             __builtin_amdgcn_s_sleep(2);
         }
         *val = v;
+        if (ok) done(v);
         if (l == 0) *lds_flag = ok;
     }
     __syncthreads();
     return *lds_flag != 0;
+}
+__device__ __forceinline__ bool poll_flags(const uint32_t* p, uint32_t stride, uint32_t n,
+                                           uint32_t valid, uint32_t* val, uint32_t limit,
+                                           uint32_t* abort, uint32_t* host_abort,
+                                           uint32_t* lds_flag) {
+    return poll_flags(p, stride, n, valid, val, limit, abort, host_abort, lds_flag,
+                      [](uint32_t) {});
 }
 
 }  // namespace llm
