@@ -368,9 +368,13 @@ __global__ __launch_bounds__(64 * WPB) void proj_p12_kernel(ProjArgs a) {
     uint32_t hi[SPW][NM];
     uint4 xv[SPW][RT], gv[SPW];
     uint32_t x2[SPW], g2[SPW];
+    uint32_t xw[SPW][RT];  // columns 2 lane, 2 lane + 1 of each step (spread8)
     // EPI_STORE_NORM_IN (one row: the kernel's only use): lane l loads and
     // normalises columns 2l, 2l + 1 of each step once per wavefront
     constexpr bool NIN = EPI == EPI_STORE_NORM_IN && RT == 1;
+    // every other epilogue: each step's activations loaded once per
+    // wavefront and spread to the lanes' column groups
+    constexpr bool SPREAD = EPI != EPI_STORE_NORM_IN;
 #pragma unroll
     for (int u = 0; u < SPW; u++) {
         const uint32_t du = cnt == 0 ? 0 : ((uint32_t)u < cnt ? u : cnt - 1);
@@ -383,11 +387,15 @@ __global__ __launch_bounds__(64 * WPB) void proj_p12_kernel(ProjArgs a) {
             // columns 2 lane, 2 lane + 1 of the step (normalised once per wave)
             x2[u] = *(const uint32_t*)(a.x + (size_t)(s0 + du) * 128 + 2 * lane);
             g2[u] = *(const uint32_t*)(a.in_gamma + (s0 + du) * 128 + 2 * lane);
+        } else if constexpr (SPREAD) {
+#pragma unroll
+            for (int r = 0; r < RT; r++)
+                xw[u][r] = *(const uint32_t*)(a.x + (size_t)r * a.ldx + (size_t)(s0 + du) * 128 + 2 * lane);
         } else {
 #pragma unroll
             for (int r = 0; r < RT; r++) xv[u][r] = *(const uint4*)(xp + (size_t)r * a.ldx + du * 128);
-            if (EPI == EPI_STORE_NORM_IN)  // the norm table is padded to whole k-steps
-                gv[u] = *(const uint4*)(a.in_gamma + (s0 + du) * 128 + j * 8);
+            // the norm table is padded to whole k-steps
+            gv[u] = *(const uint4*)(a.in_gamma + (s0 + du) * 128 + j * 8);
         }
     }
     if constexpr (NIN) {
@@ -417,9 +425,14 @@ __global__ __launch_bounds__(64 * WPB) void proj_p12_kernel(ProjArgs a) {
         const uint32_t keep = lane_mask((uint32_t)u < cnt);
 #pragma unroll
         for (int r = 0; r < RT; r++) {
-            const uint4 x = and4(EPI == EPI_STORE_NORM_IN && !NIN ? norm8(xv[u][r], gv[u], a.in_gain)
-                                                                  : xv[u][r],
-                                 keep);
+            uint4 xr;
+            if constexpr (SPREAD)
+                xr = spread8(xw[u][r], j);
+            else if constexpr (NIN)
+                xr = xv[u][r];
+            else
+                xr = norm8(xv[u][r], gv[u], a.in_gain);
+            const uint4 x = and4(xr, keep);
             sx[r] = dot2(0x00010001u, x.x, sx[r]);
             sx[r] = dot2(0x00010001u, x.y, sx[r]);
             sx[r] = dot2(0x00010001u, x.z, sx[r]);

@@ -32,6 +32,20 @@ __device__ __forceinline__ uint4 and4(uint4 v, uint32_t m) {
     return make_uint4(v.x & m, v.y & m, v.z & m, v.w & m);
 }
 
+// The activations of lane (i, j) of a 4-row weight block -- columns
+// 8j .. 8j + 7 of a 128-column k-step -- from the step's 256 bytes loaded
+// once per wavefront (lane l holds columns 2l, 2l + 1 in `w`) and spread
+// through the LDS crossbar (ds_bpermute, no LDS memory): one 4-byte load
+// per lane instead of a 16-byte load that the four lanes of each column
+// group would repeat (decode down 8.3 -> 8.0 us).  Every lane of the
+// wavefront must be active.
+__device__ __forceinline__ uint4 spread8(uint32_t w, int j) {
+    return make_uint4((uint32_t)__builtin_amdgcn_ds_bpermute(16 * j, (int)w),
+                      (uint32_t)__builtin_amdgcn_ds_bpermute(16 * j + 4, (int)w),
+                      (uint32_t)__builtin_amdgcn_ds_bpermute(16 * j + 8, (int)w),
+                      (uint32_t)__builtin_amdgcn_ds_bpermute(16 * j + 12, (int)w));
+}
+
 // One input normalised with a constant gain: rnd(x * gg, 16), gg = gain *
 // gamma (int32), in 32-bit arithmetic: with gg = 2^16 gh + gl (0 <= gl <
 // 2^16), floor((x gg + 2^15) / 2^16) = x gh + floor((x gl + 2^15) / 2^16)
@@ -241,7 +255,6 @@ __device__ __forceinline__ bool proj_block(const ProjArgs& a, uint32_t b, int64_
     const uint32_t S = a.steps;
     const uint32_t s0 = wave * S / WPB, s1 = (wave + 1) * S / WPB;
     const uint32_t cnt = s1 - s0;  // <= SPW (the launcher's choice)
-    const int16_t* xp = a.x + (size_t)s0 * 128 + j * 8;
     static_assert(!P12 || SPW <= 32, "int32 sums of the 12-bit products");
     uint4 wv[NB][SPW], gv[SPW];
     uint2 lv[NB][SPW];     // P12: low bytes of the lane's 8 columns
@@ -308,6 +321,10 @@ __device__ __forceinline__ bool proj_block(const ProjArgs& a, uint32_t b, int64_
 #pragma unroll
             for (int r = 0; r < RT; r++) xv[u][r] = *(const uint4*)&xs[wave][u][r][4 * j];
     } else {
+        // 16 bytes per lane (not spread8: after the wait the spreading's LDS
+        // round trip lies on the launch's critical path, measured +0.3 us
+        // for the fused sublayer)
+        const int16_t* xp = a.x + (size_t)s0 * 128 + j * 8;
 #pragma unroll
         for (int u = 0; u < SPW; u++) {
             const uint32_t du = cnt == 0 ? 0 : ((uint32_t)u < cnt ? u : cnt - 1);
