@@ -1212,7 +1212,12 @@ static hipError_t launch_mfma_q(const ProjArgs& a, uint32_t parts, hipStream_t s
 // one matrix, and for K = 11008).  One matrix with a long K (down, K =
 // 11008) takes 16 wavefronts of ~3 steps over at least 256 workgroups
 // (P8 down 11.5 -> 11.1 us against 8 wavefronts of ~6 steps over 128
-// chunks x 2; Q|K|V and O, K = 2048, are slower so).
+// chunks x 2; Q|K|V and O, K = 2048, are slower so).  Not splitting K
+// costs more than the partial sums' hand-off saves: 16 wavefronts of ~6
+// steps over 128 workgroups took 14.2 us against 11.7, and 8-output
+// chunks over 256 workgroups without a split (the MFMA's columns 8-15
+// repeating 0-7) 14.1 us, 13.3 with 3 steps of loads in flight: the
+// longer per-wavefront chain of steps, not the hand-off, sets the time.
 MfSplit mf12_split(uint32_t nc, uint32_t steps, uint32_t nm) {
     MfSplit s{LLM_MF12_KS, 1};
     uint32_t target = LLM_MF12_WG_TARGET;
