@@ -18,6 +18,9 @@
 #ifndef LLM_PROJ_WPB
 #define LLM_PROJ_WPB 4      // wavefronts per 4-row block (VALU kernel)
 #endif
+#ifndef LLM_P12_WPB
+#define LLM_P12_WPB 8       // the same, 12-bit kernel, one matrix (decode QKV: 748 vs 746 tok/s at 4)
+#endif
 #ifndef LLM_PROJ_WPB_SILU
 #define LLM_PROJ_WPB_SILU 8 // the same for gate|up (twice the loads per step)
 #endif
@@ -1115,10 +1118,10 @@ static hipError_t launch_proj_rt(const ProjArgs& a, int L, uint32_t blocks,
 }
 
 // The p12 kernel (one or two rows): gate|up with 8 wavefronts per block,
-// long reductions (the down projection) with 16 and the others with 4, as
-// the 16-bit kernel, and 16 wherever fewer would take more than 8 k-steps
-// each; every wavefront's steps loaded at once (proj_uses_p12 bounds the
-// steps by 16 x 8).
+// long reductions (the down projection) with 16 and the others (Q|K|V, O)
+// with LLM_P12_WPB = 8 (4 in the 16-bit kernel), and 16 wherever fewer
+// would take more than 8 k-steps each; every wavefront's steps loaded at
+// once (proj_uses_p12 bounds the steps by 16 x 8).
 template <int RT, int EPI, int W, bool CORR>
 static void launch_p12_c(const ProjArgs& a, uint32_t blocks, hipStream_t st) {
     const uint32_t spw = (a.steps + W - 1) / W;
@@ -1143,9 +1146,9 @@ static hipError_t launch_p12_rt(const ProjArgs& a, uint32_t blocks, hipStream_t 
         if (a.steps > 8 * LLM_PROJ_WPB_SILU) return launch_p12_w<RT, EPI, 16>(a, blocks, st);
         return launch_p12_w<RT, EPI, LLM_PROJ_WPB_SILU>(a, blocks, st);
     } else {
-        if (a.steps >= LLM_PROJ_LONG_STEPS || a.steps > 8 * LLM_PROJ_WPB)
+        if (a.steps >= LLM_PROJ_LONG_STEPS || a.steps > 8 * LLM_P12_WPB)
             return launch_p12_w<RT, EPI, 16>(a, blocks, st);
-        return launch_p12_w<RT, EPI, LLM_PROJ_WPB>(a, blocks, st);
+        return launch_p12_w<RT, EPI, LLM_P12_WPB>(a, blocks, st);
     }
 }
 
