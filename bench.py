@@ -334,7 +334,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build targets one GPU; --gpus {args.gpus} is "
-              "not supported (the sharded design is described in DESIGN.md)",
+              "not supported (no collectives or sharded launches are built)",
               file=sys.stderr)
         sys.exit(2)
     import llm_accel
