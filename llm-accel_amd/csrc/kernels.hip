@@ -964,7 +964,12 @@ __global__ __launch_bounds__(64 * KS) void proj_mfma12_kernel(ProjArgs a, uint32
 // goes into one 64-bit atomicMax per row.  The key orders by score, then
 // by smaller v, so equal scores resolve to the first index.
 // ---------------------------------------------------------------------
-template <int RT, int L>
+// XS: the activation rows are staged in LDS once per workgroup (1-2 rows,
+// at most kLmStageSteps k-steps) and every step reads them from there, so
+// that the loads in the loop are the table's only (the four lanes of a
+// column group read the same 16 bytes: an LDS broadcast).
+constexpr uint32_t kLmStageSteps = 32;
+template <int RT, int L, bool XS = false>
 __global__ __launch_bounds__(256) void lm_argmax_kernel(const int16_t* __restrict__ w,
                                                         uint32_t S, uint32_t n,
                                                         const int16_t* __restrict__ x,
@@ -977,6 +982,17 @@ __global__ __launch_bounds__(256) void lm_argmax_kernel(const int16_t* __restric
     unsigned long long best[RT];
 #pragma unroll
     for (int r = 0; r < RT; r++) best[r] = 0;
+    static_assert(!XS || RT <= 2, "staged rows: 1-2");
+    __shared__ __attribute__((aligned(16))) int16_t xs[XS ? RT : 1][XS ? kLmStageSteps * 128 : 8];
+    if constexpr (XS) {
+        // rows beyond `rows` stage row 0 (in bounds; ignored); S <= kLmStageSteps
+        for (uint32_t e = threadIdx.x; e < S * 16; e += 256)
+#pragma unroll
+            for (int r = 0; r < RT; r++)
+                *(uint4*)&xs[r][8 * e] =
+                    *(const uint4*)(x + (size_t)(r < (int)rows ? r : 0) * ldx + 8 * e);
+        __syncthreads();
+    }
     for (uint32_t b = blockIdx.x * 4 + wave; b < nblocks; b += stride) {
         const int16_t* wp = w + ((size_t)b * S * 4 + i) * 128 + j * 8;
         const int16_t* xp = x + j * 8;
@@ -992,8 +1008,9 @@ __global__ __launch_bounds__(256) void lm_argmax_kernel(const int16_t* __restric
 #pragma unroll
                 for (int r = 0; r < RT; r++) {
                     // rows beyond `rows` read row 0 (in bounds; ignored)
-                    const uint4 xv = *(const uint4*)(xp + (size_t)(r < (int)rows ? r : 0) * ldx +
-                                                     s * 128);
+                    const uint4 xv = XS ? *(const uint4*)&xs[XS ? r : 0][s * 128 + j * 8]
+                                        : *(const uint4*)(xp + (size_t)(r < (int)rows ? r : 0) * ldx +
+                                                          s * 128);
                     if (L == 0) {
                         acc[r] += dot2_wide(wv.x, xv.x) + dot2_wide(wv.y, xv.y) +
                                   dot2_wide(wv.z, xv.z) + dot2_wide(wv.w, xv.w);
@@ -1042,6 +1059,17 @@ static hipError_t launch_lm_rt(const int16_t* w, uint32_t steps, uint32_t n,
     const uint32_t nblocks = (n + 3) / 4;
     uint32_t grid = (nblocks + 3) / 4;
     if (grid > 2048) grid = 2048;
+    if (RT <= 2 && steps <= kLmStageSteps) {
+        constexpr bool XS = RT <= 2;
+        switch (L) {
+        case 0: lm_argmax_kernel<RT, 0, XS><<<grid, 256, 0, st>>>(w, steps, n, x, ldx, rows, keys); break;
+        case 1: lm_argmax_kernel<RT, 1, XS><<<grid, 256, 0, st>>>(w, steps, n, x, ldx, rows, keys); break;
+        case 4: lm_argmax_kernel<RT, 4, XS><<<grid, 256, 0, st>>>(w, steps, n, x, ldx, rows, keys); break;
+        case 8: lm_argmax_kernel<RT, 8, XS><<<grid, 256, 0, st>>>(w, steps, n, x, ldx, rows, keys); break;
+        default: lm_argmax_kernel<RT, 16, XS><<<grid, 256, 0, st>>>(w, steps, n, x, ldx, rows, keys); break;
+        }
+        return hipGetLastError();
+    }
     switch (L) {
     case 0: lm_argmax_kernel<RT, 0><<<grid, 256, 0, st>>>(w, steps, n, x, ldx, rows, keys); break;
     case 1: lm_argmax_kernel<RT, 1><<<grid, 256, 0, st>>>(w, steps, n, x, ldx, rows, keys); break;
